@@ -1,0 +1,63 @@
+"""ctypes binding of the C ABI declared in include/tokengate_hip.h.
+
+The library is loaded from the fa2bias SITE directory (FA2BIAS_SITE overrides).  Every call
+raises RuntimeError with the library's own message when the entry point returns nonzero.
+Nothing here falls back to another implementation: a missing library is an error.
+"""
+import ctypes as C
+import os
+import threading
+
+from tokengate_amd.fa2bias.site_path import LIB_NAME, SITE
+
+_lock = threading.Lock()
+_lib = None
+
+vp, i32, i64, f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_float
+
+# name -> argtypes, in header order.  Keep in step with include/tokengate_hip.h.
+SIGNATURES = {
+    "tg_abi_version": [],
+    "tg_last_error": [],
+    "tg_keybias_fwd": [vp, vp, vp, vp, vp, vp,
+                       i32, i32, i32, i32, i32, i32,
+                       i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                       i64, i64, f32, i32, vp],
+    "tg_keybias_varlen_fwd": [vp, vp, vp, vp, vp, vp, vp,
+                              i32, i32, i32, i32, i32, i32,
+                              i64, i64, i64, i64, i64, i64, i64, i64,
+                              i64, i64, f32, i32, vp],
+}
+RESTYPES = {"tg_last_error": C.c_char_p}
+
+
+def lib_path(site: str = None) -> str:
+    return os.path.join(site or SITE, LIB_NAME)
+
+
+def load(site: str = None):
+    """Load (once) and return the ctypes library with argtypes set."""
+    global _lib
+    with _lock:
+        if _lib is not None and site is None:
+            return _lib
+        path = lib_path(site)
+        if not os.path.exists(path):
+            raise RuntimeError(f"{LIB_NAME} is not built ({path}): build it with "
+                               f"`python -m tokengate_amd.build`")
+        lib = C.CDLL(path)
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = RESTYPES.get(name, C.c_int)
+        if site is None:
+            _lib = lib
+        return lib
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.tg_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name}: {msg}")

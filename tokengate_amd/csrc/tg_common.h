@@ -1,0 +1,82 @@
+// Shared device helpers for the gfx950 kernels: vector types, MFMA wrappers, LDS access,
+// cross-lane reductions, and the thread-local error string behind tg_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+namespace tg {
+
+typedef uint16_t bf16_t;  // raw bf16 bits in global memory
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- host-side error reporting -------------------------------------------------------------
+int set_error(const char *fmt, ...);   // formats into the thread-local buffer, returns 1
+void clear_error();
+const char *last_error();
+
+#define TG_CHECK(cond, ...)                 \
+  do {                                      \
+    if (!(cond)) return ::tg::set_error(__VA_ARGS__); \
+  } while (0)
+
+#define TG_HIP_CHECK(expr)                                                              \
+  do {                                                                                  \
+    hipError_t _e = (expr);                                                             \
+    if (_e != hipSuccess)                                                               \
+      return ::tg::set_error("%s failed: %s", #expr, hipGetErrorString(_e));            \
+  } while (0)
+
+// ---- device helpers -----------------------------------------------------------------------
+
+// C = A(32x16) * B(16x32) + C on the bf16 matrix cores.  Lane l holds A[l%32][8*(l/32)+j] and
+// B[8*(l/32)+j][l%32] for j=0..7; C value v sits at row 8*(v/4)+4*(l/32)+(v%4), column l%32.
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte LDS load / store at a byte offset into a __shared__ buffer.
+__device__ __forceinline__ bf16x8 lds_load16(const char *base, uint32_t byte_off) {
+  return *reinterpret_cast<const bf16x8 *>(base + byte_off);
+}
+__device__ __forceinline__ void lds_store16(char *base, uint32_t byte_off, u32x4 v) {
+  *reinterpret_cast<u32x4 *>(base + byte_off) = v;
+}
+__device__ __forceinline__ void lds_store8(char *base, uint32_t byte_off, u32x2 v) {
+  *reinterpret_cast<u32x2 *>(base + byte_off) = v;
+}
+
+// 16-byte global load with a validity predicate (zero when invalid, no access made).
+__device__ __forceinline__ u32x4 gload16(const bf16_t *p, bool valid) {
+  u32x4 r = {0u, 0u, 0u, 0u};
+  if (valid) r = *reinterpret_cast<const u32x4 *>(p);
+  return r;
+}
+
+// Combine a value held by lane l and lane l^32 (the two halves of a wave64).
+__device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+__device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Two floats -> packed bf16 pair (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  bf16x2 p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t x) {
+  return __builtin_bit_cast(float, (uint32_t)x << 16);
+}
+
+}  // namespace tg
