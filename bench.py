@@ -1,0 +1,178 @@
+"""Benchmark: key-bias causal attention forward at 32k context on one MI355X.
+
+One step = one launch of the key-bias attention forward (the drop-in op
+recursive_kvs::fa2_keybias_fwd) over the 32k workload: B=1, S=32768, 16 query heads, 8 KV heads,
+head_dim 128, bf16, causal; Q/K/V ~ N(0,1)/sqrt(128); per-key bias log(sigmoid(z)), z ~ N(0,3),
+forced to 0 on positions [0,64) and [32512,32768), broadcast over heads.  Inputs are generated
+on the device before timing (synthetic data).
+
+Prints ONE JSON line with the bench contract fields plus:
+  roofline     — the attention kernel's algorithmic TFLOP/s (2*B*H*D*S*(S+1) per launch over
+                 the mean launch time from HIP events on the launch stream) against the bf16
+                 dense MFMA peak; traffic = HBM bytes per launch from the committed rocprofv3
+                 counter summary when present;
+  cpu_baseline — the oracle (float32 numpy, all host cores through BLAS) on a bounded sample of
+                 the same workload: the last query rows of every head, full causal key range;
+  extra        — secondary measurements (the 4k shape).
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA peak
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+
+def causal_flops(b, h, s, d=128):
+    return 2.0 * b * h * d * s * (s + 1)
+
+
+def make_inputs(S, H, Hkv, sigma, seed, device, prefix=64, suffix=256, qkv_scale=None):
+    import torch
+    D = 128
+    g = torch.Generator(device=device).manual_seed(seed)
+    sc = qkv_scale if qkv_scale is not None else 1.0
+    q = (torch.randn(1, S, H, D, generator=g, device=device) * sc).to(torch.bfloat16)
+    k = (torch.randn(1, S, Hkv, D, generator=g, device=device) * sc).to(torch.bfloat16)
+    v = (torch.randn(1, S, Hkv, D, generator=g, device=device) * sc).to(torch.bfloat16)
+    z = torch.randn(1, S, generator=g, device=device) * sigma
+    kb = torch.nn.functional.logsigmoid(z)
+    if prefix:
+        kb[:, :prefix] = 0.0
+    if suffix:
+        kb[:, S - suffix:] = 0.0
+    scale = D ** -0.5
+    bias_raw = (kb[:, None, :].expand(1, H, S).float() / scale).contiguous()
+    return q, k, v, bias_raw, scale
+
+
+def time_fwd(q, k, v, bias_raw, scale, steps, warmup):
+    """Returns (ms_per_step from the bracketing host clock, mean kernel ms from HIP events)."""
+    import torch
+    op = torch.ops.recursive_kvs.fa2_keybias_fwd
+    for _ in range(warmup):
+        op(q, k, v, bias_raw, scale, True)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        op(q, k, v, bias_raw, scale, True)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
+    return (t1 - t0) * 1e3 / steps, kern_ms
+
+
+def cpu_baseline(q, k, v, bias_raw, scale, seconds):
+    """Time the float32 oracle on the last query rows of the 32k workload (all heads) for about
+    `seconds` of CPU work; returns TFLOP/s of that sample and a description."""
+    import numpy as np
+    from oracle import attention as ora
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
+    except Exception:
+        threads = len(os.sched_getaffinity(0))
+    qn = q.float().cpu().numpy()
+    kn = k.float().cpu().numpy()
+    vn = v.float().cpu().numpy()
+    bn = bias_raw.cpu().numpy()
+    S, H = qn.shape[1], qn.shape[2]
+    chunk = 32
+    done_rows, flops = 0, 0.0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds and done_rows < S:
+        hi = S - done_rows
+        rows = np.arange(max(0, hi - chunk), hi)
+        ora.keybias_fwd(qn, kn, vn, bn, scale, True, rows=rows, dtype=np.float32)
+        flops += H * float(np.sum(4.0 * 128 * (rows + 1)))
+        done_rows += len(rows)
+    dt = time.perf_counter() - t0
+    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"oracle float32 numpy fwd, last {done_rows} query rows x {H} heads of the 32k causal "
+                      f"workload (full key range each), {flops:.3e} FLOP in {dt:.1f} s"}
+
+
+def traffic_from_profile():
+    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "keybias_fwd_32k_counters.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: every GPU box here has one, and this path is timed on one "
+              "GPU's share (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from tokengate_amd.fa2bias import keybias  # noqa: F401  (registers the custom ops)
+    dev = torch.device("cuda:0")
+
+    S, H, Hkv = 32768, 16, 8
+    q, k, v, bias_raw, scale = make_inputs(S, H, Hkv, 3.0, 2, dev, qkv_scale=1.0 / math.sqrt(128))
+    flops = causal_flops(1, H, S)
+    ms_step, kern_ms = time_fwd(q, k, v, bias_raw, scale, args.steps, args.warmup)
+    value = flops / (ms_step * 1e-3) / 1e12
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+
+    extra = {"kernel_ms_32k": round(kern_ms, 4)}
+    if not args.no_extra:
+        q1, k1, v1, b1, s1 = make_inputs(4096, H, Hkv, 2.0, 0, dev, prefix=0, suffix=0)
+        _, k1ms = time_fwd(q1, k1, v1, b1, s1, 20, 5)
+        extra["fwd_4k_tflops"] = round(causal_flops(1, H, 4096) / (k1ms * 1e-3) / 1e12, 2)
+        extra["fwd_4k_kernel_ms"] = round(k1ms, 4)
+
+    cpu = cpu_baseline(q, k, v, bias_raw, scale, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    line = {
+        "metric": "key-bias attn TFLOP/s at 32k bf16 (% MFMA peak); pruned-prefill TTFT ms",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "key-bias attention forward, causal GQA, 32k context",
+                   "batch": 1, "seq_len": S, "heads": H, "kv_heads": Hkv, "head_dim": 128,
+                   "bias": "log(sigmoid(z)), z~N(0,3), 0 on [0,64) and [32512,32768), broadcast over heads",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_from_profile()},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

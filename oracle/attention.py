@@ -39,28 +39,29 @@ def _logits(qb, kg, bias_row, scale, causal, q_rows, sq, sk):
     return z
 
 
-def keybias_fwd(q, k, v, bias_raw, scale, causal=True, rows=None):
+def keybias_fwd(q, k, v, bias_raw, scale, causal=True, rows=None, dtype=np.float64):
     """Forward.  q (B,Sq,H,D), k/v (B,Sk,Hkv,D), bias_raw (B,H,Sk) or None.
 
     rows: optional index array of query rows to evaluate (all by default).
-    Returns out (B,len(rows),H,D) float64 and lse (B,H,len(rows)) float64."""
+    dtype: evaluation precision (float64 for checking; float32 for the timed CPU baseline).
+    Returns out (B,len(rows),H,D) and lse (B,H,len(rows)) in that precision."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     G = H // Hkv
     rows = np.arange(Sq) if rows is None else np.asarray(rows)
-    out = np.zeros((B, len(rows), H, D))
-    lse = np.full((B, H, len(rows)), np.inf)
+    out = np.zeros((B, len(rows), H, D), dtype=dtype)
+    lse = np.full((B, H, len(rows)), np.inf, dtype=dtype)
     for b in range(B):
         for h in range(H):
             g = h // G
-            z = _logits(q[b, :, h].astype(np.float64), k[b, :, g].astype(np.float64),
-                        None if bias_raw is None else bias_raw[b, h].astype(np.float64),
-                        scale, causal, rows, Sq, Sk)
+            z = _logits(q[b, :, h].astype(dtype), k[b, :, g].astype(dtype),
+                        None if bias_raw is None else bias_raw[b, h].astype(dtype),
+                        dtype(scale), causal, rows, Sq, Sk)
             m = z.max(axis=1, initial=-np.inf)
             ok = np.isfinite(m)
             p = np.exp(z - np.where(ok, m, 0.0)[:, None])
             l = p.sum(axis=1)
-            o = (p @ v[b, :, g].astype(np.float64)) / np.where(l > 0, l, 1.0)[:, None]
+            o = (p @ v[b, :, g].astype(dtype)) / np.where(l > 0, l, 1.0)[:, None]
             out[b, :, h] = np.where(ok[:, None], o, 0.0)
             lse[b, h] = np.where(ok, m + np.log(np.where(l > 0, l, 1.0)), np.inf)
     return out, lse
