@@ -5,20 +5,23 @@
 //   lse[i]  = ln sum_j exp(z[i,j]);   out_i = sum_j exp(z[i,j] - lse[i]) v_j
 // with the query head h reading kv head h / (H / Hkv).
 //
-// Work decomposition (one workgroup = 4 waves = 256 threads):
-//   * a workgroup owns 128 consecutive query positions of one KV head and HP query heads of its
-//     GQA group (HP = 2 when the group size is even): every K/V fragment a wave reads from LDS
-//     feeds HP matrix-core products;
-//   * each wave owns 32 query positions x HP heads; the KV sequence is streamed in 64-key tiles,
-//     double-buffered in LDS (K as rows, V transposed), one barrier per tile;
+// Work decomposition (one workgroup = 8 waves = 512 threads, two waves per SIMD):
+//   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
+//     size is even) over 8 * 32/HP consecutive query positions; every K/V tile it streams
+//     through LDS serves all HP heads;
+//   * each wave owns 32 MFMA columns = HP heads x 32/HP query positions; the KV sequence is
+//     streamed in 64-key tiles by LDS DMA (buffer_load ... lds: no staging registers, zero fill
+//     past Sk), double-buffered, one barrier per tile, the next tile in flight during compute;
 //   * scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_bf16: the accumulator
-//     then holds one query per lane (column l%32) and 16 keys per lane, so the online-softmax max
-//     and sum are in-lane plus one permlane32 swap;
+//     then holds one (head, query) column per lane and 16 keys per lane, so the online-softmax
+//     max and sum are in-lane plus one cross-half exchange;
 //   * K rows are stored in LDS in a permuted order (sigma) chosen so that lane group g of the
 //     S^T accumulator holds 16 CONSECUTIVE keys; the accumulator, rounded to bf16, is then directly
-//     the B operand of O^T = V^T P^T, whose A operand is 8 consecutive keys of V^T (16-byte LDS
-//     read);
-//   * O^T accumulates per lane for one query, so the per-query rescale is a scalar per lane.
+//     the B operand of O^T = V^T P^T, whose A operand (8 consecutive keys at one d per lane) comes
+//     from row-major V through the transposing LDS read ds_read_b64_tr_b16;
+//   * O^T accumulates per lane for one column, so the per-query rescale is a scalar per lane, and
+//     it is applied lazily (only when the running max grows by more than 2^8);
+//   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
@@ -30,17 +33,17 @@ namespace {
 
 constexpr int kD = 128;        // head dim
 constexpr int kBN = 64;        // keys per tile
-constexpr int kWQ = 32;        // query positions per wave
-constexpr int kWaves = 4;
-constexpr int kBM = kWQ * kWaves;   // query positions per workgroup
+constexpr int kWaves = 8;      // 2 waves per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// A wave's 32 MFMA columns are HP heads x (32/HP) query positions; a workgroup covers
+// kWaves * 32/HP positions.
+template <int HP> constexpr int qpw() { return 32 / HP; }
+template <int HP> constexpr int bm() { return kWaves * qpw<HP>(); }
 
-constexpr int kKRowBytes = kD * 2;      // one K row in LDS (256 B, 16 chunks of 16 B)
-constexpr int kVRowBytes = kBN * 2;     // one V^T row (one d) in LDS (128 B, 8 chunks)
+constexpr int kKRowBytes = kD * 2;      // one K or V row in LDS (256 B, 16 chunks of 16 B)
 constexpr int kKTileBytes = kBN * kKRowBytes;
-constexpr int kVTileBytes = kD * kVRowBytes;
 
 struct FwdArgs {
   const bf16_t *q, *k, *v;
@@ -58,27 +61,37 @@ struct FwdArgs {
   float scale_log2;            // softmax_scale * log2(e)
 };
 
-// Key j (0..31) of a 32-key block is stored at LDS row sigma_inv(j) so that MFMA row
-// m = 8a + 4g + b (a, b in 0..3) carries key 16g + 4a + b: lane group g of the S^T accumulator
-// then holds keys 16g .. 16g+15 of the block, in register order.
-__device__ __forceinline__ int sigma_inv(int j) {
-  return ((j & 15) >> 2) * 8 + (j >> 4) * 4 + (j & 3);
-}
-// XOR swizzle of the 16-byte chunks of a V^T row: conflict-free reads of 8 consecutive rows and
-// 4-cycle transposed writes.
-__device__ __forceinline__ uint32_t v_swz(int d) { return (uint32_t)((d + (d >> 3)) & 7); }
+// MFMA row m = 8a + 4g + b (a, b in 0..3) of a 32-key block carries key sigma(m) = 16g + 4a + b,
+// so that lane group g of the S^T accumulator holds keys 16g .. 16g+15 in register order.
+__device__ __forceinline__ int sigma(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
 
+// Lazy rescaling threshold (log2 units): the running max used for exp2 is raised only when a tile
+// exceeds it by more than this, so P <= 2^8 (exact in bf16's exponent range) and the O rescale
+// is skipped on almost every tile.
+constexpr float kRescaleTau = 8.0f;
+
+// LDS tile layouts (64 keys x 128 d, 256 B per row, 16-byte chunks):
+//   K: row lr holds key 32*(lr/32) + sigma(lr%32); logical chunk c at physical chunk c ^ (lr%16)
+//      -> the S^T A-operand read (32 consecutive rows, one chunk) is bank-conflict free.
+//   V: row = key (natural order); logical chunk c at physical chunk c ^ 4*(key%4)
+//      -> the transposing reads (4 keys x 64 B per 16-lane group) spread over all banks.
+// Both are filled by LDS DMA straight from global memory (no staging registers); keys past Sk
+// read as zero through the buffer descriptor's range check.
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
-__global__ __launch_bounds__(kThreads) void keybias_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) char ks[2][kKTileBytes];
-  __shared__ __attribute__((aligned(16))) char vs[2][kVTileBytes];
-  __shared__ __attribute__((aligned(16))) float bs[2][HP][kBN];
+__global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
+  constexpr int QW = qpw<HP>();
+  constexpr int BM = bm<HP>();
+  __shared__ __attribute__((aligned(1024))) char ks[2][kKTileBytes];
+  __shared__ __attribute__((aligned(1024))) char vs[2][kKTileBytes];
+  __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int lq = lane & 31;
+  const int lq = lane & 31;      // MFMA column: head lq / QW, query lq % QW
   const int g = lane >> 5;
+  const int hl = lq / QW;        // this lane's head within the workgroup's HP heads
+  const int ql = lq % QW;
 
   // ---- which (query tile, sequence, kv head, head pair) this workgroup owns ----
   const int hgroups = a.group / HP;
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(kThreads) void keybias_fwd_kernel(FwdArgs a) {
     sq = min(s1 - s0, a.sq);   // rows past max_seqlen are outside the bias row: not computed
     sk = sq;
   }
-  const int q0 = qt * kBM;
+  const int q0 = qt * BM;
   if (q0 >= sq) return;   // workgroup-uniform: past the end of this sequence
   const int off = sk - sq;
   const int h0 = kh * a.group + hg * HP;
@@ -108,231 +121,198 @@ __global__ __launch_bounds__(kThreads) void keybias_fwd_kernel(FwdArgs a) {
   const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
   const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
   bf16_t *obase = a.o + (VARLEN ? row0 * a.o_rs : (int64_t)b * a.o_bs) + (int64_t)h0 * a.o_hs;
-  const float *bbase = nullptr;
-  if constexpr (HAS_BIAS) bbase = a.bias + (int64_t)b * a.bias_bs + (int64_t)h0 * a.bias_hs;
+
+  // Buffer descriptors: exactly the bytes of rows [0, sk) of this (sequence, kv head).
+  const uint32_t kspan = sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.k_rs + kD) * 2) : 0u;
+  const uint32_t vspan = sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.v_rs + kD) * 2) : 0u;
+  const brsrc_t krs = make_rsrc(kbase, kspan);
+  const brsrc_t vrs = make_rsrc(vbase, vspan);
+  const float *bbase = HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)h0 * a.bias_hs : nullptr;
+  const brsrc_t brs =
+      make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
 
   // ---- this wave's queries and its Q fragments (B operand of S^T = K Q^T) ----
-  const int qw0 = q0 + wave * kWQ;
-  const int qrow = qw0 + lq;
+  const int qw0 = q0 + wave * QW;
+  const int qrow = qw0 + ql;
   const bool qvalid = qrow < sq;
   const bool wave_has_rows = qw0 < sq;
-  const int qw_hi = min(qw0 + kWQ, sq) - 1;
-  bf16x8 qf[HP][8];
+  const int qw_hi = min(qw0 + QW, sq) - 1;
+  bf16x8 qf[8];
 #pragma unroll
-  for (int h = 0; h < HP; ++h)
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-      qf[h][s] = __builtin_bit_cast(
-          bf16x8, gload16(qbase + (int64_t)qrow * a.q_rs + (int64_t)h * a.q_hs + 16 * s + 8 * g, qvalid));
+  for (int s = 0; s < 8; ++s)
+    qf[s] = __builtin_bit_cast(
+        bf16x8, gload16(qbase + (int64_t)qrow * a.q_rs + (int64_t)hl * a.q_hs + 16 * s + 8 * g, qvalid));
 
   int kv_end = sk;
-  if constexpr (CAUSAL) kv_end = min(sk, q0 + kBM + off);
+  if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
   const int n_tiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
 
-  // ---- global -> register -> LDS staging of one KV tile ----
-  u32x4 kreg[4], vreg[4];
-  float breg[HP];
-  const int ld_c = tid & 15;     // 16-byte chunk along d
-  const int ld_r = tid >> 4;     // 0..15
-  auto gload_tile = [&](int n0) {
+  // ---- per-lane DMA source offsets (bytes within a tile; + tile * 64 rows per tile) ----
+  // 16 KB per tile = 16 wave-loads of 1 KB: wave w issues loads 2w and 2w+1 of K and of V.
+  uint32_t koff[2], voff[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = n0 + ld_r + 16 * i;
-      kreg[i] = gload16(kbase + (int64_t)key * a.k_rs + 8 * ld_c, key < sk);
-    }
+  for (int it = 0; it < 2; ++it) {
+    const int lr = (wave * 2 + it) * 4 + (lane >> 4);     // K LDS row written by this lane
+    const int kc = (lane & 15) ^ (lr & 15);               // logical chunk stored there
+    const int kkey = 32 * (lr >> 5) + sigma(lr & 31);
+    koff[it] = (uint32_t)(kkey * a.k_rs * 2 + kc * 16);
+    const int vkey = (wave * 2 + it) * 4 + (lane >> 4);   // V LDS row (= key) written by this lane
+    const int vc = (lane & 15) ^ (4 * (vkey & 3));
+    voff[it] = (uint32_t)(vkey * a.v_rs * 2 + vc * 16);
+  }
+  auto issue_tile = [&](int tile, int buf) {
+    const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
+    const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = n0 + 4 * ld_r + i;
-      vreg[i] = gload16(vbase + (int64_t)key * a.v_rs + 8 * ld_c, key < sk);
-    }
-    if constexpr (HAS_BIAS) {
-      if (tid < kBN) {
-        const int key = n0 + tid;
-#pragma unroll
-        for (int h = 0; h < HP; ++h)
-          breg[h] = key < sk ? bbase[(int64_t)h * a.bias_hs + key] * a.scale_log2 : 0.f;
-      }
-    }
-  };
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = ld_r + 16 * i;
-      const int lr = (r & 32) + sigma_inv(r & 31);
-      lds_store16(ks[buf], lr * kKRowBytes + ((ld_c ^ (lr & 15)) << 4), kreg[i]);
-    }
-    // V: thread holds keys 4*ld_r .. +3 at d = 8*ld_c .. +7; write V^T rows d, 4 keys (8 B) each.
-    const int kq = ld_r;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t w0 = vreg[0][p], w1 = vreg[1][p], w2 = vreg[2][p], w3 = vreg[3][p];
-      const u32x2 lo = {(w0 & 0xffffu) | (w1 << 16), (w2 & 0xffffu) | (w3 << 16)};
-      const u32x2 hi = {(w0 >> 16) | (w1 & 0xffff0000u), (w2 >> 16) | (w3 & 0xffff0000u)};
-      const int d0 = 8 * ld_c + 2 * p;
-      const int d1 = d0 + 1;
-      lds_store8(vs[buf], d0 * kVRowBytes + (((uint32_t)(kq >> 1) ^ v_swz(d0)) << 4) + (kq & 1) * 8, lo);
-      lds_store8(vs[buf], d1 * kVRowBytes + (((uint32_t)(kq >> 1) ^ v_swz(d1)) << 4) + (kq & 1) * 8, hi);
+    for (int it = 0; it < 2; ++it) {
+      dma16(krs, ks[buf] + (wave * 2 + it) * 1024, kb0 + koff[it]);
+      dma16(vrs, vs[buf] + (wave * 2 + it) * 1024, vb0 + voff[it]);
     }
     if constexpr (HAS_BIAS) {
-      if (tid < kBN) {
-#pragma unroll
-        for (int h = 0; h < HP; ++h) bs[buf][h][tid] = breg[h];
-      }
+      if (wave < HP) dma4(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
     }
   };
 
-  f32x16 oacc[HP][4];
-  float mrun[HP], lrun[HP];
-#pragma unroll
-  for (int h = 0; h < HP; ++h) {
-    mrun[h] = -INFINITY;
-    lrun[h] = 0.f;
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) oacc[h][d][v] = 0.f;
-  }
+  // V transposed-read addressing: lane l of 16-lane group G reads key K0 + (l%16)/4, 4 d-values
+  // starting at 32*dblk + 16*(G%2) + 4*(l%4).
+  const int r16 = lane & 15;
+  const uint32_t v_rowpart = (uint32_t)((r16 >> 2) * kKRowBytes + (r16 & 1) * 8);
+  const int v_cpart = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
+  const int v_swz = r16 >> 2;
 
-  if (n_tiles > 0) {
-    gload_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
+  f32x16 oacc[4];
+  float mrun = -INFINITY, lrun = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) oacc[d][v] = 0.f;
+
+  if (n_tiles > 0) issue_tile(0, 0);
 
   for (int t = 0; t < n_tiles; ++t) {
     const int buf = t & 1;
     const int n0 = t * kBN;
-    if (t + 1 < n_tiles) gload_tile(n0 + kBN);
+    wait_all_mem();
+    __syncthreads();                       // tile t resident; buffer buf^1 free
+    if (t + 1 < n_tiles) issue_tile(t + 1, buf ^ 1);
+    if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
 
-    const bool active = wave_has_rows && !(CAUSAL && n0 > qw_hi + off);
-    if (active) {
-      const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
-      // ---- S^T = K Q^T ----
-      f32x16 sacc[HP][2];
+    // ---- S^T = K Q^T: 2 key blocks x 8 d-steps ----
+    f32x16 sacc[2];
 #pragma unroll
-      for (int h = 0; h < HP; ++h)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) sacc[h][kb][v] = 0.f;
+    for (int s = 0; s < 8; ++s) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int lr = 32 * kb + lq;
-          const bf16x8 kf = lds_load16(ks[buf], lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
-#pragma unroll
-          for (int h = 0; h < HP; ++h) sacc[h][kb] = mfma32(kf, qf[h][s], sacc[h][kb]);
-        }
-      }
-      // ---- online softmax (one query per lane; 32 keys per lane per head) ----
-      uint32_t pk[HP][2][8];
-#pragma unroll
-      for (int h = 0; h < HP; ++h) {
-        float tv[2][16];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          if constexpr (HAS_BIAS) {
-            const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][h][32 * kb + 16 * g]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const f32x4 bb = bp[i];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) tv[kb][4 * i + e] = fmaf(sacc[h][kb][4 * i + e], a.scale_log2, bb[e]);
-            }
-          } else {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) tv[kb][v] = sacc[h][kb][v] * a.scale_log2;
-          }
-          if (need_mask) {
-            const int kbase_idx = n0 + 32 * kb + 16 * g;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int key = kbase_idx + v;
-              bool masked = key >= sk;
-              if constexpr (CAUSAL) masked = masked || (key > qrow + off);
-              tv[kb][v] = masked ? -INFINITY : tv[kb][v];
-            }
-          }
-        }
-        float mx = tv[0][0];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, tv[kb][v]);
-        mx = pair_max(mx);
-        const float m_new = fmaxf(mrun[h], mx);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = fast_exp2(mrun[h] - m_use);
-        mrun[h] = m_new;
-        lrun[h] *= alpha;
-#pragma unroll
-        for (int d = 0; d < 4; ++d) oacc[h][d] *= alpha;
-        float psum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int v = 0; v < 16; v += 2) {
-            const float p0 = fast_exp2(tv[kb][v] - m_use);
-            const float p1 = fast_exp2(tv[kb][v + 1] - m_use);
-            psum += p0 + p1;
-            pk[h][kb][v >> 1] = pack_bf16x2(p0, p1);
-          }
-        }
-        lrun[h] += psum;
-      }
-      // ---- O^T += V^T P^T ----
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-          bf16x8 pb[HP];
-#pragma unroll
-          for (int h = 0; h < HP; ++h) {
-            const u32x4 w = {pk[h][kb][4 * s], pk[h][kb][4 * s + 1], pk[h][kb][4 * s + 2], pk[h][kb][4 * s + 3]};
-            pb[h] = __builtin_bit_cast(bf16x8, w);
-          }
-          const uint32_t kc = 4 * kb + 2 * g + s;
-#pragma unroll
-          for (int dblk = 0; dblk < 4; ++dblk) {
-            const int d = 32 * dblk + lq;
-            const bf16x8 vf = lds_load16(vs[buf], d * kVRowBytes + ((kc ^ v_swz(d)) << 4));
-#pragma unroll
-            for (int h = 0; h < HP; ++h) oacc[h][dblk] = mfma32(vf, pb[h], oacc[h][dblk]);
-          }
-        }
+        const int lr = 32 * kb + lq;
+        const bf16x8 kf = lds_load16(ks[buf], lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
+        sacc[kb] = mfma32(kf, qf[s], sacc[kb]);
       }
     }
 
-    if (t + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
+    // ---- online softmax: one (head, query) column per lane, 32 keys per lane ----
+    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
+    float tv[2][16];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      if constexpr (HAS_BIAS) {
+        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 bb = bp[i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tv[kb][4 * i + e] = sacc[kb][4 * i + e] + bb[e];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) tv[kb][v] = sacc[kb][v];
+      }
+      if (need_mask) {
+        const int kidx = n0 + 32 * kb + 16 * g;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = kidx + v;
+          bool masked = key >= sk;
+          if constexpr (CAUSAL) masked = masked || (key > qrow + off);
+          tv[kb][v] = masked ? -INFINITY : tv[kb][v];
+        }
+      }
+    }
+    float mx = tv[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, tv[kb][v]);
+    mx = pair_max(mx) * a.scale_log2;     // tile max in log2 units (-inf if fully masked)
+    if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleTau) != 0) {
+      const float m_new = fmaxf(mrun, mx);
+      // 0 on the first visible tile; rows that have seen no key yet (m_new = -inf) keep 1.
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(mrun - m_new);
+      mrun = m_new;
+      lrun *= alpha;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) oacc[d] *= alpha;
+    }
+    const float mneg = mrun == -INFINITY ? 0.f : -mrun;
+    uint32_t pk[2][8];
+    float psum = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        const float p0 = fast_exp2(fmaf(tv[kb][v], a.scale_log2, mneg));
+        const float p1 = fast_exp2(fmaf(tv[kb][v + 1], a.scale_log2, mneg));
+        psum += p0 + p1;
+        pk[kb][v >> 1] = pack_bf16x2(p0, p1);
+      }
+    }
+    lrun += psum;
+
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 w = {pk[kb][4 * s], pk[kb][4 * s + 1], pk[kb][4 * s + 2], pk[kb][4 * s + 3]};
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, w);
+        const uint32_t krow = (uint32_t)((32 * kb + 16 * g + 8 * s) * kKRowBytes) + v_rowpart;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk) {
+          const uint32_t ch = (uint32_t)((4 * (dblk ^ v_swz) + v_cpart) << 4);
+          const s16x4 lo = lds_read_tr16(vs[buf] + krow + ch);
+          const s16x4 hi = lds_read_tr16(vs[buf] + krow + 4 * kKRowBytes + ch);
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          oacc[dblk] = mfma32(vf, pb, oacc[dblk]);
+        }
+      }
+    }
   }
 
   // ---- epilogue: normalise, write O (bf16) and LSE (natural log) ----
+  const float l = pair_sum(lrun);
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (qvalid) {
+    bf16_t *orow = obase + (int64_t)qrow * a.o_rs + (int64_t)hl * a.o_hs;
 #pragma unroll
-  for (int h = 0; h < HP; ++h) {
-    const float l = pair_sum(lrun[h]);
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    if (qvalid) {
-      bf16_t *orow = obase + (int64_t)qrow * a.o_rs + (int64_t)h * a.o_hs;
+    for (int dblk = 0; dblk < 4; ++dblk) {
 #pragma unroll
-      for (int dblk = 0; dblk < 4; ++dblk) {
-#pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          const int d = 32 * dblk + 8 * a4 + 4 * g;
-          const u32x2 w = {pack_bf16x2(oacc[h][dblk][4 * a4] * inv, oacc[h][dblk][4 * a4 + 1] * inv),
-                           pack_bf16x2(oacc[h][dblk][4 * a4 + 2] * inv, oacc[h][dblk][4 * a4 + 3] * inv)};
-          *reinterpret_cast<u32x2 *>(orow + d) = w;
-        }
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d = 32 * dblk + 8 * a4 + 4 * g;
+        const u32x2 w = {pack_bf16x2(oacc[dblk][4 * a4] * inv, oacc[dblk][4 * a4 + 1] * inv),
+                         pack_bf16x2(oacc[dblk][4 * a4 + 2] * inv, oacc[dblk][4 * a4 + 3] * inv)};
+        *reinterpret_cast<u32x2 *>(orow + d) = w;
       }
-      if (g == 0) {
-        const float lse = l > 0.f ? (mrun[h] + __log2f(l)) * kLn2 : INFINITY;
-        const int hh = h0 + h;
-        if constexpr (VARLEN)
-          a.lse[(int64_t)hh * a.lse_total + row0 + qrow] = lse;
-        else
-          a.lse[((int64_t)b * a.h + hh) * sq + qrow] = lse;
-      }
+    }
+    if (g == 0) {
+      const float lse = l > 0.f ? (mrun + __log2f(l)) * kLn2 : INFINITY;
+      const int hh = h0 + hl;
+      if constexpr (VARLEN)
+        a.lse[(int64_t)hh * a.lse_total + row0 + qrow] = lse;
+      else
+        a.lse[((int64_t)b * a.h + hh) * sq + qrow] = lse;
     }
   }
 }
@@ -375,6 +355,9 @@ int check_common(const void *q, const void *k, const void *v, const void *out, c
   return 0;
 }
 
+// Buffer descriptors address at most 4 GiB: rows x row stride of bf16 (or fp32 bias) must fit.
+bool span_ok(int64_t rows, int64_t row_stride) { return (rows + 1) * row_stride * 2 < (1ll << 32) - 1024; }
+
 bool strides_ok(std::initializer_list<int64_t> s) {
   for (int64_t x : s)
     if (x % 8 != 0) return false;
@@ -402,7 +385,11 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
                        k_head_stride, v_batch_stride, v_row_stride, v_head_stride, o_batch_stride,
                        o_row_stride, o_head_stride}),
            "q/k/v/out strides must be multiples of 8 elements");
+  TG_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
   if (batch == 0 || seqlen_q == 0) return 0;
+  TG_CHECK(span_ok(seqlen_k, k_row_stride) && span_ok(seqlen_k, v_row_stride) &&
+               (bias_raw == nullptr || span_ok(seqlen_k + bias_head_stride, 2)),
+           "one (batch, kv head) slice of k/v/bias must span less than 4 GiB");
   FwdArgs a{};
   a.q = static_cast<const bf16_t *>(q);
   a.k = static_cast<const bf16_t *>(k);
@@ -417,9 +404,10 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
   a.bias_bs = bias_batch_stride; a.bias_hs = bias_head_stride;
   a.batch = batch; a.sq = seqlen_q; a.sk = seqlen_k;
   a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
-  a.n_qtiles = (seqlen_q + kBM - 1) / kBM;
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
+  const int block_m = hp == 2 ? bm<2>() : bm<1>();
+  a.n_qtiles = (seqlen_q + block_m - 1) / block_m;
   const int64_t nblocks = (int64_t)a.n_qtiles * batch * (num_heads / hp);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
   dispatch_fwd<false>(a, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
@@ -443,7 +431,11 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
   TG_CHECK(strides_ok({q_row_stride, q_head_stride, k_row_stride, k_head_stride, v_row_stride, v_head_stride,
                        o_row_stride, o_head_stride}),
            "q/k/v/out strides must be multiples of 8 elements");
+  TG_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
   if (num_seqs == 0 || max_seqlen == 0 || total == 0) return 0;
+  TG_CHECK(span_ok(total, k_row_stride) && span_ok(total, v_row_stride) &&
+               (bias_raw == nullptr || span_ok(max_seqlen + bias_head_stride, 2)),
+           "the packed k/v/bias must span less than 4 GiB");
   FwdArgs a{};
   a.q = static_cast<const bf16_t *>(q);
   a.k = static_cast<const bf16_t *>(k);
@@ -460,9 +452,10 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
   a.lse_total = total;
   a.batch = num_seqs; a.sq = max_seqlen; a.sk = max_seqlen;
   a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
-  a.n_qtiles = (max_seqlen + kBM - 1) / kBM;
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
+  const int block_m = hp == 2 ? bm<2>() : bm<1>();
+  a.n_qtiles = (max_seqlen + block_m - 1) / block_m;
   const int64_t nblocks = (int64_t)a.n_qtiles * num_seqs * (num_heads / hp);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
   dispatch_fwd<true>(a, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);

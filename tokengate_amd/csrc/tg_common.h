@@ -65,6 +65,33 @@ __device__ __forceinline__ u32x4 gload16(const bf16_t *p, bool valid) {
 __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
 __device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
 
+// ---- buffer resources and LDS DMA (gfx950) --------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t brsrc_t;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4_t;
+
+// Raw buffer descriptor over [base, base + num_bytes): loads past num_bytes return zero and
+// make no memory access.
+__device__ __forceinline__ brsrc_t make_rsrc(const void *base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)num_bytes, 0x00020000);
+}
+// Asynchronous 16-byte-per-lane copy global -> LDS: lane i's 16 bytes land at
+// lds_wave_base + 16*i.  Completion is tracked by vmcnt.
+__device__ __forceinline__ void dma16(brsrc_t rs, void *lds_wave_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)lds_wave_base, 16, voff, 0, 0, 0);
+}
+// Same, 4 bytes per lane (lds_wave_base + 4*i).
+__device__ __forceinline__ void dma4(brsrc_t rs, void *lds_wave_base, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)lds_wave_base, 4, voff, 0, 0, 0);
+}
+// Transposing LDS read (ds_read_b64_tr_b16): within each group of 16 lanes, lane j receives
+// element j%4 of the four 16-bit values addressed by lanes 4k + j/4, for k = 0..3.
+__device__ __forceinline__ s16x4 lds_read_tr16(const void *lds_addr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)lds_addr);
+}
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Two floats -> packed bf16 pair (round to nearest even, v_cvt_pk_bf16_f32).
