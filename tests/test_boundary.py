@@ -1,0 +1,115 @@
+"""The drop-in boundary on the CPU: availability, ABI stamp, exported symbols, argument errors and
+fake kernels — the behaviours the reference's kernels/fa2bias/keybias.py has without a GPU."""
+import ctypes
+import json
+import os
+import re
+import shutil
+import subprocess
+import sys
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_symbols():
+    syms = []
+    for name in os.listdir(os.path.join(ROOT, "include")):
+        if name.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", name)).read()
+            syms += re.findall(r"^\s*(?:int|const\s+char\s*\*|void)\s*(tg_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(syms))
+
+
+def test_library_exports_every_header_symbol():
+    from tokengate_amd import _lib
+    syms = _header_symbols()
+    assert "tg_keybias_fwd" in syms and "tg_abi_version" in syms
+    lib = ctypes.CDLL(_lib.lib_path())
+    for s in syms:
+        assert hasattr(lib, s), f"{s} declared in include/ but not exported"
+    assert set(syms) == set(_lib.SIGNATURES), "ctypes signature table out of step with the header"
+
+
+def test_abi_version_and_stamp():
+    from tokengate_amd import _lib
+    from tokengate_amd.fa2bias.site_path import ABI, BUILD_INFO, SITE
+    assert _lib.load().tg_abi_version() == ABI
+    assert json.load(open(os.path.join(SITE, BUILD_INFO)))["abi"] == ABI
+
+
+def _run_py(code, env_extra):
+    env = dict(os.environ, **env_extra)
+    env["PYTHONPATH"] = ROOT
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, env=env, cwd=ROOT, timeout=300)
+    return r
+
+
+def test_available_false_and_ext_raises_without_build(tmp_path):
+    code = ("from tokengate_amd.fa2bias import keybias as kb\n"
+            "assert not kb.available()\n"
+            "try:\n    kb.ext()\nexcept RuntimeError as e:\n    print('ERR', e)\n")
+    r = _run_py(code, {"FA2BIAS_SITE": str(tmp_path)})
+    assert r.returncode == 0, r.stderr
+    assert "ERR" in r.stdout and "tokengate_amd.build" in r.stdout
+
+
+def test_require_varlen_rejects_old_abi(tmp_path):
+    from tokengate_amd import _lib
+    shutil.copy(_lib.lib_path(), tmp_path / os.path.basename(_lib.lib_path()))
+    (tmp_path / "BUILD_INFO.json").write_text(json.dumps({"abi": 1}))
+    code = ("from tokengate_amd.fa2bias import keybias as kb\n"
+            "assert kb.available()\n"
+            "try:\n    kb.require_varlen()\nexcept RuntimeError as e:\n    print('ERR', e)\n")
+    r = _run_py(code, {"FA2BIAS_SITE": str(tmp_path)})
+    assert r.returncode == 0, r.stderr
+    assert "ERR" in r.stdout and "ABI 1" in r.stdout
+    (tmp_path / "BUILD_INFO.json").unlink()   # no stamp reads as ABI 1 too
+    r = _run_py(code, {"FA2BIAS_SITE": str(tmp_path)})
+    assert "ABI 1" in r.stdout
+
+
+def test_require_varlen_accepts_current_build():
+    from tokengate_amd.fa2bias import keybias
+    keybias.require_varlen()
+
+
+def test_c_abi_rejects_bad_head_dim_without_touching_the_gpu():
+    from tokengate_amd import _lib
+    lib = _lib.load()
+    rc = lib.tg_keybias_fwd(16, 16, 16, None, 16, 16, 1, 8, 8, 2, 1, 64,
+                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None)
+    assert rc != 0 and b"head_dim" in lib.tg_last_error()
+    rc = lib.tg_keybias_fwd(16, 16, 16, None, 16, 16, 1, 8, 8, 3, 2, 128,
+                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None)
+    assert rc != 0 and b"divide" in lib.tg_last_error()
+
+
+def test_python_checks_match_reference_messages():
+    from tokengate_amd.fa2bias.keybias import ext
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="CUDA device"):
+        ext().fwd(q, k, k, None, None, 0.0, 0.1, True, -1, -1, 0.0, False, None)
+    with pytest.raises(RuntimeError, match="fp16 and bf16"):
+        ext().fwd(q.float(), k.float(), k.float(), None, None, 0.0, 0.1, True, -1, -1, 0.0, False, None)
+
+
+def test_fake_kernels_give_reference_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    import tokengate_amd.fa2bias.keybias  # noqa: F401
+    with FakeTensorMode():
+        q = torch.empty(2, 100, 16, 128, dtype=torch.bfloat16)
+        k = torch.empty(2, 100, 8, 128, dtype=torch.bfloat16)
+        b = torch.empty(2, 16, 100)
+        out, lse = torch.ops.recursive_kvs.fa2_keybias_fwd(q, k, k, b, 0.1, True)
+        assert out.shape == q.shape and lse.shape == (2, 16, 100) and lse.dtype == torch.float32
+        dq, dk, dv, db = torch.ops.recursive_kvs.fa2_keybias_bwd(q, q, k, k, q, lse, b, 0.1, True)
+        assert dq.shape == q.shape and dk.shape == k.shape and db.shape == b.shape
+        qv = torch.empty(300, 16, 128, dtype=torch.bfloat16)
+        kv = torch.empty(300, 8, 128, dtype=torch.bfloat16)
+        cu = torch.empty(4, dtype=torch.int32)
+        ov, lv = torch.ops.recursive_kvs.fa2_keybias_varlen_fwd(qv, kv, kv, torch.empty(3, 16, 128), cu, 128, 0.1, True)
+        assert ov.shape == qv.shape and lv.shape == (16, 300)

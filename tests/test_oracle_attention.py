@@ -1,0 +1,166 @@
+"""Pins the attention oracle (CPU) against library routines and invariants.
+
+Each check is chosen so that a plausible mistake in the oracle fails it: a dropped or unscaled
+bias (SDPA with an additive float mask), a wrong GQA head mapping (SDPA enable_gqa / repeat),
+log2 instead of natural LSE (torch.logsumexp), top-left instead of bottom-right causal alignment
+(row-suffix invariant), a wrong dBias scale or sign (autograd through SDPA; finite differences).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as ora
+
+
+def _inputs(B, Sq, Sk, H, Hkv, D, seed, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Sq, H, D, generator=g).to(torch.bfloat16).double()
+    k = torch.randn(B, Sk, Hkv, D, generator=g).to(torch.bfloat16).double()
+    v = torch.randn(B, Sk, Hkv, D, generator=g).to(torch.bfloat16).double()
+    b = (torch.randn(B, H, Sk, generator=g) * 3.0).double() if bias else None
+    return q, k, v, b
+
+
+def _sdpa(q, k, v, bias_raw, scale, causal):
+    """torch SDPA (math path, float64) with the key bias as an additive float mask."""
+    B, Sq, H, D = q.shape
+    Sk, Hkv = k.shape[1], k.shape[2]
+    qt, kt, vt = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    mask = torch.zeros(B, H, Sq, Sk, dtype=q.dtype)
+    if bias_raw is not None:
+        mask = mask + scale * bias_raw[:, :, None, :]
+    if causal:
+        i = torch.arange(Sq)[:, None]
+        j = torch.arange(Sk)[None, :]
+        mask = mask.masked_fill(j > i + (Sk - Sq), float("-inf"))
+    out = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=mask, scale=scale, enable_gqa=(H != Hkv))
+    logits = (qt @ kt.repeat_interleave(H // Hkv, 1).transpose(-1, -2)) * scale + mask
+    return out.transpose(1, 2), torch.logsumexp(logits, dim=-1)
+
+
+@pytest.mark.parametrize("H,Hkv", [(4, 4), (4, 2), (6, 2), (8, 1)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_fwd_matches_sdpa(H, Hkv, causal, with_bias):
+    q, k, v, b = _inputs(2, 37, 37, H, Hkv, 16, seed=H * 10 + Hkv, bias=with_bias)
+    scale = 16 ** -0.5
+    out, lse = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), None if b is None else b.numpy(), scale, causal)
+    ro, rl = _sdpa(q, k, v, b, scale, causal)
+    np.testing.assert_allclose(out, ro.numpy(), rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(lse, rl.numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_bias_shift_invariance():
+    q, k, v, b = _inputs(1, 20, 20, 4, 2, 8, seed=3)
+    scale = 8 ** -0.5
+    o1, l1 = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    o2, l2 = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy() + 5.0, scale, True)
+    np.testing.assert_allclose(o1, o2, rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(l2, l1 + 5.0 * scale, rtol=1e-12, atol=1e-12)
+
+
+def test_pad_bias_removes_key():
+    """bias -1e9 (logit units) on key j is attention without key j (the reference's pad rule)."""
+    q, k, v, b = _inputs(1, 9, 12, 2, 1, 8, seed=4)
+    scale = 8 ** -0.5
+    bb = b.numpy().copy()
+    bb[:, :, 5] = -1e9 / scale
+    o1, _ = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), bb, scale, False)
+    keep = [j for j in range(12) if j != 5]
+    o2, _ = ora.keybias_fwd(q.numpy(), k.numpy()[:, keep], v.numpy()[:, keep], b.numpy()[:, :, keep], scale, False)
+    np.testing.assert_allclose(o1, o2, rtol=1e-12, atol=1e-12)
+
+
+def test_causal_alignment_is_bottom_right():
+    """Sq < Sk: the rows equal the last Sq rows of the square causal attention;
+    Sq > Sk: the first Sq-Sk rows see nothing (out 0, lse +inf), the rest equal the square case."""
+    q, k, v, b = _inputs(1, 30, 30, 4, 2, 8, seed=5)
+    scale = 8 ** -0.5
+    full_o, full_l = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    o, l = ora.keybias_fwd(q.numpy()[:, 18:], k.numpy(), v.numpy(), b.numpy(), scale, True)
+    np.testing.assert_allclose(o, full_o[:, 18:], rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(l, full_l[:, :, 18:], rtol=1e-12, atol=1e-12)
+    q2 = np.concatenate([np.random.default_rng(0).standard_normal((1, 7, 4, 8)), q.numpy()], axis=1)
+    o2, l2 = ora.keybias_fwd(q2, k.numpy(), v.numpy(), b.numpy(), scale, True)
+    assert np.all(o2[:, :7] == 0) and np.all(np.isinf(l2[:, :, :7]))
+    np.testing.assert_allclose(o2[:, 7:], full_o, rtol=1e-12, atol=1e-12)
+
+
+def test_rows_subset_matches_full():
+    q, k, v, b = _inputs(1, 50, 50, 4, 2, 8, seed=6)
+    scale = 8 ** -0.5
+    fo, fl = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    rows = np.array([0, 7, 31, 49])
+    so, sl = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True, rows=rows)
+    np.testing.assert_allclose(so, fo[:, rows], rtol=1e-12)
+    np.testing.assert_allclose(sl, fl[:, :, rows], rtol=1e-12)
+
+
+@pytest.mark.parametrize("H,Hkv,causal", [(4, 2, True), (4, 4, False), (6, 2, True)])
+def test_bwd_matches_autograd(H, Hkv, causal):
+    q, k, v, b = _inputs(2, 23, 23, H, Hkv, 8, seed=7 + H)
+    scale = 8 ** -0.5
+    g = torch.Generator().manual_seed(99)
+    dout = torch.randn(2, 23, H, 8, generator=g).double()
+    qr, kr, vr, br = [t.clone().requires_grad_(True) for t in (q, k, v, b)]
+    out, _ = _sdpa(qr, kr, vr, br, scale, causal)
+    (out * dout).sum().backward()
+    dq, dk, dv, dbias, sd = ora.keybias_bwd(dout.numpy(), q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, causal)
+    np.testing.assert_allclose(dq, qr.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(dk, kr.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(dv, vr.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(dbias, br.grad.numpy(), rtol=1e-9, atol=1e-10)
+    np.testing.assert_allclose(sd, (out.detach() * dout).sum(-1).transpose(1, 2).numpy(), rtol=1e-9, atol=1e-10)
+
+
+def test_dbias_finite_difference():
+    """dL/dbias_raw by central differences: the scale factor and sign of the bias gradient."""
+    q, k, v, b = _inputs(1, 6, 6, 2, 1, 4, seed=8)
+    scale = 0.37
+    rng = np.random.default_rng(1)
+    dout = rng.standard_normal((1, 6, 2, 4))
+    _, _, _, dbias, _ = ora.keybias_bwd(dout, q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+
+    def loss(bb):
+        o, _ = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), bb, scale, True)
+        return float((o * dout).sum())
+
+    eps = 1e-6
+    for (h, j) in [(0, 0), (1, 3), (0, 5)]:
+        bp = b.numpy().copy(); bp[0, h, j] += eps
+        bm = b.numpy().copy(); bm[0, h, j] -= eps
+        fd = (loss(bp) - loss(bm)) / (2 * eps)
+        assert abs(fd - dbias[0, h, j]) < 1e-6 * max(1.0, abs(fd)), (h, j, fd, dbias[0, h, j])
+
+
+def test_varlen_matches_block_diagonal_sdpa():
+    lens = [5, 1, 9, 0, 4]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    total, H, Hkv, D = int(cu[-1]), 4, 2, 8
+    g = torch.Generator().manual_seed(10)
+    q = torch.randn(total, H, D, generator=g).double()
+    k = torch.randn(total, Hkv, D, generator=g).double()
+    v = torch.randn(total, Hkv, D, generator=g).double()
+    bias = torch.randn(len(lens), H, max(lens), generator=g).double()
+    scale = D ** -0.5
+    out, lse = ora.keybias_varlen_fwd(q.numpy(), k.numpy(), v.numpy(), bias.numpy(), cu, scale, True)
+    # one packed row with a block-diagonal causal mask and each key's own-sequence bias
+    seq = np.repeat(np.arange(len(lens)), lens)
+    pos = np.concatenate([np.arange(n) for n in lens])
+    mask = torch.full((H, total, total), float("-inf"), dtype=torch.float64)
+    for i in range(total):
+        for j in range(total):
+            if seq[i] == seq[j] and pos[j] <= pos[i]:
+                mask[:, i, j] = scale * bias[seq[j], :, pos[j]]
+    ro = F.scaled_dot_product_attention(q.transpose(0, 1)[None], k.transpose(0, 1)[None], v.transpose(0, 1)[None],
+                                        attn_mask=mask[None], scale=scale, enable_gqa=True)[0].transpose(0, 1)
+    np.testing.assert_allclose(out, ro.numpy(), rtol=1e-10, atol=1e-10)
+    logits = (q.transpose(0, 1) @ k.transpose(0, 1).repeat_interleave(2, 0).transpose(-1, -2)) * scale + mask
+    np.testing.assert_allclose(lse, torch.logsumexp(logits, -1).numpy(), rtol=1e-10, atol=1e-10)
+
+
+def test_bf16_round_matches_torch():
+    x = np.random.default_rng(0).standard_normal(10000).astype(np.float32) * 100
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(ora.bf16_round(x), ref)
