@@ -69,6 +69,34 @@ int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const flo
                           int64_t bias_seq_stride, int64_t bias_head_stride,
                           float softmax_scale, int32_t causal, hipStream_t stream);
 
+/* Dense key-bias attention backward.
+ * Replaces ext().bwd(dout, q, k, v, out, lse, None, None, None, bias_raw, 0.0, scale, causal,
+ * -1, -1, 0.0, False, None, None) -> (dq, dk, dv, softmax_d, dbias) (kernels/fa2bias/keybias.py:52-63;
+ * patched mha_bwd and the dBias reduction, keybias.patch:87-129, 219-271).
+ * Outputs (caller-allocated, fully overwritten): dq like q, dk/dv like k/v (summed over the query
+ * heads of each KV head), softmax_d (B, H, Sq) fp32 = rowsum(dout * out), and, when bias_raw is
+ * given, dbias (B, H, Sk) fp32 = softmax_scale * sum_i dS[i, j] (the gradient with respect to
+ * bias_raw).  Deterministic: no atomics.
+ * strides: 28 int64 on the host, in elements:
+ *   q, k, v, out, dout, dq, dk, dv as (batch, row, head) triples, then bias (batch, head) and
+ *   dbias (batch, head). */
+int tg_keybias_bwd(const void *dout, const void *q, const void *k, const void *v, const void *out,
+                   const float *lse, const float *bias_raw, void *dq, void *dk, void *dv, float *dbias,
+                   float *softmax_d, int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                   int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                   const int64_t *strides, float softmax_scale, int32_t causal, hipStream_t stream);
+
+/* Variable-length backward (kernels/fa2bias/keybias.py:103-115).  lse and softmax_d are (H, total);
+ * bias_raw and dbias are (num_seqs, H, max_seqlen).
+ * strides: 20 int64 on the host: q, k, v, out, dout, dq, dk, dv as (row, head) pairs, then bias
+ * (seq, head) and dbias (seq, head). */
+int tg_keybias_varlen_bwd(const void *dout, const void *q, const void *k, const void *v, const void *out,
+                          const float *lse, const float *bias_raw, void *dq, void *dk, void *dv,
+                          float *dbias, float *softmax_d, const int32_t *cu_seqlens,
+                          int32_t num_seqs, int32_t max_seqlen, int32_t total,
+                          int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                          const int64_t *strides, float softmax_scale, int32_t causal, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

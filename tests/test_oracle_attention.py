@@ -164,3 +164,20 @@ def test_bf16_round_matches_torch():
     x = np.random.default_rng(0).standard_normal(10000).astype(np.float32) * 100
     ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     assert np.array_equal(ora.bf16_round(x), ref)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_torch_oracle_matches_numpy(causal):
+    from oracle import attention_torch as ort
+    q, k, v, b = _inputs(2, 41, 45, 6, 2, 16, seed=21)
+    scale = 16 ** -0.5
+    g = torch.Generator().manual_seed(5)
+    dout = torch.randn(2, 41, 6, 16, generator=g).double()
+    o, l = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, causal)
+    to, tl = ort.fwd(q.float(), k.float(), v.float(), b.float(), scale, causal, chunk=16)
+    np.testing.assert_allclose(to.numpy(), o, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(tl.numpy(), l, rtol=1e-5, atol=1e-5)
+    ref = ora.keybias_bwd(dout.numpy(), q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, causal)
+    got = ort.bwd(dout.float(), q.float(), k.float(), v.float(), b.float(), scale, causal, chunk=16)
+    for r, t in zip(ref, got):
+        np.testing.assert_allclose(t.numpy(), r, rtol=1e-3, atol=1e-4)

@@ -27,6 +27,8 @@ SIGNATURES = {
                               i32, i32, i32, i32, i32, i32,
                               i64, i64, i64, i64, i64, i64, i64, i64,
                               i64, i64, f32, i32, vp],
+    "tg_keybias_bwd": [vp] * 12 + [i32] * 6 + [vp, f32, i32, vp],
+    "tg_keybias_varlen_bwd": [vp] * 13 + [i32] * 6 + [vp, f32, i32, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p}
 

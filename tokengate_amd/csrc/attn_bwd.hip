@@ -1,0 +1,638 @@
+// Key-bias causal GQA attention, backward, for gfx950 (MI355X).
+//
+// Math (reference: kernels/fa2bias/keybias.patch:87-129, 219-271; keybias.py:52-82):
+//   P = exp(z - lse), D_i = sum_d dO_i * O_i, dS = P * (dO V^T - D),
+//   dQ = scale dS K,  dK = scale sum_{h in group} dS^T Q,  dV = sum_{h in group} P^T dO,
+//   dbias_raw[b,h,j] = scale * sum_i dS[i,j]   (the gradient with respect to bias_raw).
+//
+// Three launches, no atomics (every output element is written exactly once, so results are
+// deterministic, unlike the reference's atomicAdd dBias, keybias.patch:267):
+//   1. preprocess: D = rowsum(dO * O) (returned as softmax_d, like FA2);
+//   2. dQ kernel, query-parallel (same 8-wave / 32-column structure as the forward): per 64-key
+//      tile recompute S^T = K Q^T and dP^T = V dO^T, form dS^T, accumulate dQ^T += K^T dS^T;
+//   3. dK/dV/dBias kernel, key-parallel: each wave owns 32 keys (K^T and V^T resident in
+//      registers) of one KV head and loops over every query head of its GQA group and every
+//      32-query tile: S = Q K^T, dP = dO V^T, P, dS, dV^T += dO^T P, dK^T += Q^T dS, and the dBias
+//      column sums stay in registers (one scalar per lane per head).
+// Tiles that are read both row-major (MFMA A operand, sigma-permuted rows) and transposed
+// (ds_read_b64_tr_b16) are stored in natural row order with the swizzle dual_swz(), which is
+// bank-conflict free for both access patterns.
+#include "tg_common.h"
+#include "../../include/tokengate_hip.h"
+
+namespace tg {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kRow = kD * 2;          // bytes per K/V/Q/dO row
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct BwdArgs {
+  const bf16_t *q, *k, *v, *o, *dout;
+  const float *lse, *bias;
+  float *softmax_d;
+  bf16_t *dq, *dk, *dv;
+  float *dbias;
+  const int32_t *cu_seqlens;
+  int64_t q_bs, q_rs, q_hs, k_bs, k_rs, k_hs, v_bs, v_rs, v_hs, o_bs, o_rs, o_hs;
+  int64_t do_bs, do_rs, do_hs, dq_bs, dq_rs, dq_hs, dk_bs, dk_rs, dk_hs, dv_bs, dv_rs, dv_hs;
+  int64_t bias_bs, bias_hs, dbias_bs, dbias_hs;
+  int64_t lse_total;       // varlen: lse / softmax_d are (H, total)
+  int batch, sq, sk, h, hkv, group;
+  int n_tiles;             // grid decomposition (q tiles for dQ, key tiles for dK/dV)
+  float scale, scale_log2;
+};
+
+__device__ __forceinline__ int sigma(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+// Chunk swizzle of a natural-order tile read both row-major (sigma rows) and transposed.
+__device__ __forceinline__ uint32_t dual_swz(int row) {
+  return (uint32_t)(4 * (row & 3) + (((row >> 2) ^ ((row >> 4) << 1)) & 3));
+}
+
+// Sequence geometry shared by the kernels.
+struct Seq {
+  int64_t row0;
+  int sq, sk;
+};
+template <bool VARLEN>
+__device__ __forceinline__ Seq seq_of(const BwdArgs &a, int b) {
+  Seq s{0, a.sq, a.sk};
+  if constexpr (VARLEN) {
+    const int s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
+    s.row0 = s0;
+    s.sq = min(s1 - s0, a.sq);
+    s.sk = s.sq;
+  }
+  return s;
+}
+
+// ---- 1. D = rowsum(dO * O): 16 lanes per (row, head) ----------------------------------------
+template <bool VARLEN>
+__global__ __launch_bounds__(256) void bwd_preprocess_kernel(BwdArgs a, int64_t nrows) {
+  const int64_t r = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;   // (b, i, h) flattened
+  const int sub = threadIdx.x & 15;
+  float acc = 0.f;
+  int64_t b = 0, i = 0, hh = 0;
+  bool valid = r < nrows;
+  if (valid) {
+    hh = r % a.h;
+    const int64_t bi = r / a.h;
+    if constexpr (VARLEN) {
+      i = bi;   // packed row
+    } else {
+      b = bi / a.sq;
+      i = bi % a.sq;
+    }
+    const bf16_t *o = a.o + b * a.o_bs + i * a.o_rs + hh * a.o_hs + 8 * sub;
+    const bf16_t *d = a.dout + b * a.do_bs + i * a.do_rs + hh * a.do_hs + 8 * sub;
+    const u32x4 ov = *reinterpret_cast<const u32x4 *>(o);
+    const u32x4 dv = *reinterpret_cast<const u32x4 *>(d);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      acc += bf16_to_f32((bf16_t)(ov[w] & 0xffff)) * bf16_to_f32((bf16_t)(dv[w] & 0xffff));
+      acc += bf16_to_f32((bf16_t)(ov[w] >> 16)) * bf16_to_f32((bf16_t)(dv[w] >> 16));
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  acc += __shfl_xor(acc, 8);
+  if (valid && sub == 0) {
+    if constexpr (VARLEN)
+      a.softmax_d[hh * a.lse_total + i] = acc;
+    else
+      a.softmax_d[(b * a.h + hh) * a.sq + i] = acc;
+  }
+}
+
+// ---- 2. dQ kernel ------------------------------------------------------------------------
+constexpr int kQWaves = 8;
+constexpr int kQThreads = 64 * kQWaves;
+constexpr int kBN = 64;                 // keys per tile
+constexpr int kTileBytes = kBN * kRow;  // 16 KiB
+template <int HP> constexpr int dq_bm() { return kQWaves * (32 / HP); }
+
+template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
+__global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
+  constexpr int QW = 32 / HP;
+  constexpr int BM = dq_bm<HP>();
+  __shared__ __attribute__((aligned(1024))) char ks[2][kTileBytes];   // natural rows, dual_swz
+  __shared__ __attribute__((aligned(1024))) char vs[2][kTileBytes];   // sigma rows, chunk ^ (row%16)
+  __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  const int hl = lq / QW, ql = lq % QW;
+  const int hgroups = a.group / HP;
+  const int per_q = a.hkv * hgroups;
+  const int x = blockIdx.x % per_q, rest = blockIdx.x / per_q;
+  const int kh = x % a.hkv, hg = x / a.hkv;
+  const int b = rest % a.batch;
+  const int qt = a.n_tiles - 1 - rest / a.batch;
+  const Seq sq_ = seq_of<VARLEN>(a, b);
+  const int sq = sq_.sq, sk = sq_.sk;
+  const int64_t row0 = sq_.row0;
+  const int q0 = qt * BM;
+  if (q0 >= sq) return;
+  const int off = sk - sq;
+  const int h0 = kh * a.group + hg * HP;
+  const int hh = h0 + hl;
+
+  const int64_t qb = VARLEN ? row0 * a.q_rs : (int64_t)b * a.q_bs;
+  const int64_t dob = VARLEN ? row0 * a.do_rs : (int64_t)b * a.do_bs;
+  const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
+  const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
+  const brsrc_t krs = make_rsrc(kbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.k_rs + kD) * 2) : 0u);
+  const brsrc_t vrs = make_rsrc(vbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.v_rs + kD) * 2) : 0u);
+  const float *bbase = HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)h0 * a.bias_hs : nullptr;
+  const brsrc_t brs =
+      make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
+
+  const int qw0 = q0 + wave * QW;
+  const int qrow = qw0 + ql;
+  const bool qvalid = qrow < sq;
+  const bool wave_has_rows = qw0 < sq;
+  const int qw_hi = min(qw0 + QW, sq) - 1;
+  bf16x8 qf[8], df[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    qf[s] = __builtin_bit_cast(bf16x8, gload16(a.q + qb + (int64_t)qrow * a.q_rs + (int64_t)hh * a.q_hs + 16 * s + 8 * g, qvalid));
+    df[s] = __builtin_bit_cast(bf16x8, gload16(a.dout + dob + (int64_t)qrow * a.do_rs + (int64_t)hh * a.do_hs + 16 * s + 8 * g, qvalid));
+  }
+  float lse2 = INFINITY, dsum = 0.f;
+  if (qvalid) {
+    const int64_t li = VARLEN ? (int64_t)hh * a.lse_total + row0 + qrow : ((int64_t)b * a.h + hh) * sq + qrow;
+    lse2 = a.lse[li] * kLog2e;
+    dsum = a.softmax_d[li];
+  }
+
+  int kv_end = sk;
+  if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
+  const int n_tiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
+
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int row = (wave * 2 + it) * 4 + (lane >> 4);
+    koff[it] = (uint32_t)(row * a.k_rs * 2 + (((lane & 15) ^ dual_swz(row)) << 4));
+    const int vkey = 32 * (row >> 5) + sigma(row & 31);
+    voff[it] = (uint32_t)(vkey * a.v_rs * 2 + (((lane & 15) ^ (row & 15)) << 4));
+  }
+  auto issue_tile = [&](int tile, int buf) {
+    const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
+    const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+      dma16(krs, ks[buf] + (wave * 2 + it) * 1024, kb0 + koff[it]);
+      dma16(vrs, vs[buf] + (wave * 2 + it) * 1024, vb0 + voff[it]);
+    }
+    if constexpr (HAS_BIAS) {
+      if (wave < HP) dma4(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
+    }
+  };
+
+  // transposed K reads (A operand of dQ^T = K^T dS^T)
+  const int r16 = lane & 15;
+  const int tr_row = r16 >> 2;
+  const int tr_c = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
+  const uint32_t tr_half = (uint32_t)((r16 & 1) * 8);
+
+  f32x16 dqacc[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) dqacc[d][v] = 0.f;
+
+  if (n_tiles > 0) issue_tile(0, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    const int buf = t & 1;
+    const int n0 = t * kBN;
+    wait_all_mem();
+    __syncthreads();
+    if (t + 1 < n_tiles) issue_tile(t + 1, buf ^ 1);
+    if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
+
+    // S^T = K Q^T and dP^T = V dO^T (A operands: sigma rows of K and V)
+    f32x16 sacc[2], pacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) { sacc[kb][v] = 0.f; pacc[kb][v] = 0.f; }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int krow = 32 * kb + sigma(lq);
+        const bf16x8 kf = lds_load16(ks[buf], krow * kRow + (((uint32_t)(2 * s + g) ^ dual_swz(krow)) << 4));
+        sacc[kb] = mfma32(kf, qf[s], sacc[kb]);
+        const int vrow = 32 * kb + lq;
+        const bf16x8 vf = lds_load16(vs[buf], vrow * kRow + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
+        pacc[kb] = mfma32(vf, df[s], pacc[kb]);
+      }
+    }
+    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
+    uint32_t dsk[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      float bb[16];
+      if constexpr (HAS_BIAS) {
+        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 t4 = bp[i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bb[4 * i + e] = t4[e];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 16; v += 2) {
+        float ds2[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          float z = sacc[kb][v + e];
+          if constexpr (HAS_BIAS) z += bb[v + e];
+          float p = fast_exp2(fmaf(z, a.scale_log2, -lse2));
+          if (need_mask) {
+            const int key = n0 + 32 * kb + 16 * g + v + e;
+            bool masked = key >= sk;
+            if constexpr (CAUSAL) masked = masked || (key > qrow + off);
+            p = masked ? 0.f : p;
+          }
+          ds2[e] = p * (pacc[kb][v + e] - dsum);
+        }
+        dsk[kb][v >> 1] = pack_bf16x2(ds2[0], ds2[1]);
+      }
+    }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 w = {dsk[kb][4 * s], dsk[kb][4 * s + 1], dsk[kb][4 * s + 2], dsk[kb][4 * s + 3]};
+        const bf16x8 bop = __builtin_bit_cast(bf16x8, w);
+        const int k0 = 32 * kb + 16 * g + 8 * s;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk) {
+          const int c = 4 * dblk + tr_c;
+          const int r0 = k0 + tr_row, r1 = k0 + 4 + tr_row;
+          const s16x4 lo = lds_read_tr16(ks[buf] + r0 * kRow + (((uint32_t)c ^ dual_swz(r0)) << 4) + tr_half);
+          const s16x4 hi = lds_read_tr16(ks[buf] + r1 * kRow + (((uint32_t)c ^ dual_swz(r1)) << 4) + tr_half);
+          const bf16x8 aop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+          dqacc[dblk] = mfma32(aop, bop, dqacc[dblk]);
+        }
+      }
+    }
+  }
+  if (qvalid) {
+    bf16_t *row = a.dq + (VARLEN ? row0 * a.dq_rs : (int64_t)b * a.dq_bs) + (int64_t)qrow * a.dq_rs + (int64_t)hh * a.dq_hs;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d = 32 * dblk + 8 * a4 + 4 * g;
+        const u32x2 w = {pack_bf16x2(dqacc[dblk][4 * a4] * a.scale, dqacc[dblk][4 * a4 + 1] * a.scale),
+                         pack_bf16x2(dqacc[dblk][4 * a4 + 2] * a.scale, dqacc[dblk][4 * a4 + 3] * a.scale)};
+        *reinterpret_cast<u32x2 *>(row + d) = w;
+      }
+  }
+}
+
+// ---- 3. dK / dV / dBias kernel -----------------------------------------------------------
+constexpr int kKWaves = 4;
+constexpr int kKThreads = 64 * kKWaves;
+constexpr int kKBlock = 32 * kKWaves;   // keys per workgroup
+constexpr int kQT = 32;                 // queries per tile
+constexpr int kQTileBytes = kQT * kRow; // 8 KiB
+
+template <bool CAUSAL, bool HAS_BIAS, bool VARLEN>
+__global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char qs[2][kQTileBytes];    // natural rows, dual_swz
+  __shared__ __attribute__((aligned(1024))) char dos[2][kQTileBytes];
+  __shared__ __attribute__((aligned(128))) float ls[2][kQT];            // lse (natural log)
+  __shared__ __attribute__((aligned(128))) float dsh[2][kQT];           // D
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  // heaviest first: under the causal mask the first key tiles see the most queries
+  const int kh = blockIdx.x % a.hkv;
+  const int rest = blockIdx.x / a.hkv;
+  const int b = rest % a.batch;
+  const int kt = rest / a.batch;
+  const Seq sq_ = seq_of<VARLEN>(a, b);
+  const int sq = sq_.sq, sk = sq_.sk;
+  const int64_t row0 = sq_.row0;
+  const int n0 = kt * kKBlock;
+  if (n0 >= sk) return;
+  const int off = sk - sq;
+  const int kw0 = n0 + 32 * wave;
+  const int key = kw0 + lq;              // this lane's key (MFMA column)
+  const bool kvalid = key < sk;
+  const bool wave_has_keys = kw0 < sk;
+
+  const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
+  const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
+  bf16x8 kf[8], vf[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    kf[s] = __builtin_bit_cast(bf16x8, gload16(kbase + (int64_t)key * a.k_rs + 16 * s + 8 * g, kvalid));
+    vf[s] = __builtin_bit_cast(bf16x8, gload16(vbase + (int64_t)key * a.v_rs + 16 * s + 8 * g, kvalid));
+  }
+
+  // first query tile that sees any of this workgroup's keys
+  int m_start = 0;
+  if constexpr (CAUSAL) m_start = max(0, n0 - off) / kQT * kQT;
+  const int n_qt = sq > m_start ? (sq - m_start + kQT - 1) / kQT : 0;
+
+  const int qrow_l = (wave * 2) * 4 + (lane >> 4);   // rows written by this lane's two DMA slots:
+  uint32_t qoff[2], dooff[2];                          // wave w covers rows 8w .. 8w+7
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int row = qrow_l + 4 * it;
+    const uint32_t c16 = ((uint32_t)(lane & 15) ^ dual_swz(row)) << 4;
+    qoff[it] = (uint32_t)(row * a.q_rs * 2) + c16;
+    dooff[it] = (uint32_t)(row * a.do_rs * 2) + c16;
+  }
+
+  const int r16 = lane & 15;
+  const int tr_row = r16 >> 2;
+  const int tr_c = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
+  const uint32_t tr_half = (uint32_t)((r16 & 1) * 8);
+
+  f32x16 dkacc[4], dvacc[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) { dkacc[d][v] = 0.f; dvacc[d][v] = 0.f; }
+
+  for (int hi = 0; hi < a.group; ++hi) {
+    const int hh = kh * a.group + hi;
+    const bf16_t *qbase = a.q + (VARLEN ? row0 * a.q_rs : (int64_t)b * a.q_bs) + (int64_t)hh * a.q_hs;
+    const bf16_t *dobase = a.dout + (VARLEN ? row0 * a.do_rs : (int64_t)b * a.do_bs) + (int64_t)hh * a.do_hs;
+    const brsrc_t qrs = make_rsrc(qbase, sq > 0 ? (uint32_t)(((int64_t)(sq - 1) * a.q_rs + kD) * 2) : 0u);
+    const brsrc_t dors = make_rsrc(dobase, sq > 0 ? (uint32_t)(((int64_t)(sq - 1) * a.do_rs + kD) * 2) : 0u);
+    const int64_t li0 = VARLEN ? (int64_t)hh * a.lse_total + row0 : ((int64_t)b * a.h + hh) * sq;
+    const brsrc_t lrs = make_rsrc(a.lse + li0, (uint32_t)sq * 4);
+    const brsrc_t drs = make_rsrc(a.softmax_d + li0, (uint32_t)sq * 4);
+    float bk = 0.f;
+    if constexpr (HAS_BIAS)
+      if (kvalid) bk = a.bias[(int64_t)b * a.bias_bs + (int64_t)hh * a.bias_hs + key];
+    float dbacc = 0.f;
+
+    auto issue_tile = [&](int m0, int buf) {
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        dma16(qrs, qs[buf] + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff[it]);
+        dma16(dors, dos[buf] + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff[it]);
+      }
+      if (wave == 0 && lane < kQT) dma4(lrs, &ls[buf][0], (uint32_t)(m0 + lane) * 4);
+      if (wave == 1 && lane < kQT) dma4(drs, &dsh[buf][0], (uint32_t)(m0 + lane) * 4);
+    };
+
+    __syncthreads();   // previous head's last tile fully consumed before its buffers are reused
+    if (n_qt > 0) issue_tile(m_start, 0);
+    for (int t = 0; t < n_qt; ++t) {
+      const int buf = t & 1;
+      const int m0 = m_start + t * kQT;
+      wait_all_mem();
+      __syncthreads();
+      if (t + 1 < n_qt) issue_tile(m0 + kQT, buf ^ 1);
+      if (!wave_has_keys || (CAUSAL && m0 + kQT - 1 + off < kw0)) continue;
+
+      // S = Q K^T and dP = dO V^T: A operands are sigma rows of the Q / dO tiles
+      f32x16 sacc, pacc;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) { sacc[v] = 0.f; pacc[v] = 0.f; }
+      const int srow = sigma(lq);
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const uint32_t o16 = srow * kRow + (((uint32_t)(2 * s + g) ^ dual_swz(srow)) << 4);
+        sacc = mfma32(lds_load16(qs[buf], o16), kf[s], sacc);
+        pacc = mfma32(lds_load16(dos[buf], o16), vf[s], pacc);
+      }
+      // rows of the accumulators: queries m0 + 16g + v
+      const f32x4 *lp = reinterpret_cast<const f32x4 *>(&ls[buf][16 * g]);
+      const f32x4 *dp = reinterpret_cast<const f32x4 *>(&dsh[buf][16 * g]);
+      const bool need_mask = (m0 + kQT > sq) || (kw0 + 32 > sk) || (CAUSAL && kw0 + 31 > m0 + off);
+      uint32_t pk[8], dk8[8];
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const f32x4 l4 = lp[i4], d4 = dp[i4];
+        float p[4], ds[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * i4 + e;
+          float z = sacc[v];
+          if constexpr (HAS_BIAS) z += bk;
+          p[e] = fast_exp2(fmaf(z, a.scale_log2, -l4[e] * kLog2e));
+          if (need_mask) {
+            const int qi = m0 + 16 * g + v;
+            bool masked = qi >= sq || !kvalid;
+            if constexpr (CAUSAL) masked = masked || (key > qi + off);
+            p[e] = masked ? 0.f : p[e];
+          }
+          ds[e] = p[e] * (pacc[v] - d4[e]);
+          dbacc += ds[e];
+        }
+        pk[2 * i4] = pack_bf16x2(p[0], p[1]);
+        pk[2 * i4 + 1] = pack_bf16x2(p[2], p[3]);
+        dk8[2 * i4] = pack_bf16x2(ds[0], ds[1]);
+        dk8[2 * i4 + 1] = pack_bf16x2(ds[2], ds[3]);
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS (A operands: transposed reads of the dO / Q tiles)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 wp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
+        const u32x4 wd = {dk8[4 * s], dk8[4 * s + 1], dk8[4 * s + 2], dk8[4 * s + 3]};
+        const bf16x8 pop = __builtin_bit_cast(bf16x8, wp);
+        const bf16x8 dop = __builtin_bit_cast(bf16x8, wd);
+        const int q0r = 16 * g + 8 * s;
+#pragma unroll
+        for (int dblk = 0; dblk < 4; ++dblk) {
+          const int c = 4 * dblk + tr_c;
+          const int r0 = q0r + tr_row, r1 = q0r + 4 + tr_row;
+          const uint32_t o0 = r0 * kRow + (((uint32_t)c ^ dual_swz(r0)) << 4) + tr_half;
+          const uint32_t o1 = r1 * kRow + (((uint32_t)c ^ dual_swz(r1)) << 4) + tr_half;
+          const bf16x8 dot_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(dos[buf] + o0),
+                                                                                 lds_read_tr16(dos[buf] + o1),
+                                                                                 0, 1, 2, 3, 4, 5, 6, 7));
+          dvacc[dblk] = mfma32(dot_, pop, dvacc[dblk]);
+          const bf16x8 qt_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qs[buf] + o0),
+                                                                                lds_read_tr16(qs[buf] + o1),
+                                                                                0, 1, 2, 3, 4, 5, 6, 7));
+          dkacc[dblk] = mfma32(qt_, dop, dkacc[dblk]);
+        }
+      }
+    }
+    if constexpr (HAS_BIAS) {
+      const float tot = pair_sum(dbacc);
+      if (g == 0 && kvalid)
+        a.dbias[(int64_t)b * a.dbias_bs + (int64_t)hh * a.dbias_hs + key] = tot * a.scale;
+    }
+  }
+  if (kvalid) {
+    bf16_t *krow = a.dk + (VARLEN ? row0 * a.dk_rs : (int64_t)b * a.dk_bs) + (int64_t)key * a.dk_rs + (int64_t)kh * a.dk_hs;
+    bf16_t *vrow = a.dv + (VARLEN ? row0 * a.dv_rs : (int64_t)b * a.dv_bs) + (int64_t)key * a.dv_rs + (int64_t)kh * a.dv_hs;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; ++dblk)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d = 32 * dblk + 8 * a4 + 4 * g;
+        const u32x2 wk = {pack_bf16x2(dkacc[dblk][4 * a4] * a.scale, dkacc[dblk][4 * a4 + 1] * a.scale),
+                          pack_bf16x2(dkacc[dblk][4 * a4 + 2] * a.scale, dkacc[dblk][4 * a4 + 3] * a.scale)};
+        const u32x2 wv = {pack_bf16x2(dvacc[dblk][4 * a4], dvacc[dblk][4 * a4 + 1]),
+                          pack_bf16x2(dvacc[dblk][4 * a4 + 2], dvacc[dblk][4 * a4 + 3])};
+        *reinterpret_cast<u32x2 *>(krow + d) = wk;
+        *reinterpret_cast<u32x2 *>(vrow + d) = wv;
+      }
+  }
+}
+
+// ---- host dispatch ---------------------------------------------------------------------------
+template <bool VARLEN>
+void launch_bwd(const BwdArgs &a0, bool causal, bool has_bias, int64_t nrows, hipStream_t st) {
+  BwdArgs a = a0;
+  hipLaunchKernelGGL(bwd_preprocess_kernel<VARLEN>, dim3((unsigned)((nrows * 16 + 255) / 256)), dim3(256), 0, st,
+                     a, nrows);
+  const int hp = (a.group % 2 == 0) ? 2 : 1;
+  const int bmq = hp == 2 ? dq_bm<2>() : dq_bm<1>();
+  a.n_tiles = (a.sq + bmq - 1) / bmq;
+  const unsigned nq = (unsigned)((int64_t)a.n_tiles * a.batch * (a.h / hp));
+#define TG_DQ(HPV, C, B)                                                                               \
+  if (hp == HPV && causal == C && has_bias == B)                                                       \
+    hipLaunchKernelGGL((bwd_dq_kernel<HPV, C, B, VARLEN>), dim3(nq), dim3(kQThreads), 0, st, a);
+  TG_DQ(2, true, true) TG_DQ(2, true, false) TG_DQ(2, false, true) TG_DQ(2, false, false)
+  TG_DQ(1, true, true) TG_DQ(1, true, false) TG_DQ(1, false, true) TG_DQ(1, false, false)
+#undef TG_DQ
+  const int nkt = (a.sk + kKBlock - 1) / kKBlock;
+  const unsigned nk = (unsigned)((int64_t)nkt * a.batch * a.hkv);
+#define TG_DKV(C, B)                                                                                   \
+  if (causal == C && has_bias == B)                                                                    \
+    hipLaunchKernelGGL((bwd_dkdv_kernel<C, B, VARLEN>), dim3(nk), dim3(kKThreads), 0, st, a);
+  TG_DKV(true, true) TG_DKV(true, false) TG_DKV(false, true) TG_DKV(false, false)
+#undef TG_DKV
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool strides_ok(std::initializer_list<int64_t> s) {
+  for (int64_t x : s)
+    if (x % 8 != 0) return false;
+  return true;
+}
+bool span_ok(int64_t rows, int64_t row_stride) { return (rows + 1) * row_stride * 2 < (1ll << 32) - 1024; }
+
+int check_bwd(const void *dout, const void *q, const void *k, const void *v, const void *out, const float *lse,
+              const void *dq, const void *dk, const void *dv, const float *softmax_d, int32_t num_heads,
+              int32_t num_heads_k, int32_t head_dim, float softmax_scale) {
+  TG_CHECK(head_dim == kD, "this build supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
+  TG_CHECK(dout && q && k && v && out && lse && dq && dk && dv && softmax_d, "null tensor pointer");
+  TG_CHECK(aligned16(dout) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dq) &&
+               aligned16(dk) && aligned16(dv),
+           "tensors must be 16-byte aligned");
+  TG_CHECK(num_heads > 0 && num_heads_k > 0 && num_heads % num_heads_k == 0,
+           "Number of heads in key/value must divide number of heads in query (%d, %d)", num_heads, num_heads_k);
+  TG_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
+  return 0;
+}
+
+}  // namespace
+}  // namespace tg
+
+using namespace tg;
+
+extern "C" int tg_keybias_bwd(const void *dout, const void *q, const void *k, const void *v, const void *out,
+                              const float *lse, const float *bias_raw, void *dq, void *dk, void *dv, float *dbias,
+                              float *softmax_d, int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                              int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                              const int64_t *strides, float softmax_scale, int32_t causal, hipStream_t stream) {
+  clear_error();
+  if (int e = check_bwd(dout, q, k, v, out, lse, dq, dk, dv, softmax_d, num_heads, num_heads_k, head_dim,
+                        softmax_scale))
+    return e;
+  TG_CHECK(strides != nullptr, "null strides");
+  TG_CHECK(batch >= 0 && seqlen_q >= 0 && seqlen_k >= 0, "negative size");
+  TG_CHECK(bias_raw == nullptr || dbias != nullptr, "dbias is required with a bias");
+  BwdArgs a{};
+  const int64_t *s = strides;
+  a.q_bs = s[0]; a.q_rs = s[1]; a.q_hs = s[2];
+  a.k_bs = s[3]; a.k_rs = s[4]; a.k_hs = s[5];
+  a.v_bs = s[6]; a.v_rs = s[7]; a.v_hs = s[8];
+  a.o_bs = s[9]; a.o_rs = s[10]; a.o_hs = s[11];
+  a.do_bs = s[12]; a.do_rs = s[13]; a.do_hs = s[14];
+  a.dq_bs = s[15]; a.dq_rs = s[16]; a.dq_hs = s[17];
+  a.dk_bs = s[18]; a.dk_rs = s[19]; a.dk_hs = s[20];
+  a.dv_bs = s[21]; a.dv_rs = s[22]; a.dv_hs = s[23];
+  a.bias_bs = s[24]; a.bias_hs = s[25]; a.dbias_bs = s[26]; a.dbias_hs = s[27];
+  TG_CHECK(strides_ok({a.q_bs, a.q_rs, a.q_hs, a.k_bs, a.k_rs, a.k_hs, a.v_bs, a.v_rs, a.v_hs, a.o_bs, a.o_rs,
+                       a.o_hs, a.do_bs, a.do_rs, a.do_hs, a.dq_bs, a.dq_rs, a.dq_hs, a.dk_bs, a.dk_rs, a.dk_hs,
+                       a.dv_bs, a.dv_rs, a.dv_hs}),
+           "tensor strides must be multiples of 8 elements");
+  if (batch == 0 || seqlen_q == 0 || seqlen_k == 0) return 0;
+  TG_CHECK(span_ok(seqlen_k, a.k_rs) && span_ok(seqlen_k, a.v_rs) && span_ok(seqlen_q, a.q_rs) &&
+               span_ok(seqlen_q, a.do_rs),
+           "one (batch, head) slice must span less than 4 GiB");
+  a.dout = static_cast<const bf16_t *>(dout);
+  a.q = static_cast<const bf16_t *>(q);
+  a.k = static_cast<const bf16_t *>(k);
+  a.v = static_cast<const bf16_t *>(v);
+  a.o = static_cast<const bf16_t *>(out);
+  a.lse = lse;
+  a.bias = bias_raw;
+  a.dq = static_cast<bf16_t *>(dq);
+  a.dk = static_cast<bf16_t *>(dk);
+  a.dv = static_cast<bf16_t *>(dv);
+  a.dbias = dbias;
+  a.softmax_d = softmax_d;
+  a.batch = batch; a.sq = seqlen_q; a.sk = seqlen_k;
+  a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
+  a.scale = softmax_scale;
+  a.scale_log2 = softmax_scale * kLog2e;
+  launch_bwd<false>(a, causal != 0, bias_raw != nullptr, (int64_t)batch * seqlen_q * num_heads, stream);
+  TG_HIP_CHECK(hipPeekAtLastError());
+  return 0;
+}
+
+extern "C" int tg_keybias_varlen_bwd(const void *dout, const void *q, const void *k, const void *v,
+                                     const void *out, const float *lse, const float *bias_raw, void *dq, void *dk,
+                                     void *dv, float *dbias, float *softmax_d, const int32_t *cu_seqlens,
+                                     int32_t num_seqs, int32_t max_seqlen, int32_t total, int32_t num_heads,
+                                     int32_t num_heads_k, int32_t head_dim, const int64_t *strides,
+                                     float softmax_scale, int32_t causal, hipStream_t stream) {
+  clear_error();
+  if (int e = check_bwd(dout, q, k, v, out, lse, dq, dk, dv, softmax_d, num_heads, num_heads_k, head_dim,
+                        softmax_scale))
+    return e;
+  TG_CHECK(strides != nullptr && cu_seqlens != nullptr, "null strides or cu_seqlens");
+  TG_CHECK(num_seqs >= 0 && max_seqlen >= 0 && total >= 0, "negative size");
+  TG_CHECK(bias_raw == nullptr || dbias != nullptr, "dbias is required with a bias");
+  BwdArgs a{};
+  const int64_t *s = strides;   // (row, head) pairs; batch strides unused
+  a.q_rs = s[0]; a.q_hs = s[1]; a.k_rs = s[2]; a.k_hs = s[3]; a.v_rs = s[4]; a.v_hs = s[5];
+  a.o_rs = s[6]; a.o_hs = s[7]; a.do_rs = s[8]; a.do_hs = s[9]; a.dq_rs = s[10]; a.dq_hs = s[11];
+  a.dk_rs = s[12]; a.dk_hs = s[13]; a.dv_rs = s[14]; a.dv_hs = s[15];
+  a.bias_bs = s[16]; a.bias_hs = s[17]; a.dbias_bs = s[18]; a.dbias_hs = s[19];
+  TG_CHECK(strides_ok({a.q_rs, a.q_hs, a.k_rs, a.k_hs, a.v_rs, a.v_hs, a.o_rs, a.o_hs, a.do_rs, a.do_hs, a.dq_rs,
+                       a.dq_hs, a.dk_rs, a.dk_hs, a.dv_rs, a.dv_hs}),
+           "tensor strides must be multiples of 8 elements");
+  if (num_seqs == 0 || max_seqlen == 0 || total == 0) return 0;
+  TG_CHECK(span_ok(total, a.k_rs) && span_ok(total, a.v_rs) && span_ok(total, a.q_rs) && span_ok(total, a.do_rs),
+           "the packed tensors must span less than 4 GiB");
+  a.dout = static_cast<const bf16_t *>(dout);
+  a.q = static_cast<const bf16_t *>(q);
+  a.k = static_cast<const bf16_t *>(k);
+  a.v = static_cast<const bf16_t *>(v);
+  a.o = static_cast<const bf16_t *>(out);
+  a.lse = lse;
+  a.bias = bias_raw;
+  a.dq = static_cast<bf16_t *>(dq);
+  a.dk = static_cast<bf16_t *>(dk);
+  a.dv = static_cast<bf16_t *>(dv);
+  a.dbias = dbias;
+  a.softmax_d = softmax_d;
+  a.cu_seqlens = cu_seqlens;
+  a.lse_total = total;
+  a.batch = num_seqs; a.sq = max_seqlen; a.sk = max_seqlen;
+  a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
+  a.scale = softmax_scale;
+  a.scale_log2 = softmax_scale * kLog2e;
+  launch_bwd<true>(a, causal != 0, bias_raw != nullptr, (int64_t)total * num_heads, stream);
+  TG_HIP_CHECK(hipPeekAtLastError());
+  return 0;
+}

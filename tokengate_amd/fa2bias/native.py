@@ -8,6 +8,8 @@ signatures and their validation (the patched mha_fwd / mha_bwd checks, keybias.p
 ctypes on torch's current stream.  Tensors are never copied to make them fit: a layout the
 kernels cannot read raises RuntimeError, as the reference's TORCH_CHECKs do.
 """
+import ctypes
+
 import torch
 
 from tokengate_amd import _lib
@@ -114,3 +116,82 @@ class KeyBiasExt:
                       bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
                       float(softmax_scale), int(bool(is_causal)), _stream(q))
         return [out, lse, torch.empty(0, device=q.device), torch.empty(0, device=q.device)]
+
+    def bwd(self, dout, q, k, v, out, softmax_lse, dq_, dk_, dv_, alibi_slopes_, p_dropout, softmax_scale,
+            is_causal, window_size_left, window_size_right, softcap, deterministic, gen_, rng_state):
+        _check_qkv(q, k, v)
+        _check_unsupported(p_dropout, window_size_left, window_size_right, softcap, False)
+        _check(dout.dtype == q.dtype and out.dtype == q.dtype, "dout and out must have the dtype of q")
+        _check(dout.stride(-1) == 1 and out.stride(-1) == 1, "dout and out must have contiguous last dimension")
+        B, Sq, H, D = q.shape
+        Sk, Hkv = k.shape[1], k.shape[2]
+        _check(tuple(dout.shape) == tuple(q.shape) and tuple(out.shape) == tuple(q.shape), "dout/out shape mismatch")
+        _check(tuple(softmax_lse.shape) == (B, H, Sq) and softmax_lse.dtype == torch.float32
+               and softmax_lse.is_contiguous(), "softmax_lse must be contiguous fp32 (batch, heads, seqlen_q)")
+        bias = alibi_slopes_
+        if bias is not None:
+            _check_bias(bias, B, H, Sk)
+        dq = dq_ if dq_ is not None else torch.empty_like(q)
+        dk = dk_ if dk_ is not None else torch.empty_like(k)
+        dv = dv_ if dv_ is not None else torch.empty_like(v)
+        for t, ref in ((dq, q), (dk, k), (dv, v)):
+            _check(t.shape == ref.shape and t.dtype == ref.dtype and t.stride(-1) == 1, "gradient buffer mismatch")
+        softmax_d = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
+        dbias = torch.empty((B, H, Sk), dtype=torch.float32, device=q.device) if bias is not None else None
+        strides = []
+        for t in (q, k, v, out, dout, dq, dk, dv):
+            strides += [t.stride(0), t.stride(1), t.stride(2)]
+        strides += [bias.stride(0), bias.stride(1)] if bias is not None else [0, 0]
+        strides += [dbias.stride(0), dbias.stride(1)] if dbias is not None else [0, 0]
+        arr = (ctypes.c_int64 * len(strides))(*strides)
+        if B and Sq and Sk:
+            _lib.call("tg_keybias_bwd", dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                      softmax_lse.data_ptr(), bias.data_ptr() if bias is not None else None,
+                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                      dbias.data_ptr() if dbias is not None else None, softmax_d.data_ptr(),
+                      B, Sq, Sk, H, Hkv, D, ctypes.cast(arr, ctypes.c_void_p), float(softmax_scale),
+                      int(bool(is_causal)), _stream(q))
+        elif B and Sq:
+            dq.zero_()
+            softmax_d.zero_()
+        return [dq, dk, dv, softmax_d, dbias]
+
+    def varlen_bwd(self, dout, q, k, v, out, softmax_lse, dq_, dk_, dv_, cu_seqlens_q, cu_seqlens_k,
+                   alibi_slopes_, max_seqlen_q, max_seqlen_k, p_dropout, softmax_scale, zero_tensors, is_causal,
+                   window_size_left, window_size_right, softcap, deterministic, gen_, rng_state):
+        _check_qkv(q, k, v)
+        _check_unsupported(p_dropout, window_size_left, window_size_right, softcap, False)
+        _check(cu_seqlens_q.data_ptr() == cu_seqlens_k.data_ptr() and max_seqlen_q == max_seqlen_k,
+               "this build runs self-attention over one cu_seqlens (q and k must share it)")
+        _check(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_cuda and cu_seqlens_q.is_contiguous(),
+               "cu_seqlens_q must have dtype int32, live on the device and be contiguous")
+        _check(dout.stride(-1) == 1 and out.stride(-1) == 1, "dout and out must have contiguous last dimension")
+        total, H, D = q.shape
+        Hkv = k.shape[1]
+        nseq = cu_seqlens_q.numel() - 1
+        _check(tuple(softmax_lse.shape) == (H, total) and softmax_lse.dtype == torch.float32
+               and softmax_lse.is_contiguous(), "softmax_lse must be contiguous fp32 (heads, total)")
+        bias = alibi_slopes_
+        if bias is not None:
+            _check_bias(bias, nseq, H, max_seqlen_k, "key bias (num_seqs, num_heads, max_seqlen_k)")
+        dq = dq_ if dq_ is not None else torch.empty_like(q)
+        dk = dk_ if dk_ is not None else torch.empty_like(k)
+        dv = dv_ if dv_ is not None else torch.empty_like(v)
+        if zero_tensors:
+            dq.zero_(); dk.zero_(); dv.zero_()
+        softmax_d = torch.empty((H, total), dtype=torch.float32, device=q.device)
+        dbias = torch.zeros((nseq, H, max_seqlen_k), dtype=torch.float32, device=q.device) if bias is not None else None
+        strides = []
+        for t in (q, k, v, out, dout, dq, dk, dv):
+            strides += [t.stride(0), t.stride(1)]
+        strides += [bias.stride(0), bias.stride(1)] if bias is not None else [0, 0]
+        strides += [dbias.stride(0), dbias.stride(1)] if dbias is not None else [0, 0]
+        arr = (ctypes.c_int64 * len(strides))(*strides)
+        if nseq > 0 and total > 0 and max_seqlen_q > 0:
+            _lib.call("tg_keybias_varlen_bwd", dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                      out.data_ptr(), softmax_lse.data_ptr(), bias.data_ptr() if bias is not None else None,
+                      dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                      dbias.data_ptr() if dbias is not None else None, softmax_d.data_ptr(),
+                      cu_seqlens_q.data_ptr(), nseq, int(max_seqlen_q), total, H, Hkv, D,
+                      ctypes.cast(arr, ctypes.c_void_p), float(softmax_scale), int(bool(is_causal)), _stream(q))
+        return [dq, dk, dv, softmax_d, dbias]
