@@ -97,6 +97,57 @@ int tg_keybias_varlen_bwd(const void *dout, const void *q, const void *k, const 
                           int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
                           const int64_t *strides, float softmax_scale, int32_t causal, hipStream_t stream);
 
+/* ---- gate path (tokengate/e2e_gate/gate_module/gate_forward.py:1384-1522) ---------------- */
+
+/* Scoring head over packed rows: scores[r] = w2 . silu(W1 x_r + b1) + b2, fp32.
+ * x (n_rows, d_in) bf16 with row stride x_row_stride (elements), W1 (d_hidden, d_in) bf16
+ * row-major (nn.Linear weight), b1 / w2 fp32 (d_hidden).  d_in = 2048, d_hidden = 256 (the
+ * Linear(2048->256) -> SiLU -> Linear(256->1) head).  Stands in for the gate-layer scoring that
+ * feeds the selection (gate_branch_hs / E2EGate.forward, gate_forward.py:491-524,
+ * e2e_gate_module.py:348-385). */
+int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in,
+                      int32_t d_hidden, const void *w1, const float *b1, const float *w2, float b2,
+                      float *scores, hipStream_t stream);
+
+/* Order-preserving top-K keep lists, one per sequence (gate_forward.py:1396-1421, _keep_indices
+ * :77-81, torch.topk via _select_topk_or_random :84-99).
+ * geom: device int32 (num_seqs, 6) rows [row_start, seq_len, art_start, art_end, k_clamped,
+ * kept_start]: the sequence's scores are scores[row_start + i], 0 <= i < seq_len; its state span
+ * (article) is [art_start, art_end); k_clamped = max(1, min(K, art_end - art_start)) (0 for an
+ * empty article); its keep list goes to keep[kept_start ...]: 0..art_start-1, then the article
+ * positions of the k_clamped largest scores in ascending position order, then art_end..seq_len-1.
+ * Ties at the threshold go to the lower position; -0.0 equals +0.0; NaN ranks above +inf.
+ * sumsq (optional, device fp32 per sequence) receives the sum of squared article scores.
+ * max_article_len: the largest art_end - art_start (selects the LDS-resident variant). */
+int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32_t num_seqs,
+                      int32_t max_article_len, int64_t *keep, float *sumsq, hipStream_t stream);
+
+/* One row stream of the pack: source row r starts at src + r * src_row_stride and consists of
+ * n_chunks chunks of chunk_bytes, src_chunk_stride apart (1 chunk for a (rows, ...) contiguous
+ * row; Hkv chunks for a head-major cache); destination row j is the chunks back to back at
+ * dst + j * dst_row_stride.  Byte units; everything 16-byte aligned. */
+typedef struct tg_pack_stream {
+  const void *src;
+  void *dst;
+  int64_t src_row_stride;
+  int64_t dst_row_stride;
+  int64_t src_chunk_stride;
+  int32_t chunk_bytes;
+  int32_t n_chunks;
+} tg_pack_stream;
+
+/* Ragged gather of the kept rows (gate_forward.py:1454-1522: hs_pruned, kept_positions,
+ * gate_bias_batched, the below-gate KV index_select), packed back to back in keep order
+ * (cu_seqlens layout: sequence b's rows start at geom[b].kept_start).  For kept row j of
+ * sequence b, every stream copies source row geom[b].row_start + keep[j] to destination row j;
+ * positions_out[j] = keep[j] (int64, optional); bias_out[j] (optional) = the kept row's score
+ * bias_src[row_start + keep[j]] scaled by rsqrt(sumsq[b] / n_art + rms_eps) when sumsq is given,
+ * on article rows, and 0 on prefix / suffix rows.  At most 16 streams. */
+int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep,
+                 const int32_t *geom, int32_t num_seqs, int64_t total_kept, int64_t *positions_out,
+                 const float *bias_src, const float *sumsq, float rms_eps, float *bias_out,
+                 hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

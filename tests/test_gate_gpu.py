@@ -1,0 +1,169 @@
+"""GPU parity of the gate path: keep lists and packed rows bit-exact against the oracle on the same
+score tensor; the scoring head within tolerance of a float64 evaluation.
+
+Covers the reference's selection semantics (gate_forward.py:1409-1421): K_c = max(1, min(K, n_art)),
+K >= n_art keeps everything, prefix/suffix always kept, ascending order; ties (bf16-rounded scores
+make them common) go to the lower position; NaN and signed zeros; ragged batches; articles longer
+than the LDS-resident limit; and the 32k scoring + pruning workload (hidden [1, 32768, 2048], state
+span 64..32511, K in {100, 500, 2000}, two layers of K/V [8 heads, 128]).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gate as og
+from tests.attn_util import assert_close, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_select(scores_np, seqs, dev):
+    from tokengate_amd import gate
+    scores = torch.tensor(scores_np, dtype=torch.float32, device=dev)
+    p = gate.plan([s[0] for s in seqs], [s[1] for s in seqs], [s[2] for s in seqs], [s[3] for s in seqs],
+                  [s[4] for s in seqs], dev)
+    keep, sumsq = gate.select_keep(scores, p)
+    torch.cuda.synchronize()
+    return keep.cpu().numpy(), sumsq.cpu().numpy(), p
+
+
+def _check_select(scores_np, seqs, dev):
+    keep, sumsq, p = _run_select(scores_np, seqs, dev)
+    ref, starts, kcs = og.select_and_pack(scores_np.astype(np.float64), seqs)
+    assert p.k_clamped == kcs and p.cu_kept[:-1] == starts
+    assert keep.dtype == np.int64 and np.array_equal(keep, ref)
+    for b, (r0, L, s, e, K) in enumerate(seqs):
+        art = scores_np[r0 + s:r0 + e].astype(np.float64)
+        art = art[np.isfinite(art)] if not np.isfinite(scores_np).all() else art
+        if len(art) and np.isfinite(scores_np[r0 + s:r0 + e]).all():
+            np.testing.assert_allclose(sumsq[b], np.sum(art * art), rtol=1e-4)
+    return keep, p
+
+
+def test_random_ragged_batch(cuda):
+    rng = np.random.default_rng(0)
+    seqs, r0 = [], 0
+    for L, s, e, K in [(5000, 64, 4744, 100), (300, 0, 300, 10_000_000), (1, 0, 1, 5), (2000, 10, 1990, 0),
+                       (777, 700, 700, 9), (4096, 64, 3840, 2000), (64, 3, 60, 57)]:
+        seqs.append((r0, L, s, e, K))
+        r0 += L
+    scores = rng.standard_normal(r0).astype(np.float32)
+    _check_select(scores, seqs, cuda)
+    # bf16-rounded scores: many exact ties at the threshold
+    scores_bf = torch.from_numpy(scores).to(torch.bfloat16).float().numpy()
+    _check_select(scores_bf, seqs, cuda)
+
+
+@pytest.mark.parametrize("kind", ["all_equal", "few_values", "nan_and_zeros", "steps"])
+def test_heavy_ties(cuda, kind):
+    rng = np.random.default_rng(1)
+    n = 10_000
+    if kind == "all_equal":
+        s = np.full(n, 0.5, np.float32)
+    elif kind == "few_values":
+        s = rng.integers(0, 4, n).astype(np.float32)
+    elif kind == "nan_and_zeros":
+        s = rng.choice(np.array([0.0, -0.0, 1.0, -1.0, np.nan], np.float32), n)
+    else:
+        s = np.repeat(np.arange(100, dtype=np.float32), 100)[rng.permutation(n)]
+    seqs = [(0, n, 7, n - 3, K) for K in (1,)]
+    for K in (1, 2, 17, 1000, 4999, 9989, 9990, 20000):
+        _check_select(s, [(0, n, 7, n - 3, K)], cuda)
+
+
+def test_long_article_global_path(cuda):
+    """Articles longer than the LDS-resident limit (32768 keys) take the global-memory variant."""
+    rng = np.random.default_rng(2)
+    L = 100_000
+    s = torch.from_numpy(rng.standard_normal(2 * L).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    seqs = [(0, L, 64, L - 256, 4000), (L, L, 0, L, 50_000)]
+    _check_select(s, seqs, cuda)
+
+
+def test_single_sequence_helper(cuda):
+    from tokengate_amd import gate
+    rng = np.random.default_rng(3)
+    art = rng.standard_normal(500).astype(np.float32)
+    kp = gate.keep_indices(torch.from_numpy(art).to(cuda), 40, 12, 512, 600).cpu().numpy()
+    assert np.array_equal(kp, og.keep_indices(art, 40, 12, 512, 600))
+
+
+def test_pack_bit_exact_row_and_head_major(cuda):
+    from tokengate_amd import gate
+    rng = np.random.default_rng(4)
+    g = torch.Generator(device=cuda).manual_seed(4)
+    seqs, r0 = [], 0
+    for L, s, e, K in [(1000, 16, 900, 50), (333, 0, 333, 333), (2048, 64, 1792, 700)]:
+        seqs.append((r0, L, s, e, K))
+        r0 += L
+    total = r0
+    scores = torch.from_numpy(rng.standard_normal(total).astype(np.float32)).to(cuda)
+    p = gate.plan([x[0] for x in seqs], [x[1] for x in seqs], [x[2] for x in seqs], [x[3] for x in seqs],
+                  [x[4] for x in seqs], cuda)
+    keep, sumsq = gate.select_keep(scores, p)
+    hidden = torch.randn(total, 2048, generator=g, device=cuda).to(torch.bfloat16)
+    k_rows = torch.randn(total, 8, 128, generator=g, device=cuda).to(torch.bfloat16)
+    v_head_major = torch.randn(8, total, 128, generator=g, device=cuda).to(torch.bfloat16)   # (Hkv, S, D)
+    T = p.total_kept
+    hs_out = torch.empty(T, 2048, dtype=torch.bfloat16, device=cuda)
+    k_out = torch.empty(T, 8, 128, dtype=torch.bfloat16, device=cuda)
+    v_out = torch.empty(T, 8, 128, dtype=torch.bfloat16, device=cuda)
+    pos = torch.empty(T, dtype=torch.int64, device=cuda)
+    bias = torch.empty(T, dtype=torch.float32, device=cuda)
+    gate.pack(keep, p, [(hidden, hs_out), (k_rows, k_out), (v_head_major.transpose(0, 1), v_out)],
+              positions=pos, bias_src=scores, sumsq=sumsq, bias_out=bias)
+    torch.cuda.synchronize()
+    src_rows = np.concatenate([x[0] + keep.cpu().numpy()[p.cu_kept[b]:p.cu_kept[b + 1]] for b, x in enumerate(seqs)])
+    idx = torch.from_numpy(src_rows).to(cuda)
+    assert torch.equal(hs_out, hidden.index_select(0, idx))
+    assert torch.equal(k_out, k_rows.index_select(0, idx))
+    assert torch.equal(v_out, v_head_major.index_select(1, idx).transpose(0, 1))
+    assert torch.equal(pos.cpu(), keep.cpu())
+    sc = scores.cpu().numpy().astype(np.float64)
+    ref_bias = np.concatenate([og.gate_bias(sc[x[0] + x[2]:x[0] + x[3]], keep.cpu().numpy()[p.cu_kept[b]:p.cu_kept[b + 1]],
+                                            x[2], x[3]) for b, x in enumerate(seqs)])
+    assert_close("pack bias", to_np(bias), ref_bias, max_abs=1e-5, rel_l2=1e-6)
+
+
+def _xavier(shape, g, dev):
+    fan_out, fan_in = shape
+    a = math.sqrt(6.0 / (fan_in + fan_out))
+    return (torch.rand(shape, generator=g, device=dev) * 2 - 1) * a
+
+
+@pytest.mark.parametrize("K", [100, 500, 2000])
+def test_config_scoring_and_pruning_32k(cuda, K):
+    from tokengate_amd import gate
+    S, d, s, e = 32768, 2048, 64, 32512
+    g = torch.Generator(device=cuda).manual_seed(5)
+    hidden = torch.randn(1, S, d, generator=g, device=cuda).to(torch.bfloat16)
+    w1 = _xavier((256, d), g, cuda).to(torch.bfloat16)
+    w2 = _xavier((1, 256), g, cuda)[0].contiguous()
+    b1 = torch.zeros(256, device=cuda)
+    x = hidden[0]
+    scores = gate.score_mlp(x, w1, b1, w2, 0.0)
+    torch.cuda.synchronize()
+    ref = og.score_mlp(to_np(x[s:e]), to_np(w1), np.zeros(256), to_np(w2), 0.0)
+    assert_close(f"scores K={K}", to_np(scores[s:e]), ref, max_abs=2e-3, rel_l2=1e-4)
+    # selection and pack on the kernel's own score tensor, bit-exact
+    p = gate.plan([0], [S], [s], [e], [K], cuda)
+    keep, sumsq = gate.select_keep(scores, p)
+    kv = [torch.randn(S, 8, 128, generator=g, device=cuda).to(torch.bfloat16) for _ in range(4)]   # K,V x 2 layers
+    T = p.total_kept
+    assert T == s + K + (S - e)
+    outs = [torch.empty(T, 2048, dtype=torch.bfloat16, device=cuda)] + \
+           [torch.empty(T, 8, 128, dtype=torch.bfloat16, device=cuda) for _ in kv]
+    pos = torch.empty(T, dtype=torch.int64, device=cuda)
+    bias = torch.empty(T, dtype=torch.float32, device=cuda)
+    gate.pack(keep, p, list(zip([x] + kv, outs)), positions=pos, bias_src=scores, sumsq=sumsq, bias_out=bias)
+    torch.cuda.synchronize()
+    ref_keep = og.keep_indices(scores.cpu().numpy()[s:e], K, s, e, S)
+    assert np.array_equal(keep.cpu().numpy(), ref_keep)
+    idx = torch.from_numpy(ref_keep).to(cuda)
+    for src, out in zip([x] + kv, outs):
+        assert torch.equal(out, src.index_select(0, idx))
+    assert np.array_equal(pos.cpu().numpy(), ref_keep)
+    ref_bias = og.gate_bias(scores.cpu().numpy()[s:e].astype(np.float64), ref_keep, s, e)
+    assert_close("bias", to_np(bias), ref_bias, max_abs=1e-5, rel_l2=1e-6)

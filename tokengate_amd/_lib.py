@@ -29,6 +29,9 @@ SIGNATURES = {
                               i64, i64, f32, i32, vp],
     "tg_keybias_bwd": [vp] * 12 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_keybias_varlen_bwd": [vp] * 13 + [i32] * 6 + [vp, f32, i32, vp],
+    "tg_gate_score_mlp": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
+    "tg_gate_topk_keep": [vp, vp, i32, i32, vp, vp, vp],
+    "tg_gate_pack": [vp, i32, vp, vp, i32, i64, vp, vp, vp, f32, vp, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p}
 
