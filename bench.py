@@ -13,7 +13,9 @@ Prints ONE JSON line with the bench contract fields plus:
                  counter summary when present;
   cpu_baseline — the oracle (float32 numpy, all host cores through BLAS) on a bounded sample of
                  the same workload: the last query rows of every head, full causal key range;
-  extra        — secondary measurements (the 4k shape).
+  extra        — secondary measurements: the 4k forward, the B4 x 8192 backward (TFLOP/s of
+                 5*B*H*D*S*(S+1)), and the 32k gate path (scoring, top-K, pack; the short gate
+                 launches are timed as replays of a captured HIP graph).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
 """
@@ -72,6 +74,139 @@ def time_fwd(q, k, v, bias_raw, scale, steps, warmup):
     t1 = time.perf_counter()
     kern_ms = sum(a.elapsed_time(b) for a, b in ev) / steps
     return (t1 - t0) * 1e3 / steps, kern_ms
+
+
+def time_events(fn, iters, warmup=3):
+    """Mean milliseconds of fn() between HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(iters):
+        fn()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def time_graph(fn, iters=20, reps=5):
+    """Mean milliseconds of fn() with `iters` calls captured in one HIP graph and replayed `reps`
+    times: the device time of short launches without the host's launch latency."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(reps):
+        graph.replay()
+    b.record(st)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / (iters * reps)
+
+
+def bench_bwd(dev, iters=5):
+    """Backward at B=4, S=8192, 16/8 heads (preprocess + dQ + dK/dV/dBias launches)."""
+    import torch
+    from tokengate_amd.fa2bias.keybias import ext
+    B, S, H, Hkv = 4, 8192, 16, 8
+    g = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(B, S, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, S, Hkv, 128, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, S, Hkv, 128, generator=g, device=dev).to(torch.bfloat16)
+    kb = torch.nn.functional.logsigmoid(torch.randn(B, S, generator=g, device=dev) * 2.0)
+    scale = 128 ** -0.5
+    bias_raw = (kb[:, None, :].expand(B, H, S) / scale).contiguous()
+    dout = torch.randn(B, S, H, 128, generator=g, device=dev).to(torch.bfloat16)
+    out, lse, _, _ = ext().fwd(q, k, v, None, bias_raw, 0.0, scale, True, -1, -1, 0.0, False, None)
+    ms = time_events(lambda: ext().bwd(dout, q, k, v, out, lse, None, None, None, bias_raw, 0.0, scale, True,
+                                       -1, -1, 0.0, False, None, None), iters, warmup=2)
+    flops = 5.0 * B * H * 128 * S * (S + 1)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "tflops": round(tf, 2), "frac_mfma": round(tf / PEAK_BF16_TFLOPS, 4),
+            "flop": flops, "shape": "B4 S8192 H16/8 D128 causal, bias [4,8192] broadcast"}
+
+
+def bench_gate(dev, iters=50):
+    """Scoring + top-K + pack on the 32k gate workload: hidden [1,32768,2048], state span 64..32511,
+    synthetic head Linear(2048->256)->SiLU->Linear(256->1) (Xavier, seed 5), K/V of 2 layers."""
+    import torch
+    from tokengate_amd import gate
+    S, d, s, e = 32768, 2048, 64, 32512
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(S, d, generator=g, device=dev).to(torch.bfloat16)
+    a1 = math.sqrt(6.0 / (d + 256))
+    w1 = ((torch.rand(256, d, generator=g, device=dev) * 2 - 1) * a1).to(torch.bfloat16)
+    w2 = (torch.rand(256, generator=g, device=dev) * 2 - 1) * math.sqrt(6.0 / 257)
+    b1 = torch.zeros(256, device=dev)
+    kv = [torch.randn(S, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    scores = torch.empty(S, dtype=torch.float32, device=dev)
+    n_art = e - s
+    ms_score = time_graph(lambda: gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e]))
+    score_bytes = n_art * d * 2 + w1.numel() * 2 + n_art * 4
+    score_flop = 2.0 * n_art * d * 256
+    res = {"score": {"ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
+                     "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                     "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1), "rows": n_art}}
+    for K in (100, 500, 2000):
+        p = gate.plan([0], [S], [s], [e], [K], dev)
+        T = p.total_kept
+        outs = [torch.empty(T, d, dtype=torch.bfloat16, device=dev)] + \
+               [torch.empty(T, 8, 128, dtype=torch.bfloat16, device=dev) for _ in kv]
+        pos = torch.empty(T, dtype=torch.int64, device=dev)
+        bias = torch.empty(T, dtype=torch.float32, device=dev)
+        keep = torch.empty(T, dtype=torch.int64, device=dev)
+        ss = torch.empty(1, dtype=torch.float32, device=dev)
+        pairs = list(zip([x] + kv, outs))
+        ms_topk = time_graph(lambda: gate.select_keep(scores, p, keep_out=keep, sumsq_out=ss))
+        ms_pack = time_graph(lambda: gate.pack(keep, p, pairs, positions=pos, bias_src=scores, sumsq=ss,
+                                               bias_out=bias))
+        pack_bytes = 2 * T * (d * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4)
+        topk_bytes = n_art * 4 + T * 8
+        both = (pack_bytes + topk_bytes) / ((ms_topk + ms_pack) * 1e-3) / 1e9
+        res[f"K{K}"] = {"kept": T, "topk_ms": round(ms_topk, 4), "pack_ms": round(ms_pack, 4),
+                        "pack_gbs": round(pack_bytes / (ms_pack * 1e-3) / 1e9, 1),
+                        "pack_frac_hbm": round(pack_bytes / (ms_pack * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "topk_plus_pack_gbs": round(both, 1),
+                        "topk_plus_pack_frac_hbm": round(both / PEAK_HBM_GBS, 4),
+                        "bytes": pack_bytes + topk_bytes}
+    return res
+
+
+def cpu_prune_baseline(seconds=3.0):
+    """The oracle's top-K + keep + gathers (numpy, host cores) at the 32k gate workload, K=2000:
+    topk order, sort, keep list, hidden + 2 layers' K/V row gathers."""
+    import numpy as np
+    from oracle import gate as og
+    rng = np.random.default_rng(0)
+    S, s, e, K = 32768, 64, 32512, 2000
+    sc = rng.standard_normal(e - s).astype(np.float32)
+    hid = rng.standard_normal((S, 2048)).astype(np.float16)       # 2-byte rows like bf16
+    kvs = [rng.standard_normal((S, 8, 128)).astype(np.float16) for _ in range(4)]
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        kp = og.keep_indices(sc, K, s, e, S)
+        _ = hid[kp]
+        for t in kvs:
+            _ = t[kp]
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"ms": round(dt * 1e3, 3), "cores": 1, "kind": "port",
+            "sample": "oracle numpy top-K + keep + gathers of hidden and 2 layers of K/V, 32k / K=2000"}
 
 
 def cpu_baseline(q, k, v, bias_raw, scale, seconds):
@@ -146,6 +281,11 @@ def main():
         _, k1ms = time_fwd(q1, k1, v1, b1, s1, 20, 5)
         extra["fwd_4k_tflops"] = round(causal_flops(1, H, 4096) / (k1ms * 1e-3) / 1e12, 2)
         extra["fwd_4k_kernel_ms"] = round(k1ms, 4)
+        del q1, k1, v1, b1
+        extra["bwd_8k_b4"] = bench_bwd(dev)
+        extra["gate_32k"] = bench_gate(dev)
+        if args.cpu_seconds > 0:
+            extra["gate_32k"]["cpu_prune_baseline"] = cpu_prune_baseline()
 
     cpu = cpu_baseline(q, k, v, bias_raw, scale, args.cpu_seconds) if args.cpu_seconds > 0 else None
     line = {

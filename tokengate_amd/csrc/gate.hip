@@ -14,10 +14,11 @@
 // Kernels:
 //   gate_score_kernel  — s = w2 . silu(W1 x + b1) + b2 for every row of a packed (rows, 2048)
 //                        bf16 matrix (128 rows per workgroup; W1 x on bf16 MFMA, fp32 epilogue);
-//   gate_topk_kernel   — one workgroup per sequence: order-preserving uint32 keys, 4-pass 8-bit
-//                        radix select of the K_c-th largest key (keys LDS-resident when the article
-//                        fits, 32768 keys), then an index-order compaction (block scans) that keeps
-//                        keys above the threshold and the lowest-index ties, writing ascending
+//   gate_topk_*kernel  — one workgroup per sequence: order-preserving uint32 keys, 4-pass 8-bit
+//                        radix select of the K_c-th largest key (keys held in registers for
+//                        articles up to 65536 tokens, else re-read from global memory), then an
+//                        index-order compaction (ballot ranks over 64-key blocks) that keeps keys
+//                        above the threshold and the lowest-index ties, writing ascending
 //                        positions; also the article's sum of squared scores;
 //   gate_pack_kernel   — one launch gathers every kept row for any number of row streams (hidden
 //                        states, per-layer K and V, head-chunked rows) in 16-byte units, plus the
@@ -135,41 +136,18 @@ constexpr int kTThreads = 1024;
 constexpr int kTWaves = kTThreads / 64;
 constexpr int kTLdsKeys = 32768;
 
-// float -> uint32 whose unsigned order is the float order; -0 == +0; NaN above +inf.
+// float -> uint32 whose unsigned order is the float order; -0 == +0; NaN above +inf.  Branch-free
+// (selects only) so that it can run over register-resident key arrays.
 __device__ __forceinline__ uint32_t order_key(float f) {
-  if (f != f) return 0xffffffffu;
-  if (f == 0.f) f = 0.f;
   const uint32_t u = __builtin_bit_cast(uint32_t, f);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  k = (f == 0.f) ? 0x80000000u : k;
+  k = (f != f) ? 0xffffffffu : k;
+  return k;
 }
 
-// Block-wide exclusive scan of one int per thread; returns the exclusive prefix, total in *tot.
-__device__ int block_exclusive_scan(int x, int *scratch, int *tot) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int incl = x;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o);
-    if (lane >= o) incl += y;
-  }
-  if (lane == 63) scratch[wave] = incl;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < kTWaves ? scratch[lane] : 0;
-    int wi = w;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(wi, o);
-      if (lane >= o) wi += y;
-    }
-    if (lane < kTWaves) scratch[32 + lane] = wi - w;
-    if (lane == kTWaves - 1) scratch[64] = wi;
-  }
-  __syncthreads();
-  const int res = scratch[32 + wave] + incl - x;
-  *tot = scratch[64];
-  __syncthreads();
-  return res;
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
 template <bool IN_LDS>
@@ -178,8 +156,8 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *sc
   __shared__ uint32_t keys_lds[IN_LDS ? kTLdsKeys : 1];
   __shared__ int hist[kTWaves][256];
   __shared__ int htot[256];
-  __shared__ int scratch[96];
-  __shared__ uint32_t sel[4];   // prefix, k_rem
+  __shared__ int wgt[kTWaves], weq[kTWaves];
+  __shared__ uint32_t sel[2];   // prefix, k_rem
   __shared__ float red[kTWaves];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -198,18 +176,30 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *sc
     return;
   }
 
-  // keys (and the article's sum of squares)
+  // keys (LDS-resident when they fit) and the article's sum of squares.  The LDS variant issues
+  // every score load as LDS DMA at once (n / 1024 per thread in flight), then converts in place.
   float ss = 0.f;
   if constexpr (IN_LDS) {
+    const brsrc_t srs = make_rsrc(sc, (uint32_t)n * 4u);
+    for (int base = 0; base < n; base += kTThreads)
+      dma4(srs, &keys_lds[base + 64 * wave], (uint32_t)(base + tid) * 4u);
+    wait_all_mem();
+    __syncthreads();
     for (int i = tid; i < n; i += kTThreads) {
-      const float f = sc[i];
+      const float f = __builtin_bit_cast(float, keys_lds[i]);
       ss = fmaf(f, f, ss);
       keys_lds[i] = order_key(f);
     }
   } else {
-    for (int i = tid; i < n; i += kTThreads) {
-      const float f = sc[i];
-      ss = fmaf(f, f, ss);
+    for (int base = 0; base < n; base += 8 * kTThreads) {
+      float f[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int i = base + k * kTThreads + tid;
+        f[k] = i < n ? sc[i] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ss = fmaf(f[k], f[k], ss);
     }
   }
   auto key_at = [&](int i) -> uint32_t {
@@ -227,15 +217,32 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *sc
     sumsq[blockIdx.x] = t;
   }
 
-  // radix select of the kc-th largest key, 8 bits per pass from the top
+  // Radix select of the kc-th largest key, 8 bits per pass from the top.  The first digit (sign
+  // and high exponent bits) is concentrated on a few values, so its counts are aggregated per
+  // wave (one LDS atomic per distinct digit in the wave) instead of one atomic per key.
   uint32_t mask = 0u;
   for (int shift = 24; shift >= 0; shift -= 8) {
     for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
     __syncthreads();
     const uint32_t prefix = sel[0];
-    for (int i = tid; i < n; i += kTThreads) {
-      const uint32_t u = key_at(i);
-      if ((u & mask) == prefix) atomicAdd(&hist[wave][(u >> shift) & 255u], 1);
+    for (int base = 0; base < n; base += kTThreads) {
+      const int i = base + tid;
+      const uint32_t u = i < n ? key_at(i) : 0u;
+      bool active = i < n && (u & mask) == prefix;
+      const uint32_t d = (u >> shift) & 255u;
+      if (shift == 24) {
+        uint64_t act = __builtin_amdgcn_ballot_w64(active);
+        while (act) {
+          const int leader = __builtin_ctzll(act);
+          const uint32_t ld = __shfl(d, leader);
+          const uint64_t same = __builtin_amdgcn_ballot_w64(active && d == ld);
+          if (lane == leader) hist[wave][ld] += __builtin_popcountll(same);
+          act &= ~same;
+          active = active && d != ld;
+        }
+      } else if (active) {
+        atomicAdd(&hist[wave][d], 1);
+      }
     }
     __syncthreads();
     if (tid < 256) {
@@ -272,30 +279,210 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *sc
     __syncthreads();
   }
   const uint32_t T = sel[0];
-  const int k_eq = (int)sel[1];   // ties at T to keep (lowest indices first)
+  const int k_eq = (int)sel[1];   // ties at T to keep, lowest positions first
 
-  // index-order compaction: each thread owns a contiguous segment
-  const int seg = (n + kTThreads - 1) / kTThreads;
-  const int i0 = min(n, tid * seg), i1 = min(n, i0 + seg);
-  int n_eq = 0;
-  for (int i = i0; i < i1; ++i) n_eq += key_at(i) == T;
-  int tot;
-  const int eq_before = block_exclusive_scan(n_eq, scratch, &tot);
-  int n_keep = 0, r = eq_before;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t u = key_at(i);
-    if (u > T) ++n_keep;
-    else if (u == T) { n_keep += r < k_eq; ++r; }
+  // Index-order compaction: wave w owns the contiguous chunk [w*C, (w+1)*C), read 64 consecutive
+  // keys at a time; ballots rank the ties and place the kept positions.
+  const int C = ((n + kTWaves - 1) / kTWaves + 63) / 64 * 64;
+  const int c0 = min(n, wave * C), c1 = min(n, c0 + C);
+  int n_gt = 0, n_eq = 0;
+  for (int base = c0; base < c1; base += 64) {
+    const int i = base + lane;
+    const uint32_t u = i < c1 ? key_at(i) : 0u;   // 0 is below every key order_key produces
+    n_gt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < c1 && u > T));
+    n_eq += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < c1 && u == T));
   }
-  const int pos0 = block_exclusive_scan(n_keep, scratch, &tot);
+  if (lane == 0) { wgt[wave] = n_gt; weq[wave] = n_eq; }
+  __syncthreads();
+  int eq_before = 0, keep_before = 0;
+  for (int w = 0; w < wave; ++w) {
+    const int te = min(weq[w], max(0, k_eq - eq_before));
+    keep_before += wgt[w] + te;
+    eq_before += weq[w];
+  }
   int64_t *out = keep + kept0 + s;
-  int p = pos0;
-  r = eq_before;
-  for (int i = i0; i < i1; ++i) {
-    const uint32_t u = key_at(i);
-    bool take = u > T;
-    if (u == T) { take = r < k_eq; ++r; }
-    if (take) out[p++] = s + i;
+  int run_eq = eq_before, run_keep = keep_before;
+  for (int base = c0; base < c1; base += 64) {
+    const int i = base + lane;
+    const uint32_t u = i < c1 ? key_at(i) : 0u;
+    const bool valid = i < c1;
+    const bool eq = valid && u == T;
+    const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+    const bool take = valid && (u > T || (eq && run_eq + lanes_below(eqm) < k_eq));
+    const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
+    if (take) out[run_keep + lanes_below(tm)] = s + i;
+    run_eq += __builtin_popcountll(eqm);
+    run_keep += __builtin_popcountll(tm);
+  }
+}
+
+// Register-resident variant for articles of at most 1024 * KPT tokens: thread t holds keys
+// t, t + 1024, ... (KPT of them), so every pass is register arithmetic plus LDS histogram
+// updates, and the index-order compaction works on 64-key blocks (block b = round r, wave w covers
+// positions 1024 r + 64 w .. +63) whose counts are scanned by one wave.
+template <int KPT>
+__global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float *scores, const int32_t *geom,
+                                                                     int64_t *keep, float *sumsq) {
+  constexpr int NB = KPT * kTWaves;    // 64-key blocks
+  __shared__ int hist[2][kTWaves][256];   // double-buffered: the next pass's copy is cleared early
+  __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
+  __shared__ uint32_t sel[4];             // lo, hi, k_rem
+  __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
+  __shared__ float red[kTWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t *gm = geom + 6 * blockIdx.x;
+  const int64_t row_start = gm[0];
+  const int seq_len = gm[1], s = gm[2], e = gm[3], kc = gm[4];
+  const int64_t kept0 = gm[5];
+  const int n = e - s;
+  const float *sc = scores + row_start + s;
+
+  // keys in registers (all loads in flight); 0 marks a position past the article
+  const brsrc_t srs = make_rsrc(sc, n > 0 ? (uint32_t)n * 4u : 0u);
+  uint32_t key[KPT];
+#pragma unroll
+  for (int r = 0; r < KPT; ++r)
+    key[r] = __builtin_amdgcn_raw_buffer_load_b32(srs, (uint32_t)(r * kTThreads + tid) * 4u, 0, 0);
+
+  for (int i = tid; i < s; i += kTThreads) keep[kept0 + i] = i;
+  for (int i = tid; i < seq_len - e; i += kTThreads) keep[kept0 + s + kc + i] = e + i;
+  if (n <= 0 || kc <= 0) {
+    if (tid == 0 && sumsq) sumsq[blockIdx.x] = 0.f;
+    return;
+  }
+  for (int i = lane; i < 256; i += 64) hist[0][wave][i] = 0;
+
+  float ss = 0.f;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) {
+    const bool valid = r * kTThreads + tid < n;
+    const float f = __builtin_bit_cast(float, key[r]);
+    ss = valid ? fmaf(f, f, ss) : ss;
+    key[r] = valid ? order_key(f) : 0u;
+    kmin = min(kmin, valid ? key[r] : 0xffffffffu);
+    kmax = max(kmax, key[r]);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o);
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+  }
+  if (lane == 0) { red[wave] = ss; wmin[wave] = kmin; wmax[wave] = kmax; }
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int w = 0; w < kTWaves; ++w) { t += red[w]; lo = min(lo, wmin[w]); hi = max(hi, wmax[w]); }
+    if (sumsq) sumsq[blockIdx.x] = t;
+    sel[0] = lo; sel[1] = hi; sel[2] = (uint32_t)kc;
+  }
+  __syncthreads();
+
+  // Radix select of the kc-th largest key over the occupied key range [lo, hi]: each pass splits
+  // the current range into at most 256 power-of-two-wide bins.  Windowing the first pass to the
+  // data's own range spreads typical scores over many bins (a fixed top-byte digit would put
+  // most of them into a handful).
+  int pb = 0;
+  while (true) {
+    const uint32_t lo = sel[0], hi = sel[1];
+    if (lo == hi) break;                             // block-uniform
+    const uint32_t span = hi - lo;
+    const int shift = span < 256u ? 0 : 32 - __builtin_clz(span >> 8);   // span >> shift < 256
+    for (int i = lane; i < 256; i += 64) hist[pb ^ 1][wave][i] = 0;     // next pass's copy
+#pragma unroll
+    for (int r = 0; r < KPT; ++r) {
+      const uint32_t u = key[r];
+      if (u != 0u && u >= lo && u <= hi) atomicAdd(&hist[pb][wave][(u - lo) >> shift], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // lane l owns bins 255-4l .. 252-4l (descending); totals over the 16 wave histograms
+      int c[4], lt = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kTWaves; ++w) t += hist[pb][w][255 - 4 * lane - j];
+        c[j] = t;
+        lt += t;
+      }
+      int incl = lt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const int before = incl - lt;
+      const int krem = (int)sel[2];
+      if (before < krem && krem <= incl) {
+        int acc = before, d = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; break; }
+          acc += c[j];
+        }
+        const uint32_t nlo = lo + ((uint32_t)d << shift);
+        const uint32_t nhi_raw = nlo + ((1u << shift) - 1u);
+        sel[0] = nlo;
+        sel[1] = (nhi_raw < nlo || nhi_raw > hi) ? hi : nhi_raw;
+        sel[2] = (uint32_t)(krem - acc);
+      }
+    }
+    __syncthreads();
+    pb ^= 1;
+  }
+  const uint32_t T = sel[0];
+  const int k_eq = (int)sel[2];
+
+  // per-block counts (block r*16 + w covers positions 1024 r + 64 w .. + 63: index order)
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) {
+    const uint64_t gtm = __builtin_amdgcn_ballot_w64(key[r] > T);
+    const uint64_t eqm = __builtin_amdgcn_ballot_w64(key[r] == T);
+    if (lane == 0) { bgt[r * kTWaves + wave] = (int)__builtin_popcountll(gtm); beq[r * kTWaves + wave] = (int)__builtin_popcountll(eqm); }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    constexpr int PER = NB / 64;   // consecutive blocks per lane
+    int eqv[PER], gtv[PER], ge = 0, gk = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { eqv[j] = beq[lane * PER + j]; gtv[j] = bgt[lane * PER + j]; ge += eqv[j]; }
+    int ie = ge;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) { const int y = __shfl_up(ie, o); if (lane >= o) ie += y; }
+    int eb = ie - ge;
+    int kl[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int te = min(eqv[j], max(0, k_eq - eb));
+      beq0[lane * PER + j] = eb;
+      eb += eqv[j];
+      kl[j] = gtv[j] + te;
+      gk += kl[j];
+    }
+    int ik = gk;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) { const int y = __shfl_up(ik, o); if (lane >= o) ik += y; }
+    int kb = ik - gk;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) { bkeep0[lane * PER + j] = kb; kb += kl[j]; }
+  }
+  __syncthreads();
+  int e0[KPT], k0[KPT];
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) { e0[r] = beq0[r * kTWaves + wave]; k0[r] = bkeep0[r * kTWaves + wave]; }
+  int64_t *out = keep + kept0 + s;
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) {
+    const uint32_t u = key[r];
+    const bool eq = u == T;
+    const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+    const bool take = u > T || (eq && e0[r] + lanes_below(eqm) < k_eq);
+    const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
+    if (take) out[k0[r] + lanes_below(tm)] = s + r * kTThreads + tid;
   }
 }
 
@@ -304,7 +491,7 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *sc
 // row_start[b] + keep[j] of every stream and writes destination row j.
 // ---------------------------------------------------------------------------------------------
 constexpr int kPThreads = 256;
-constexpr int kPRows = 8;     // kept rows per workgroup
+constexpr int kPRows = 4;     // kept rows per workgroup
 constexpr int kMaxStreams = 16;
 
 struct PackArgs {
@@ -358,16 +545,31 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
     const tg_pack_stream st = a.st[si];
     const int units_per_chunk = st.chunk_bytes >> 4;
     const int units = units_per_chunk * st.n_chunks;
-    for (int w = tid; w < units * kPRows; w += kPThreads) {
-      const int rr = w / units, u = w % units;
-      const int64_t srow = src_row[rr];
-      if (srow < 0) continue;
-      const int ch = u / units_per_chunk, cu = u % units_per_chunk;
-      const char *src = static_cast<const char *>(st.src) + srow * st.src_row_stride +
-                        (int64_t)ch * st.src_chunk_stride + 16 * cu;
-      char *dst = static_cast<char *>(st.dst) + (j0 + rr) * st.dst_row_stride +
-                  (int64_t)ch * st.chunk_bytes + 16 * cu;
-      *reinterpret_cast<u32x4 *>(dst) = *reinterpret_cast<const u32x4 *>(src);
+    const int total = units * kPRows;
+    // four independent 16-byte loads in flight per thread before their stores
+    for (int w0 = tid; w0 < total; w0 += 4 * kPThreads) {
+      u32x4 v[4];
+      char *dst[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int w = w0 + k * kPThreads;
+        dst[k] = nullptr;
+        if (w < total) {
+          const int rr = w / units, u = w % units;
+          const int64_t srow = src_row[rr];
+          if (srow >= 0) {
+            const int ch = u / units_per_chunk, cu = u % units_per_chunk;
+            const char *src = static_cast<const char *>(st.src) + srow * st.src_row_stride +
+                              (int64_t)ch * st.src_chunk_stride + 16 * cu;
+            v[k] = *reinterpret_cast<const u32x4 *>(src);
+            dst[k] = static_cast<char *>(st.dst) + (j0 + rr) * st.dst_row_stride + (int64_t)ch * st.chunk_bytes +
+                     16 * cu;
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (dst[k]) *reinterpret_cast<u32x4 *>(dst[k]) = v[k];
     }
   }
 }
@@ -406,11 +608,13 @@ extern "C" int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32
   TG_CHECK(scores && geom && keep, "null pointer");
   TG_CHECK(num_seqs >= 0 && max_article_len >= 0, "negative size");
   if (num_seqs == 0) return 0;
-  if (max_article_len <= kTLdsKeys)
-    hipLaunchKernelGGL(gate_topk_kernel<true>, dim3(num_seqs), dim3(kTThreads), 0, stream, scores, geom, keep, sumsq);
+  const dim3 grid(num_seqs), block(kTThreads);
+  if (max_article_len <= 32 * kTThreads)
+    hipLaunchKernelGGL(gate_topk_reg_kernel<32>, grid, block, 0, stream, scores, geom, keep, sumsq);
+  else if (max_article_len <= 64 * kTThreads)
+    hipLaunchKernelGGL(gate_topk_reg_kernel<64>, grid, block, 0, stream, scores, geom, keep, sumsq);
   else
-    hipLaunchKernelGGL(gate_topk_kernel<false>, dim3(num_seqs), dim3(kTThreads), 0, stream, scores, geom, keep,
-                       sumsq);
+    hipLaunchKernelGGL(gate_topk_kernel<false>, grid, block, 0, stream, scores, geom, keep, sumsq);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }

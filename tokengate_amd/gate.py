@@ -78,14 +78,24 @@ def plan(row_starts: Sequence[int], seq_lens: Sequence[int], art_starts: Sequenc
     return KeepPlan(gh, gd, n_kept, kcs, cu, max_art)
 
 
-def select_keep(scores: torch.Tensor, p: KeepPlan, with_sumsq: bool = True) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+def select_keep(scores: torch.Tensor, p: KeepPlan, with_sumsq: bool = True,
+                keep_out: Optional[torch.Tensor] = None,
+                sumsq_out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
     """Keep lists of every sequence, packed: keep[cu_kept[b] + t] = the t-th kept position of
     sequence b (int64, ascending within a sequence).  Also the per-sequence sum of squared
-    article scores (for the RMS-normalised gate bias)."""
+    article scores (for the RMS-normalised gate bias).  keep_out / sumsq_out: optional
+    preallocated outputs (int64 of at least total_kept, float32 of at least num_seqs)."""
     if scores.dtype != torch.float32 or scores.dim() != 1 or not scores.is_contiguous():
         raise RuntimeError("scores must be a contiguous 1-D float32 tensor")
-    keep = torch.empty(p.total_kept, dtype=torch.int64, device=scores.device)
-    sumsq = torch.empty(len(p.n_kept), dtype=torch.float32, device=scores.device) if with_sumsq else None
+    keep = keep_out if keep_out is not None else torch.empty(p.total_kept, dtype=torch.int64, device=scores.device)
+    if keep.dtype != torch.int64 or keep.numel() < p.total_kept or not keep.is_contiguous():
+        raise RuntimeError("keep_out must be contiguous int64 with room for every kept row")
+    if sumsq_out is not None:
+        if sumsq_out.dtype != torch.float32 or sumsq_out.numel() < len(p.n_kept):
+            raise RuntimeError("sumsq_out must be float32 with one entry per sequence")
+        sumsq = sumsq_out
+    else:
+        sumsq = torch.empty(len(p.n_kept), dtype=torch.float32, device=scores.device) if with_sumsq else None
     if p.n_kept:
         _lib.call("tg_gate_topk_keep", scores.data_ptr(), p.geom.data_ptr(), len(p.n_kept), p.max_article,
                   keep.data_ptr(), sumsq.data_ptr() if sumsq is not None else None, _stream(scores))
