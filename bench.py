@@ -240,12 +240,16 @@ def cpu_baseline(q, k, v, bias_raw, scale, seconds):
 
 
 def traffic_from_profile():
-    """HBM bytes per launch from the committed rocprofv3 counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "keybias_fwd_32k_counters.json")
+    """HBM bytes per launch of the forward kernel at the 32k workload, from the committed
+    rocprofv3 counter summary (line 'hbm_bytes_per_launch: N'), or None."""
+    path = os.path.join(ROOT, "profiles", "keybias_fwd_32k_hbm_counters.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def main():
@@ -255,6 +259,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run three plain 1 GiB device copies (counter calibration for HBM bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: every GPU box here has one, and this path is timed on one "
@@ -287,6 +293,13 @@ def main():
         if args.cpu_seconds > 0:
             extra["gate_32k"]["cpu_prune_baseline"] = cpu_prune_baseline()
 
+    if args.calib_copy:
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     cpu = cpu_baseline(q, k, v, bias_raw, scale, args.cpu_seconds) if args.cpu_seconds > 0 else None
     line = {
         "metric": "key-bias attn TFLOP/s at 32k bf16 (% MFMA peak); pruned-prefill TTFT ms",
