@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kD = 128;        // head dim
 constexpr int kBN = 64;        // keys per tile
-constexpr int kWaves = 8;      // 2 waves per SIMD
+constexpr int kWaves = 4;      // one per SIMD; two workgroups share a CU
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -44,6 +44,7 @@ template <int HP> constexpr int bm() { return kWaves * qpw<HP>(); }
 
 constexpr int kKRowBytes = kD * 2;      // one K or V row in LDS (256 B, 16 chunks of 16 B)
 constexpr int kKTileBytes = kBN * kKRowBytes;
+constexpr int kStages = 2;              // K/V/bias ring: tile t resident, tile t+1 in flight
 
 struct FwdArgs {
   const bf16_t *q, *k, *v;
@@ -78,12 +79,13 @@ constexpr float kRescaleTau = 8.0f;
 // Both are filled by LDS DMA straight from global memory (no staging registers); keys past Sk
 // read as zero through the buffer descriptor's range check.
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
-__global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
   constexpr int QW = qpw<HP>();
   constexpr int BM = bm<HP>();
-  __shared__ __attribute__((aligned(1024))) char ks[2][kKTileBytes];
-  __shared__ __attribute__((aligned(1024))) char vs[2][kKTileBytes];
-  __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN];
+  __shared__ __attribute__((aligned(1024))) char ks[kStages][kKTileBytes];
+  __shared__ __attribute__((aligned(1024))) char vs[kStages][kKTileBytes];
+  // bias rows padded by 4 floats so that the two heads' rows fall on different banks
+  __shared__ __attribute__((aligned(256))) float bs[kStages][HP][kBN + 4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -148,15 +150,17 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
   const int n_tiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
 
   // ---- per-lane DMA source offsets (bytes within a tile; + tile * 64 rows per tile) ----
-  // 16 KB per tile = 16 wave-loads of 1 KB: wave w issues loads 2w and 2w+1 of K and of V.
-  uint32_t koff[2], voff[2];
+  // A 16 KB tile is 16 wave-loads of 1 KB; wave w issues loads w, w + kWaves, ...
+  constexpr int kLoads = kKTileBytes / 1024 / kWaves;
+  uint32_t koff[kLoads], voff[kLoads];
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int lr = (wave * 2 + it) * 4 + (lane >> 4);     // K LDS row written by this lane
+  for (int it = 0; it < kLoads; ++it) {
+    const int slot = wave + it * kWaves;                  // 1 KB slot = 4 rows
+    const int lr = slot * 4 + (lane >> 4);                // K LDS row written by this lane
     const int kc = (lane & 15) ^ (lr & 15);               // logical chunk stored there
     const int kkey = 32 * (lr >> 5) + sigma(lr & 31);
     koff[it] = (uint32_t)(kkey * a.k_rs * 2 + kc * 16);
-    const int vkey = (wave * 2 + it) * 4 + (lane >> 4);   // V LDS row (= key) written by this lane
+    const int vkey = slot * 4 + (lane >> 4);              // V LDS row (= key) written by this lane
     const int vc = (lane & 15) ^ (4 * (vkey & 3));
     voff[it] = (uint32_t)(vkey * a.v_rs * 2 + vc * 16);
   }
@@ -164,9 +168,9 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
     const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
     const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      dma16(krs, ks[buf] + (wave * 2 + it) * 1024, kb0 + koff[it]);
-      dma16(vrs, vs[buf] + (wave * 2 + it) * 1024, vb0 + voff[it]);
+    for (int it = 0; it < kLoads; ++it) {
+      dma16(krs, ks[buf] + (wave + it * kWaves) * 1024, kb0 + koff[it]);
+      dma16(vrs, vs[buf] + (wave + it * kWaves) * 1024, vb0 + voff[it]);
     }
     if constexpr (HAS_BIAS) {
       if (wave < HP) dma4(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
@@ -187,22 +191,39 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) oacc[d][v] = 0.f;
 
-  if (n_tiles > 0) issue_tile(0, 0);
+  // ring of kStages tiles: tile t lives in buffer t % kStages; tiles t+1 .. t+kStages-2 stay in
+  // flight while tile t is computed, and tile t+kStages-1 is issued into the buffer tile t-1 left.
+  const int ops_per_tile = 2 * kLoads + ((HAS_BIAS && wave < HP) ? 1 : 0);   // this wave's DMA ops
+  for (int t0 = 0; t0 < kStages - 1 && t0 < n_tiles; ++t0) issue_tile(t0, t0);
 
   for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t & 1;
+    const int buf = t % kStages;
     const int n0 = t * kBN;
-    wait_all_mem();
-    __syncthreads();                       // tile t resident; buffer buf^1 free
-    if (t + 1 < n_tiles) issue_tile(t + 1, buf ^ 1);
+    // wait until this wave's DMA for tile t is done; later tiles may stay in flight
+    const int later = min(kStages - 2, n_tiles - 1 - t);
+    wait_vm_outstanding(later * ops_per_tile);
+    __syncthreads();                       // tile t resident in every wave's view; buffer of t-1 free
+    if (t + kStages - 1 < n_tiles) issue_tile(t + kStages - 1, (t + kStages - 1) % kStages);
     if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
 
-    // ---- S^T = K Q^T: 2 key blocks x 8 d-steps ----
+    // ---- S^T = K Q^T + bias: 2 key blocks x 8 d-steps.  The accumulators start from the bias of
+    // their keys (raw-score units), so the bias add costs no VALU work. ----
     f32x16 sacc[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
+      if constexpr (HAS_BIAS) {
+        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 bb = bp[i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[kb][4 * i + e] = bb[e];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
+      }
+    }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
@@ -215,21 +236,9 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
 
     // ---- online softmax: one (head, query) column per lane, 32 keys per lane ----
     const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
-    float tv[2][16];
+    f32x16 (&tv)[2] = sacc;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      if constexpr (HAS_BIAS) {
-        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x4 bb = bp[i];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) tv[kb][4 * i + e] = sacc[kb][4 * i + e] + bb[e];
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) tv[kb][v] = sacc[kb][v];
-      }
       if (need_mask) {
         const int kidx = n0 + 32 * kb + 16 * g;
 #pragma unroll
@@ -241,11 +250,13 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
         }
       }
     }
-    float mx = tv[0][0];
+    // tile max as a tree (short dependency chain)
+    float m8[8];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, tv[kb][v]);
+    for (int i = 0; i < 8; ++i)
+      m8[i] = fmaxf(fmaxf(tv[i >> 2][4 * (i & 3)], tv[i >> 2][4 * (i & 3) + 1]),
+                    fmaxf(tv[i >> 2][4 * (i & 3) + 2], tv[i >> 2][4 * (i & 3) + 3]));
+    float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
     mx = pair_max(mx) * a.scale_log2;     // tile max in log2 units (-inf if fully masked)
     if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleTau) != 0) {
       const float m_new = fmaxf(mrun, mx);
@@ -257,19 +268,21 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
       for (int d = 0; d < 4; ++d) oacc[d] *= alpha;
     }
     const float mneg = mrun == -INFINITY ? 0.f : -mrun;
+    // P rounded to bf16 pairs; the row sum adds those same bf16 values (v_dot2 with 1.0, one
+    // instruction per pair), i.e. exactly the weights the P V product uses.
     uint32_t pk[2][8];
-    float psum = 0.f;
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};    // four independent partial sums
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
         const float p0 = fast_exp2(fmaf(tv[kb][v], a.scale_log2, mneg));
         const float p1 = fast_exp2(fmaf(tv[kb][v + 1], a.scale_log2, mneg));
-        psum += p0 + p1;
         pk[kb][v >> 1] = pack_bf16x2(p0, p1);
+        ps[(v >> 1) & 3] = sum_bf16x2(pk[kb][v >> 1], ps[(v >> 1) & 3]);
       }
     }
-    lrun += psum;
+    lrun += (ps[0] + ps[1]) + (ps[2] + ps[3]);
 
     // ---- O^T += V^T P^T ----
 #pragma unroll

@@ -91,6 +91,17 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const void *lds_addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)lds_addr);
 }
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
+// Wait until at most n (0..15) vector-memory operations of this wave are outstanding (vmcnt),
+// leaving the LDS and export counters unconstrained.
+__device__ __forceinline__ void wait_vm_outstanding(int n) {
+#define TG_VMCNT(N) case N: __builtin_amdgcn_s_waitcnt((N) | 0x0F70); break;
+  switch (n) {
+    TG_VMCNT(0) TG_VMCNT(1) TG_VMCNT(2) TG_VMCNT(3) TG_VMCNT(4) TG_VMCNT(5) TG_VMCNT(6) TG_VMCNT(7)
+    TG_VMCNT(8) TG_VMCNT(9) TG_VMCNT(10) TG_VMCNT(11) TG_VMCNT(12) TG_VMCNT(13) TG_VMCNT(14)
+    default: __builtin_amdgcn_s_waitcnt(15 | 0x0F70); break;
+  }
+#undef TG_VMCNT
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -100,6 +111,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   p[0] = (__bf16)lo;
   p[1] = (__bf16)hi;
   return __builtin_bit_cast(uint32_t, p);
+}
+
+// acc + lo + hi of a packed bf16 pair, in fp32 (v_dot2c_f32_bf16 against (1, 1)).
+__device__ __forceinline__ float sum_bf16x2(uint32_t pair, float acc) {
+  bf16x2 one;
+  one[0] = (__bf16)1.0f;
+  one[1] = (__bf16)1.0f;
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, acc, false);
 }
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
