@@ -14,8 +14,10 @@ Prints ONE JSON line with the bench contract fields plus:
   cpu_baseline — the oracle (float32 numpy, all host cores through BLAS) on a bounded sample of
                  the same workload: the last query rows of every head, full causal key range;
   extra        — secondary measurements: the 4k forward, the B4 x 8192 backward (TFLOP/s of
-                 5*B*H*D*S*(S+1)), and the 32k gate path (scoring, top-K, pack; the short gate
-                 launches are timed as replays of a captured HIP graph).
+                 5*B*H*D*S*(S+1)), the 32k gate path (scoring, top-K, pack; the short gate
+                 launches are timed as replays of a captured HIP graph), and the pruned-prefill
+                 time to first token of a Qwen3-1.7B-shaped decoder at 32k (K = 100, 2000, all)
+                 and on 8 ragged prompts of 16k-128k tokens.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--cpu-seconds 10]
 """
@@ -187,6 +189,52 @@ def bench_gate(dev, iters=50):
     return res
 
 
+def bench_ttft(dev, reps=5):
+    """Pruned-prefill time to first token (tokengate_amd.prefill.prefill_batch) on a random-init
+    Qwen3-1.7B-shaped decoder (28 layers, d 2048, 16/8 heads, head_dim 128, FFN 6144, vocab 151936,
+    RoPE theta 1e6, bf16), gate at layer 1 (scoring head Linear(2048->256)->SiLU->Linear(256->1)),
+    prompts of uniform random ids already on the device, state span = prompt minus a 64-token
+    prefix and a 256-token suffix.  Protocol of the reference's TTFT bench: sync, perf_counter,
+    prefill through the first token, sync; median of `reps` after one warmup."""
+    import statistics
+    import torch
+    from tokengate_amd import decoder as dec
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    shape = dec.QWEN3_1P7B
+    wts = dec.random_decoder(shape, seed=0, device=dev)
+    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=5, device=dev)
+    g = torch.Generator().manual_seed(7)
+    out = {}
+
+    def run(name, lens, Ks):
+        ids = [torch.randint(0, shape.vocab, (n,), generator=g).to(dev) for n in lens]
+        starts = [64] * len(lens)
+        ends = [n - 256 for n in lens]
+        fn = lambda: P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
+        times = P.ttft_ms(fn, reps=reps, warmup=1)
+        r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, phase_timing=True)
+        out[name] = {"ttft_ms": round(statistics.median(times), 3), "reps_ms": [round(t, 3) for t in times],
+                     "prompt_tokens": sum(lens), "kept_tokens": r.cu_kept[-1],
+                     "phase_ms": {k: round(v, 3) for k, v in r.phase_ms.items()}}
+        if len(lens) > 1:
+            out[name]["lens"] = lens
+            out[name]["K"] = Ks
+        del r
+        torch.cuda.empty_cache()
+
+    for K in (100, 2000):
+        run(f"32k_K{K}", [32768], [K])
+    run("32k_Kall", [32768], [10_000_000])
+    rng = torch.Generator().manual_seed(17)
+    lens = [int(x) for x in torch.randint(16384, 131073, (8,), generator=rng)]
+    Ks = [[100, 500, 2000, 4000][int(i)] for i in torch.randint(0, 4, (8,), generator=rng)]
+    run("ragged8", lens, Ks)
+    del wts
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_prune_baseline(seconds=3.0):
     """The oracle's top-K + keep + gathers (numpy, host cores) at the 32k gate workload, K=2000:
     topk order, sort, keep list, hidden + 2 layers' K/V row gathers."""
@@ -292,6 +340,7 @@ def main():
         extra["gate_32k"] = bench_gate(dev)
         if args.cpu_seconds > 0:
             extra["gate_32k"]["cpu_prune_baseline"] = cpu_prune_baseline()
+        extra["ttft"] = bench_ttft(dev)
 
     if args.calib_copy:
         src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)

@@ -1,0 +1,156 @@
+"""Oracle: the gated prefill in float32 torch (TEST INFRASTRUCTURE ONLY).
+
+Restates, for a Qwen3-shaped decoder given as float32 weights:
+  * one decoder layer — transformers' Qwen3DecoderLayer / Qwen3Attention / Qwen3MLP /
+    Qwen3RMSNorm / default RoPE (modeling_qwen3.py; transformers 5.19.0 pinned by the reference's
+    uv.lock:3897-3898), with the attention replaced by the key-bias attention the reference
+    routes through (qwen3_flex_attention.py:524-659): RMSNorm -> q/k/v projections -> per-head
+    q/k RMSNorm -> RoPE (cos/sin of fp32 angles position * inv_freq) -> causal GQA attention with
+    an additive per-key logit bias -> o_proj -> residual -> RMSNorm -> down(silu(gate) * up) ->
+    residual.  Phase 2's temperature multiplies the query and the bias per head
+    (_phase2_q_bias :433-473).
+  * prefill_batch_for_decode (gate_forward.py:1280-1580) in its own layout: prompts right-padded
+    to the longest, layers 0..gate_layer over every position, per-sample scoring and top-K
+    (K_clamped, keep = prefix + sorted top-K + suffix), kept rows gathered into a zero-padded
+    (B, n_alloc) batch whose pad slots carry a -1e9 bias, layers above the gate on that batch
+    with RoPE at the kept original positions, first token = argmax of the LM head at each
+    sample's last kept row.
+Pinned by tests/test_oracle_prefill.py against transformers' own Qwen3DecoderLayer (same
+weights, float32, eager attention) and by padded-vs-per-sequence equivalence.
+"""
+import math
+from typing import List, Optional, Sequence
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle import attention_torch as oat
+from oracle import gate as og
+
+
+def rms(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps))
+
+
+def rope_cos_sin(pos: torch.Tensor, inv_freq: torch.Tensor):
+    ang = pos.float()[..., None] * inv_freq.float()            # fp32 product, as the rotary table
+    emb = torch.cat([ang, ang], dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat([-x[..., h:], x[..., :h]], dim=-1)
+
+
+class Weights:
+    """float32 copies of a decoder's weights (any object with the DecoderWeights fields)."""
+
+    def __init__(self, wts):
+        s = wts.shape
+        self.shape = s
+        f = lambda t: t.detach().float().cpu()
+        self.embed = f(wts.embed)
+        self.final_norm = f(wts.final_norm)
+        self.lm_head = f(wts.lm_head)
+        self.inv_freq = f(wts.inv_freq)
+        self.layers = []
+        for lw in wts.layers:
+            q, k, v = torch.split(f(lw.w_qkv), [s.n_heads * s.head_dim, s.n_kv_heads * s.head_dim,
+                                                s.n_kv_heads * s.head_dim])
+            g, u = torch.split(f(lw.w_gu), [s.d_ff, s.d_ff])
+            self.layers.append(dict(ln1=f(lw.ln1), wq=q, wk=k, wv=v, q_norm=f(lw.q_norm), k_norm=f(lw.k_norm),
+                                    wo=f(lw.w_o), ln2=f(lw.ln2), wg=g, wu=u, wd=f(lw.w_down)))
+
+
+def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
+          q_temp: Optional[torch.Tensor] = None):
+    """One decoder layer on a batch x (B, n, d) float32 at positions pos (B, n); bias_logit
+    (B, H, n) per-key logit bias (before the temperature) or None; q_temp (H,) or None.
+    Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE."""
+    s = W.shape
+    L = W.layers[i]
+    B, n, _ = x.shape
+    H, Hkv, D = s.n_heads, s.n_kv_heads, s.head_dim
+    h = rms(x, L["ln1"], s.rms_eps)
+    q = (h @ L["wq"].t()).view(B, n, H, D)
+    k = (h @ L["wk"].t()).view(B, n, Hkv, D)
+    v = (h @ L["wv"].t()).view(B, n, Hkv, D)
+    q = rms(q, L["q_norm"], s.rms_eps)
+    k = rms(k, L["k_norm"], s.rms_eps)
+    cos, sin = rope_cos_sin(pos, W.inv_freq)                  # (B, n, D)
+    cos, sin = cos[:, :, None, :], sin[:, :, None, :]
+    q = q * cos + rotate_half(q) * sin
+    k = k * cos + rotate_half(k) * sin
+    scale = 1.0 / math.sqrt(D)
+    braw = None
+    if bias_logit is not None:
+        bl = bias_logit
+        if q_temp is not None:
+            bl = bl * q_temp[None, :, None]
+        braw = bl / scale
+    if q_temp is not None:
+        q = q * q_temp[None, None, :, None]
+    attn, _ = oat.fwd(q, k, v, braw, scale, causal=True)
+    x = x + attn.reshape(B, n, H * D) @ L["wo"].t()
+    h = rms(x, L["ln2"], s.rms_eps)
+    x = x + (F.silu(h @ L["wg"].t()) * (h @ L["wu"].t())) @ L["wd"].t()
+    return x, k, v
+
+
+def head_scores(head, h: torch.Tensor) -> np.ndarray:
+    """The scoring head on rows h (n, d), float64."""
+    return og.score_mlp(h.double().numpy(), head.w1.float().cpu().numpy(), head.b1.cpu().numpy(),
+                        head.w2.cpu().numpy(), head.b2)
+
+
+def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art_ends, gate_layer: int, K,
+            keep_override: Optional[List[np.ndarray]] = None, scores_override: Optional[List[np.ndarray]] = None):
+    """The reference's padded-batch prefill.  keep_override / scores_override (per sample) replace
+    the oracle's own selection / scores (to compare layouts and numerics on the same keep set).
+    Returns dict(first_tokens, logits (B, vocab), keep (list), h_gate (list of (len, d)),
+    h_last (B, n_alloc, d), kept_bias (list))."""
+    s = W.shape
+    B = len(ids_list)
+    lens = [len(x) for x in ids_list]
+    S = max(lens)
+    ids = torch.zeros(B, S, dtype=torch.long)
+    for b, x in enumerate(ids_list):
+        ids[b, :lens[b]] = torch.as_tensor(list(x), dtype=torch.long)
+    x = W.embed[ids]
+    pos = torch.arange(S)[None, :].expand(B, S)
+    for i in range(gate_layer + 1):
+        x, _, _ = layer(W, i, x, pos)
+    Ks = K if isinstance(K, (list, tuple)) else [K] * B
+    keeps, biases, h_gate = [], [], []
+    for b in range(B):
+        st, en = art_starts[b], art_ends[b]
+        h_gate.append(x[b, :lens[b]].clone())
+        sc = scores_override[b] if scores_override is not None else head_scores(head, x[b, st:en])
+        kp = keep_override[b] if keep_override is not None else og.keep_indices(sc, Ks[b], st, en, lens[b])
+        keeps.append(np.asarray(kp, dtype=np.int64))
+        biases.append(og.gate_bias(sc, keeps[-1], st, en))
+    n_alloc = max(len(k) for k in keeps)
+    hp = torch.zeros(B, n_alloc, s.d_model)
+    kpos = torch.zeros(B, n_alloc, dtype=torch.long)
+    gb = torch.full((B, n_alloc), -1e9, dtype=torch.float64)
+    for b in range(B):
+        kt = torch.as_tensor(keeps[b])
+        hp[b, :len(kt)] = x[b, kt]
+        kpos[b, :len(kt)] = kt
+        gb[b, :len(kt)] = torch.as_tensor(biases[b])
+    if tuple(head.gate_scale.shape) != (s.n_layers - gate_layer - 1, s.n_heads):
+        raise ValueError("gate_scale must be (layers above the gate, heads)")
+    gs = F.softplus(head.gate_scale.float().cpu())                  # (L2, H)
+    at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
+    xx = hp
+    for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
+        bl = gb.float()[:, None, :] * gs[j][None, :, None]
+        bl = torch.where(gb[:, None, :] <= -1e8, torch.full_like(bl, -1e9), bl)
+        xx, _, _ = layer(W, i, xx, kpos, bias_logit=bl, q_temp=at[j] if at is not None else None)
+    last = torch.tensor([len(k) - 1 for k in keeps])
+    rows = xx[torch.arange(B), last]
+    logits = rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()
+    return dict(first_tokens=logits.argmax(-1), logits=logits, keep=keeps, h_gate=h_gate, h_last=xx,
+                kept_bias=biases)

@@ -1,0 +1,107 @@
+"""GPU parity of the decoder ops of the gated prefill against float32 torch evaluations of the same
+math (the oracle's Qwen3 layer pieces, pinned against transformers by test_oracle_prefill.py):
+residual add + RMSNorm, per-head q/k RMSNorm + RoPE (positions up to 2^17, per-head query scale,
+k/v cache writes), SiLU(gate) * up.  Bound: max-abs <= 2e-2 relative to max(1, |ref|) and
+rel-L2 <= 1e-2 (one bf16 rounding of the output)."""
+import math
+
+import pytest
+import torch
+
+from oracle import prefill as op
+from tests.attn_util import assert_close_grad, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(t):
+    return t.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,d,with_res", [(1, 2048, False), (777, 2048, True), (64, 1024, True),
+                                             (5, 4096, False), (33, 2560, True)])
+def test_rmsnorm(cuda, rows, d, with_res):
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows + d)
+    x = _bf(torch.randn(rows, d, generator=g, device=cuda) * 3)
+    w = _bf(1 + 0.3 * torch.randn(d, generator=g, device=cuda))
+    res = _bf(torch.randn(rows, d, generator=g, device=cuda)) if with_res else None
+    res_out = torch.empty_like(x) if with_res else None
+    out = dec.rmsnorm(x, w, 1e-6, residual=res, residual_out=res_out)
+    torch.cuda.synchronize()
+    s = x.float() + res.float() if with_res else x.float()
+    if with_res:
+        assert torch.equal(res_out, _bf(s))                     # the bf16 residual stream, bit-exact
+        s = _bf(s).float()
+    ref = op.rms(s, w.float(), 1e-6)
+    assert_close_grad("rmsnorm", to_np(out), to_np(ref))
+
+
+def test_rmsnorm_in_place_residual(cuda):
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(3)
+    x = _bf(torch.randn(100, 2048, generator=g, device=cuda))
+    res = _bf(torch.randn(100, 2048, generator=g, device=cuda))
+    w = _bf(torch.ones(2048, device=cuda))
+    want_res = _bf(x.float() + res.float())
+    ref = op.rms(want_res.float(), w.float(), 1e-6)
+    out = dec.rmsnorm(x, w, 1e-6, residual=res, residual_out=res, out=x)   # both aliased
+    torch.cuda.synchronize()
+    assert torch.equal(res, want_res)
+    assert_close_grad("rmsnorm aliased", to_np(out), to_np(ref))
+
+
+@pytest.mark.parametrize("T,H,Hkv,maxpos,scaled", [(1, 16, 8, 1, False), (333, 16, 8, 4096, True),
+                                                    (257, 4, 1, 1 << 17, True), (64, 12, 4, 40000, False)])
+def test_qk_norm_rope(cuda, T, H, Hkv, maxpos, scaled):
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(T * 31 + H)
+    D = 128
+    shape = dec.DecoderShape(n_layers=1, n_heads=H, n_kv_heads=Hkv, d_model=H * D)
+    width = (H + 2 * Hkv) * D
+    qkv = _bf(torch.randn(T, width, generator=g, device=cuda) * 2)
+    qkv0 = qkv.clone()
+    pos = torch.randint(0, maxpos, (T,), generator=g, device=cuda)
+    lw = dec.LayerWeights(None, None, _bf(1 + 0.3 * torch.randn(D, generator=g, device=cuda)),
+                          _bf(1 + 0.3 * torch.randn(D, generator=g, device=cuda)), None, None, None, None)
+    inv = dec.rope_inv_freq(shape, cuda)
+    qs = (0.5 + torch.rand(H, generator=g, device=cuda)) if scaled else None
+    k = torch.empty(T, Hkv, D, dtype=torch.bfloat16, device=cuda)
+    v = torch.empty_like(k)
+    q = dec.qk_norm_rope(qkv, pos, lw, shape, inv, k, v, qs)
+    torch.cuda.synchronize()
+    x = qkv0.float()
+    qr = op.rms(x[:, :H * D].view(T, H, D), lw.q_norm.float(), 1e-6)
+    kr = op.rms(x[:, H * D:(H + Hkv) * D].view(T, Hkv, D), lw.k_norm.float(), 1e-6)
+    cos, sin = op.rope_cos_sin(pos.cpu(), inv.cpu())
+    cos, sin = cos.to(cuda)[:, None, :], sin.to(cuda)[:, None, :]
+    qr = qr * cos + op.rotate_half(qr) * sin
+    kr = kr * cos + op.rotate_half(kr) * sin
+    if qs is not None:
+        qr = qr * qs[None, :, None]
+    assert_close_grad("q", to_np(q), to_np(qr))
+    assert_close_grad("k", to_np(k), to_np(kr))
+    assert torch.equal(v.view(T, -1), qkv0[:, (H + Hkv) * D:])
+    assert torch.equal(qkv[:, H * D:], qkv0[:, H * D:])          # k/v columns untouched
+    assert q.data_ptr() == qkv.data_ptr()                         # q rotated in place
+
+
+@pytest.mark.parametrize("rows,inter", [(1, 8), (1000, 6144), (37, 1000)])
+def test_silu_mul(cuda, rows, inter):
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows + inter)
+    gu = _bf(torch.randn(rows, 2 * inter, generator=g, device=cuda) * 3)
+    out = dec.silu_mul(gu)
+    torch.cuda.synchronize()
+    f = gu.float()
+    ref = torch.nn.functional.silu(f[:, :inter]) * f[:, inter:]
+    assert_close_grad("silu_mul", to_np(out), to_np(ref))
+
+
+def test_decoder_op_errors(cuda):
+    from tokengate_amd import decoder as dec
+    x = torch.zeros(4, 2050, dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        dec.rmsnorm(x[:, :2044], torch.ones(2044, dtype=torch.bfloat16, device=cuda), 1e-6)
+    with pytest.raises(RuntimeError, match="inter"):
+        dec.silu_mul(torch.zeros(3, 6, dtype=torch.bfloat16, device=cuda))

@@ -1,0 +1,207 @@
+"""Pins oracle/prefill.py (CPU, no GPU).
+
+* One decoder layer against transformers' own Qwen3DecoderLayer (the module the reference runs,
+  modeling_qwen3.py) on the same float32 weights with eager attention: causal, with a per-head
+  per-key additive bias passed as the attention mask, and with a uniform temperature (q scaled,
+  bias scaled — folded into q_norm's weight on the transformers side).
+* The reference's padded Phase-2 batch (-1e9 pad slots) equals running each sample alone, and a
+  right-padded Phase 1 equals the unpadded one, so the packed (cu_seqlens) layout of the product
+  computes the same function.
+* The keep lists and kept bias follow oracle.gate on the oracle's own scores.
+"""
+import math
+from dataclasses import dataclass
+from typing import List
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gate as og
+from oracle import prefill as op
+
+transformers = pytest.importorskip("transformers")
+from transformers import Qwen3Config  # noqa: E402
+from transformers.models.qwen3 import modeling_qwen3 as mq  # noqa: E402
+
+
+@dataclass(frozen=True)
+class Shape:
+    n_layers: int = 3
+    d_model: int = 256
+    n_heads: int = 4
+    n_kv_heads: int = 2
+    head_dim: int = 128
+    d_ff: int = 384
+    vocab: int = 97
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+
+@dataclass
+class LW:
+    ln1: torch.Tensor
+    w_qkv: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    w_o: torch.Tensor
+    ln2: torch.Tensor
+    w_gu: torch.Tensor
+    w_down: torch.Tensor
+
+
+@dataclass
+class Wts:
+    shape: Shape
+    embed: torch.Tensor
+    layers: List[LW]
+    final_norm: torch.Tensor
+    lm_head: torch.Tensor
+    inv_freq: torch.Tensor
+
+
+def _wts(shape: Shape, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=g) * 0.05
+    nw = lambda n: 1 + 0.2 * (torch.rand(n, generator=g) - 0.5)
+    d, D = shape.d_model, shape.head_dim
+    qkv = (shape.n_heads + 2 * shape.n_kv_heads) * D
+    layers = [LW(nw(d), r(qkv, d), nw(D), nw(D), r(d, shape.n_heads * D), nw(d), r(2 * shape.d_ff, d),
+                 r(d, shape.d_ff)) for _ in range(shape.n_layers)]
+    inv = 1.0 / (shape.rope_theta ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = r(shape.vocab, d) * 10
+    return Wts(shape, emb, layers, nw(d), emb, inv)
+
+
+def _hf_layer(shape: Shape, lw: LW, q_norm_mult=1.0):
+    cfg = Qwen3Config(hidden_size=shape.d_model, intermediate_size=shape.d_ff, num_attention_heads=shape.n_heads,
+                      num_key_value_heads=shape.n_kv_heads, head_dim=shape.head_dim, rms_norm_eps=shape.rms_eps,
+                      rope_theta=shape.rope_theta, num_hidden_layers=1, vocab_size=shape.vocab,
+                      max_position_embeddings=1 << 17)
+    cfg._attn_implementation = "eager"
+    L = mq.Qwen3DecoderLayer(cfg, 0).float().eval()
+    H, Hkv, D, f = shape.n_heads, shape.n_kv_heads, shape.head_dim, shape.d_ff
+    q, k, v = torch.split(lw.w_qkv, [H * D, Hkv * D, Hkv * D])
+    gt, up = torch.split(lw.w_gu, [f, f])
+    with torch.no_grad():
+        L.input_layernorm.weight.copy_(lw.ln1)
+        L.post_attention_layernorm.weight.copy_(lw.ln2)
+        L.self_attn.q_proj.weight.copy_(q)
+        L.self_attn.k_proj.weight.copy_(k)
+        L.self_attn.v_proj.weight.copy_(v)
+        L.self_attn.o_proj.weight.copy_(lw.w_o)
+        L.self_attn.q_norm.weight.copy_(lw.q_norm * q_norm_mult)
+        L.self_attn.k_norm.weight.copy_(lw.k_norm)
+        L.mlp.gate_proj.weight.copy_(gt)
+        L.mlp.up_proj.weight.copy_(up)
+        L.mlp.down_proj.weight.copy_(lw.w_down)
+    return cfg, L
+
+
+def _hf_run(shape, lw, x, pos, mask, q_norm_mult=1.0):
+    cfg, L = _hf_layer(shape, lw, q_norm_mult)
+    rot = mq.Qwen3RotaryEmbedding(cfg)
+    cos, sin = rot(x, pos)
+    with torch.no_grad():
+        out = L(x, attention_mask=mask, position_ids=pos, position_embeddings=(cos, sin))
+    return out[0] if isinstance(out, tuple) else out
+
+
+def _causal_mask(B, n, H=1):
+    m = torch.triu(torch.full((n, n), float("-inf")), diagonal=1)
+    return m[None, None].expand(B, H, n, n).clone()
+
+
+def _rel(a, b):
+    return float((a - b).norm() / b.norm())
+
+
+@pytest.mark.parametrize("n,offset", [(37, 0), (160, 40000)])
+def test_layer_matches_transformers_causal(n, offset):
+    s = Shape()
+    W = op.Weights(_wts(s))
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(2, n, s.d_model, generator=g)
+    pos = (torch.arange(n) + offset)[None].expand(2, n).contiguous()
+    ours, _, _ = op.layer(W, 0, x, pos)
+    ref = _hf_run(s, _wts(s).layers[0], x, pos, _causal_mask(2, n))
+    assert _rel(ours, ref) < 1e-5, _rel(ours, ref)
+
+
+def test_layer_matches_transformers_bias_and_temperature():
+    s = Shape()
+    W = op.Weights(_wts(s))
+    g = torch.Generator().manual_seed(2)
+    B, n = 2, 96
+    x = torch.randn(B, n, s.d_model, generator=g)
+    pos = torch.sort(torch.randperm(5000, generator=g)[:n]).values[None].expand(B, n).contiguous()
+    bias = torch.randn(B, s.n_heads, n, generator=g) * 2          # per-head per-key logit bias
+    ours, _, _ = op.layer(W, 1, x, pos, bias_logit=bias)
+    mask = _causal_mask(B, n, s.n_heads) + bias[:, :, None, :]
+    ref = _hf_run(s, _wts(s).layers[1], x, pos, mask)
+    assert _rel(ours, ref) < 1e-5
+    # uniform temperature a: q * a and bias * a; transformers side: q_norm weight * a, mask bias * a
+    a = 1.7
+    ours_t, _, _ = op.layer(W, 1, x, pos, bias_logit=bias, q_temp=torch.full((s.n_heads,), a))
+    ref_t = _hf_run(s, _wts(s).layers[1], x, pos, _causal_mask(B, n, s.n_heads) + a * bias[:, :, None, :],
+                    q_norm_mult=a)
+    assert _rel(ours_t, ref_t) < 1e-5
+    assert _rel(ours_t, ours) > 1e-3          # the temperature does change the result
+
+
+@dataclass
+class Head:
+    w1: torch.Tensor
+    b1: torch.Tensor
+    w2: torch.Tensor
+    b2: float
+    gate_scale: torch.Tensor
+    attn_scale: torch.Tensor
+
+
+def _head(s: Shape, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    return Head(torch.randn(256, s.d_model, generator=g) * 0.05, torch.zeros(256), torch.randn(256, generator=g) * 0.1,
+                0.0, torch.randn(s.n_layers - 2, s.n_heads, generator=g) * 0.3,
+                torch.randn(s.n_layers - 2, s.n_heads, generator=g) * 0.3 + math.log(math.expm1(1.0)))
+
+
+def _prompts(lens, vocab, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randint(0, vocab, (n,), generator=g).tolist() for n in lens]
+
+
+def test_padded_batch_equals_per_sample():
+    s = Shape(n_layers=4)
+    W = op.Weights(_wts(s, seed=4))
+    head = _head(s)
+    head.gate_scale = torch.randn(2, s.n_heads) * 0.3
+    head.attn_scale = torch.randn(2, s.n_heads) * 0.3 + 0.5
+    lens, starts, ends, Ks = [90, 140, 61], [5, 10, 3], [80, 120, 50], [7, 200, 1]
+    ids = _prompts(lens, s.vocab, 5)
+    full = op.prefill(W, head, ids, starts, ends, 1, Ks)
+    for b in range(3):
+        one = op.prefill(W, head, [ids[b]], [starts[b]], [ends[b]], 1, [Ks[b]])
+        assert np.array_equal(one["keep"][0], full["keep"][b])
+        n = len(one["keep"][0])
+        assert _rel(full["h_last"][b, :n], one["h_last"][0, :n]) < 1e-5
+        assert _rel(full["logits"][b], one["logits"][0]) < 1e-5
+        # Phase 1 with right padding == Phase 1 alone
+        assert _rel(full["h_gate"][b], one["h_gate"][0]) < 1e-5
+
+
+def test_keep_lists_and_bias_follow_gate_oracle():
+    s = Shape(n_layers=3)
+    W = op.Weights(_wts(s, seed=6))
+    head = _head(s, seed=7)
+    head.gate_scale = torch.zeros(2, s.n_heads)
+    head.attn_scale = torch.zeros(2, s.n_heads)
+    lens, starts, ends, Ks = [70, 55], [4, 0], [60, 55], [10, 100]
+    ids = _prompts(lens, s.vocab, 8)
+    r = op.prefill(W, head, ids, starts, ends, 0, Ks)
+    for b in range(2):
+        sc = op.head_scores(head, r["h_gate"][b][starts[b]:ends[b]])
+        kp = og.keep_indices(sc, Ks[b], starts[b], ends[b], lens[b])
+        assert np.array_equal(kp, r["keep"][b])
+        assert len(kp) == starts[b] + og.k_clamped(Ks[b], ends[b] - starts[b]) + lens[b] - ends[b]
+        np.testing.assert_allclose(r["kept_bias"][b], og.gate_bias(sc, kp, starts[b], ends[b]))

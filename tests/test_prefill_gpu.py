@@ -1,0 +1,139 @@
+"""GPU parity of the gated prefill (tokengate_amd.prefill) against the oracle's restatement of
+prefill_batch_for_decode (oracle/prefill.py, pinned against transformers' Qwen3DecoderLayer).
+
+On a ragged batch (prefix / state span / suffix per prompt, K below, at and above the span
+length) with a 4-layer Qwen3-attention-shaped decoder (d 2048, 16/8 heads, head_dim 128), gate at
+layer 1:
+  * keep lists, kept positions, packed hidden rows and the kept-row gate bias: bit-exact (bias:
+    float32 rounding) against the oracle's selection on the same scores;
+  * every decoder layer, Phase 1 (causal, all tokens) and Phase 2 (kept rows, RoPE at the
+    original positions, per-(layer, head) gate bias and temperature), teacher-forced: the oracle
+    layer applied to the pipeline's own input of that layer matches the pipeline's output within
+    max-abs 2e-2 (relative to max(1, |ref|)) and rel-L2 1e-2;
+  * the first-token logits from the pipeline's last hidden state, same bound;
+  * end to end, the oracle's float32 prefill from the token ids (on the same keep lists) against
+    the bf16 pipeline: rel-L2 of the final hidden state and logits <= 3e-2 (four layers of bf16
+    activations compound; reported per case).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gate as og
+from oracle import prefill as op
+from tests.attn_util import assert_close_grad, to_np
+
+pytestmark = pytest.mark.gpu
+
+SHAPE_KW = dict(n_layers=4, d_model=2048, n_heads=16, n_kv_heads=8, head_dim=128, d_ff=1024, vocab=512)
+
+
+def _setup(cuda, seed=0):
+    from tokengate_amd import decoder as dec
+    from tokengate_amd import gate as G
+    shape = dec.DecoderShape(**SHAPE_KW)
+    wts = dec.random_decoder(shape, seed=seed, device=cuda, std=0.02, norm_jitter=0.2)
+    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=seed + 5, device=cuda)
+    # a visible per-(layer, head) spread of gate scale and temperature
+    g = torch.Generator(device=cuda).manual_seed(seed + 9)
+    head.gate_scale = head.gate_scale + 0.5 * torch.randn(head.gate_scale.shape, generator=g, device=cuda)
+    head.attn_scale = head.attn_scale + 0.3 * torch.randn(head.attn_scale.shape, generator=g, device=cuda)
+    return shape, wts, head
+
+
+CASES = {
+    "ragged3": ([700, 1290, 333], [16, 64, 0], [600, 1100, 333], [100, 500, 4000]),
+    "one": ([517], [64], [417], [1]),
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_prefill_matches_oracle(cuda, case):
+    from tokengate_amd import prefill as P
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    lens, starts, ends, Ks = CASES[case]
+    shape, wts, head = _setup(cuda)
+    g = torch.Generator().manual_seed(11)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, capture=True)
+    torch.cuda.synchronize()
+    cap = r.capture
+    cu1 = r.cu_prompt
+    cu2 = r.cu_kept
+    scores = cap["scores"].cpu().numpy().astype(np.float64)
+    keep = cap["keep"].cpu().numpy()
+    kpos = r.kept_positions.cpu().numpy()
+    h1 = cap["h1"].float().cpu()
+    hsp = cap["hs_packed"].float().cpu()
+    kb = r.kept_bias.cpu().numpy()
+    keeps = []
+    for b in range(len(lens)):
+        sc = scores[cu1[b] + starts[b]:cu1[b] + ends[b]]
+        want = og.keep_indices(sc, Ks[b], starts[b], ends[b], lens[b])
+        got = keep[cu2[b]:cu2[b + 1]]
+        assert np.array_equal(got, want), f"seq {b}: keep list differs"
+        assert np.array_equal(kpos[cu2[b]:cu2[b + 1]], want)
+        assert r.n_kept[b] == len(want) and r.k_clamped[b] == og.k_clamped(Ks[b], ends[b] - starts[b])
+        assert torch.equal(hsp[cu2[b]:cu2[b + 1]], h1[cu1[b] + torch.as_tensor(want)])
+        np.testing.assert_allclose(kb[cu2[b]:cu2[b + 1]], og.gate_bias(sc, want, starts[b], ends[b]),
+                                   rtol=2e-6, atol=1e-7)
+        keeps.append(want)
+
+    W = op.Weights(wts)
+    ins1 = [t.float().cpu() for t in cap["phase1"]] + [h1]
+    for i in range(2):
+        for b in range(len(lens)):
+            x = ins1[i][cu1[b]:cu1[b + 1]][None]
+            pos = torch.arange(lens[b])[None]
+            ref, _, _ = op.layer(W, i, x, pos)
+            assert_close_grad(f"phase1 layer {i} seq {b}", to_np(ins1[i + 1][cu1[b]:cu1[b + 1]]), to_np(ref[0]))
+    gs = torch.nn.functional.softplus(head.gate_scale.float().cpu())
+    at = torch.nn.functional.softplus(head.attn_scale.float().cpu())
+    h2 = cap["h2"].float().cpu()
+    ins2 = [t.float().cpu() for t in cap["phase2"]] + [h2]
+    for j, i in enumerate(range(2, shape.n_layers)):
+        for b in range(len(lens)):
+            x = ins2[j][cu2[b]:cu2[b + 1]][None]
+            pos = torch.as_tensor(keeps[b])[None]
+            sc = scores[cu1[b] + starts[b]:cu1[b] + ends[b]]
+            bl = torch.as_tensor(og.gate_bias(sc, keeps[b], starts[b], ends[b]), dtype=torch.float32)
+            bl = bl[None, None, :] * gs[j][None, :, None]
+            ref, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_temp=at[j])
+            assert_close_grad(f"phase2 layer {i} seq {b}", to_np(ins2[j + 1][cu2[b]:cu2[b + 1]]), to_np(ref[0]))
+    last = torch.tensor(cu2[1:]) - 1
+    ref_logits = op.rms(h2[last], W.final_norm, shape.rms_eps) @ W.lm_head.t()
+    assert_close_grad("logits", to_np(cap["logits"]), to_np(ref_logits))
+    assert torch.equal(r.first_tokens.cpu(), cap["logits"].argmax(-1).cpu())
+
+    # end to end from the ids, on the same keep lists
+    e2e = op.prefill(W, head, ids, starts, ends, 1, Ks, keep_override=keeps)
+    for b in range(len(lens)):
+        n = r.n_kept[b]
+        d = float((h2[cu2[b]:cu2[b + 1]] - e2e["h_last"][b, :n]).norm() / e2e["h_last"][b, :n].norm())
+        dl = float((cap["logits"][b].cpu() - e2e["logits"][b]).norm() / e2e["logits"][b].norm())
+        print(f"[e2e] {case} seq {b}: rel-L2 hidden {d:.2e} logits {dl:.2e}", flush=True)
+        assert d <= 3e-2 and dl <= 3e-2
+
+
+def test_prefill_prune_below_gate(cuda):
+    """prune_below_gate=True packs the gate-and-below KV caches to the kept rows in the same launch."""
+    from tokengate_amd import prefill as P
+    lens, starts, ends, Ks = CASES["ragged3"]
+    shape, wts, head = _setup(cuda, seed=1)
+    g = torch.Generator().manual_seed(12)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    full = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
+    pruned = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, prune_below_gate=True)
+    torch.cuda.synchronize()
+    assert torch.equal(full.first_tokens, pruned.first_tokens)
+    assert torch.equal(full.kept_positions, pruned.kept_positions)
+    rows = torch.cat([full.cu_prompt[b] + full.kept_positions[full.cu_kept[b]:full.cu_kept[b + 1]]
+                      for b in range(len(lens))])
+    for i in range(2):
+        assert full.kv[i].k.shape[0] == full.cu_prompt[-1] and pruned.kv[i].k.shape[0] == pruned.cu_kept[-1]
+        assert torch.equal(pruned.kv[i].k, full.kv[i].k[rows])
+        assert torch.equal(pruned.kv[i].v, full.kv[i].v[rows])
+    for i in range(2, shape.n_layers):
+        assert torch.equal(pruned.kv[i].k, full.kv[i].k)

@@ -1,0 +1,287 @@
+"""Qwen3-shaped decoder stack for the gated prefill, on this package's gfx950 kernels.
+
+The reference runs Qwen3 through transformers' eager modules patched with its attention backends
+(qwen3_flex_attention.py:475-659): per layer RMSNorm -> q/k/v projections -> per-head q/k RMSNorm
+-> RoPE -> causal (Phase 1) or gate-biased (Phase 2) attention -> o_proj -> residual ->
+RMSNorm -> SwiGLU MLP -> residual.  Here a layer is five library GEMMs (fused QKV, O, fused
+gate/up, down; hipBLASLt through torch) and four launches of this package's kernels:
+tg_rmsnorm (residual add fused), tg_qk_norm_rope (q in place, k/v straight into the layer's KV
+cache rows), tg_keybias_varlen_fwd (every sequence of the batch in one launch, cu_seqlens
+layout, no padding), tg_silu_mul.  Tokens of all sequences are packed back to back, so Phase 1
+runs the ragged batch without the reference's right padding.
+
+Weights are bf16, generated from a seed (no checkpoint): the model is Qwen3-1.7B-shaped
+(28 layers, d 2048, 16/8 heads, head_dim 128, FFN 6144, vocab 151936, RoPE theta 1e6, tied
+embeddings), which is what the prefill measurements run.
+"""
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from tokengate_amd import _lib
+
+
+@dataclass(frozen=True)
+class DecoderShape:
+    n_layers: int = 28
+    d_model: int = 2048
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    d_ff: int = 6144
+    vocab: int = 151936
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e6
+    tie_embeddings: bool = True
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+QWEN3_1P7B = DecoderShape()
+
+
+@dataclass
+class LayerWeights:
+    ln1: torch.Tensor        # (d,) bf16 input_layernorm
+    w_qkv: torch.Tensor      # (qkv_dim, d) bf16 = [q_proj; k_proj; v_proj]
+    q_norm: torch.Tensor     # (head_dim,) bf16
+    k_norm: torch.Tensor     # (head_dim,) bf16
+    w_o: torch.Tensor        # (d, H*head_dim) bf16
+    ln2: torch.Tensor        # (d,) bf16 post_attention_layernorm
+    w_gu: torch.Tensor       # (2*d_ff, d) bf16 = [gate_proj; up_proj]
+    w_down: torch.Tensor     # (d, d_ff) bf16
+
+
+@dataclass
+class DecoderWeights:
+    shape: DecoderShape
+    embed: torch.Tensor      # (vocab, d) bf16
+    layers: List[LayerWeights]
+    final_norm: torch.Tensor
+    lm_head: torch.Tensor    # (vocab, d) bf16 (the embedding when tied)
+    inv_freq: torch.Tensor = field(default=None)   # (head_dim/2,) fp32 on the device
+
+    @property
+    def device(self) -> torch.device:
+        return self.embed.device
+
+
+def rope_inv_freq(shape: DecoderShape, device) -> torch.Tensor:
+    """1 / theta^(2i/D) in fp32, as Qwen3RotaryEmbedding's default initialisation computes it."""
+    exps = torch.arange(0, shape.head_dim, 2, dtype=torch.float32) / shape.head_dim
+    return (1.0 / (shape.rope_theta ** exps)).to(device)
+
+
+def random_decoder(shape: DecoderShape = QWEN3_1P7B, seed: int = 0, device="cuda", std: float = 0.02,
+                   norm_jitter: float = 0.0) -> DecoderWeights:
+    """Seeded random initialisation: linear / embedding weights N(0, std) (the transformers
+    initializer_range default), norm weights 1 (+ optional uniform jitter, so tests can see a
+    norm weight that is not 1)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    bf = torch.bfloat16
+
+    def lin(o, i):
+        return (torch.randn(o, i, generator=g, device=device) * std).to(bf)
+
+    def norm(n):
+        w = torch.ones(n, device=device)
+        if norm_jitter:
+            w += (torch.rand(n, generator=g, device=device) - 0.5) * 2 * norm_jitter
+        return w.to(bf)
+
+    d, D = shape.d_model, shape.head_dim
+    layers = [LayerWeights(norm(d), lin(shape.qkv_dim, d), norm(D), norm(D), lin(d, shape.n_heads * D), norm(d),
+                           lin(2 * shape.d_ff, d), lin(d, shape.d_ff)) for _ in range(shape.n_layers)]
+    embed = lin(shape.vocab, d)
+    lm_head = embed if shape.tie_embeddings else lin(shape.vocab, d)
+    return DecoderWeights(shape, embed, layers, norm(d), lm_head, rope_inv_freq(shape, device))
+
+
+# ---- fused per-token ops -----------------------------------------------------------------------
+
+def h2d(t: torch.Tensor, device) -> torch.Tensor:
+    """Asynchronous host -> device copy of a small host tensor (through pinned memory)."""
+    if torch.device(device).type != "cuda":
+        return t
+    return t.pin_memory().to(device, non_blocking=True)
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None,
+            residual_out: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out = RMSNorm(x + residual) (residual_out <- x + residual when given); rows of x are the
+    leading axis, last axis contiguous."""
+    out = torch.empty_like(x) if out is None else out
+    n, d = x.shape
+    _lib.call("tg_rmsnorm", x.data_ptr(), x.stride(0),
+              residual.data_ptr() if residual is not None else None,
+              residual.stride(0) if residual is not None else 0,
+              residual_out.data_ptr() if residual_out is not None else None,
+              residual_out.stride(0) if residual_out is not None else 0,
+              w.data_ptr(), out.data_ptr(), out.stride(0), n, d, float(eps), _stream(x))
+    return out
+
+
+def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, lw: LayerWeights, shape: DecoderShape,
+                 inv_freq: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor,
+                 q_head_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Normalises and rotates q in place inside qkv (returned as a (T, H, D) view) and writes the
+    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous)."""
+    T = qkv.shape[0]
+    H, Hkv, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    if positions.dtype != torch.int64 or positions.numel() != T:
+        raise RuntimeError("qk_norm_rope: positions must be int64 with one entry per token")
+    _lib.call("tg_qk_norm_rope", qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), T, H, Hkv, D,
+              lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), float(shape.rms_eps), inv_freq.data_ptr(),
+              q_head_scale.data_ptr() if q_head_scale is not None else None,
+              qkv.data_ptr(), qkv.stride(0), k_out.data_ptr(), k_out.stride(0), v_out.data_ptr(), v_out.stride(0),
+              _stream(qkv))
+    return qkv[:, :H * D].view(T, H, D) if qkv.is_contiguous() else qkv[:, :H * D].unflatten(1, (H, D))
+
+
+def silu_mul(gu: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    n, two_i = gu.shape
+    inter = two_i // 2
+    out = torch.empty(n, inter, dtype=gu.dtype, device=gu.device) if out is None else out
+    _lib.call("tg_silu_mul", gu.data_ptr(), gu.stride(0), n, inter, out.data_ptr(), out.stride(0), _stream(gu))
+    return out
+
+
+def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                     scale: float, bias_raw: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                     lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of every packed sequence in one launch (tg_keybias_varlen_fwd);
+    bias_raw (nseq, H, >= max_seqlen) fp32 in raw-score units (logit bias / scale) or None."""
+    T, H, D = q.shape
+    Hkv = k.shape[1]
+    out = torch.empty(T, H, D, dtype=q.dtype, device=q.device) if out is None else out
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device) if lse is None else lse
+    nseq = cu_seqlens.numel() - 1
+    if bias_raw is not None and (bias_raw.dtype != torch.float32 or bias_raw.stride(-1) != 1):
+        raise RuntimeError("varlen_attention: bias must be fp32 with a contiguous key axis")
+    _lib.call("tg_keybias_varlen_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              bias_raw.data_ptr() if bias_raw is not None else None, out.data_ptr(), lse.data_ptr(),
+              cu_seqlens.data_ptr(), nseq, int(max_seqlen), T, H, Hkv, D,
+              q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+              out.stride(0), out.stride(1),
+              bias_raw.stride(0) if bias_raw is not None else 0, bias_raw.stride(1) if bias_raw is not None else 0,
+              float(scale), 1, _stream(q))
+    return out
+
+
+# ---- layer runner ------------------------------------------------------------------------------
+
+@dataclass
+class Ragged:
+    """Token geometry of a packed batch: rows of sequence b are cu[b] .. cu[b+1]-1."""
+    cu: List[int]
+    cu_dev: torch.Tensor       # int32 (nseq + 1,) on the device
+    positions: torch.Tensor    # int64 (T,) RoPE position of every row
+    max_len: int
+
+    @property
+    def total(self) -> int:
+        return self.cu[-1]
+
+    @staticmethod
+    def from_lengths(lengths: List[int], device) -> "Ragged":
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + int(n))
+        cu_h = torch.tensor(cu, dtype=torch.int64)
+        cu_dev = h2d(cu_h.to(torch.int32), device)
+        # position of every row = row - first row of its sequence, built on the device
+        T = cu[-1]
+        lens_d = h2d(torch.tensor([int(n) for n in lengths], dtype=torch.int64), device)
+        starts_d = h2d(cu_h[:-1].clone(), device)
+        pos = torch.arange(T, dtype=torch.int64, device=device) - torch.repeat_interleave(starts_d, lens_d,
+                                                                                           output_size=T)
+        return Ragged(cu, cu_dev, pos, max(lengths, default=0))
+
+
+@dataclass
+class LayerKV:
+    k: torch.Tensor   # (rows, Hkv, D) bf16: the layer's cache, rows in the ragged layout
+    v: torch.Tensor
+
+
+class Workspace:
+    """Activation buffers reused across the layers of one phase (sized for `rows` tokens; the
+    MLP intermediates for `mlp_rows`)."""
+
+    def __init__(self, shape: DecoderShape, rows: int, device, mlp_rows: Optional[int] = None):
+        bf = torch.bfloat16
+        self.rows = rows
+        self.mlp_rows = min(rows, mlp_rows or rows)
+        d = shape.d_model
+        self.residual = torch.empty(rows, d, dtype=bf, device=device)
+        self.normed = torch.empty(rows, d, dtype=bf, device=device)
+        self.hidden = torch.empty(rows, d, dtype=bf, device=device)
+        self.qkv = torch.empty(rows, shape.qkv_dim, dtype=bf, device=device)
+        self.attn = torch.empty(rows, shape.n_heads, shape.head_dim, dtype=bf, device=device)
+        self.lse = torch.empty(shape.n_heads * rows, dtype=torch.float32, device=device)
+        self.gu = torch.empty(self.mlp_rows, 2 * shape.d_ff, dtype=bf, device=device)
+        self.act = torch.empty(self.mlp_rows, shape.d_ff, dtype=bf, device=device)
+
+
+def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws: Workspace,
+               kv: List[Optional[LayerKV]], biases=None, q_scales=None, capture: Optional[list] = None) -> torch.Tensor:
+    """Runs decoder layers `layer_ids` over the packed rows x (T, d) and returns the hidden state
+    after the last of them (T, d).  kv[i] receives layer i's cache rows.  biases[i] / q_scales[i]
+    (optional): Phase-2 raw-unit key bias (nseq, H, >= max_len) and per-head query scale (H,)
+    fp32 of layer i.  capture: optional list that receives each layer's input hidden state."""
+    shape = wts.shape
+    T = geo.total
+    if x.shape != (T, shape.d_model):
+        raise RuntimeError("run_layers: x must be (total_rows, d_model)")
+    eps = shape.rms_eps
+    scale = 1.0 / math.sqrt(shape.head_dim)
+    res, normed, hid = ws.residual[:T], ws.normed[:T], ws.hidden[:T]
+    qkv, attn, lse = ws.qkv[:T], ws.attn[:T], ws.lse[:shape.n_heads * T].view(shape.n_heads, T)
+    first = True
+    for i in layer_ids:
+        lw = wts.layers[i]
+        if first:
+            res.copy_(x)
+            rmsnorm(res, lw.ln1, eps, out=normed)
+            first = False
+        else:
+            rmsnorm(hid, lw.ln1, eps, residual=res, residual_out=res, out=normed)
+        if capture is not None:
+            capture.append(res.clone())
+        torch.matmul(normed, lw.w_qkv.t(), out=qkv)
+        q = qk_norm_rope(qkv, geo.positions, lw, shape, wts.inv_freq, kv[i].k, kv[i].v,
+                         q_scales[i] if q_scales is not None else None)
+        varlen_attention(q, kv[i].k, kv[i].v, geo.cu_dev, geo.max_len, scale,
+                         biases[i] if biases is not None else None, out=attn, lse=lse)
+        torch.matmul(attn.view(T, -1), lw.w_o.t(), out=hid)
+        rmsnorm(hid, lw.ln2, eps, residual=res, residual_out=res, out=normed)
+        for r0 in range(0, T, ws.mlp_rows):
+            r1 = min(T, r0 + ws.mlp_rows)
+            gu = ws.gu[:r1 - r0]
+            torch.matmul(normed[r0:r1], lw.w_gu.t(), out=gu)
+            act = silu_mul(gu, out=ws.act[:r1 - r0])
+            torch.matmul(act, lw.w_down.t(), out=hid[r0:r1])
+    out = torch.empty_like(hid)
+    torch.add(hid, res, out=out)
+    return out
+
+
+def alloc_kv(shape: DecoderShape, rows: int, device) -> LayerKV:
+    return LayerKV(torch.empty(rows, shape.n_kv_heads, shape.head_dim, dtype=torch.bfloat16, device=device),
+                   torch.empty(rows, shape.n_kv_heads, shape.head_dim, dtype=torch.bfloat16, device=device))
+
+
+def logits_last(wts: DecoderWeights, h: torch.Tensor, last_rows: torch.Tensor) -> torch.Tensor:
+    """Final norm + LM head on the given rows only (the rows that produce the next token)."""
+    rows = h.index_select(0, last_rows)
+    normed = rmsnorm(rows, wts.final_norm, wts.shape.rms_eps)
+    return F.linear(normed, wts.lm_head).float()

@@ -177,3 +177,53 @@ def keep_indices(scores_art: torch.Tensor, K: int, article_start: int, article_e
     p = plan([0], [seq_len], [article_start], [article_end], [K], scores_art.device)
     keep, _ = select_keep(full, p, with_sumsq=False)
     return keep
+
+
+@dataclass
+class ScoringHead:
+    """The gate's parameters for one prefill.
+
+    Scoring: score_j = w2 . silu(W1 x_j + b1) + b2 on the gate layer's hidden state (the
+    Linear(2048->256) -> SiLU -> Linear(256->1) head of the 32k gate workload).  Bias: the kept
+    article rows' scores RMS-normalised over the article (E2EGate.forward,
+    e2e_gate_module.py:348-385, eps 1e-6 :74), times softplus(gate_scale[l, h]) per Phase-2 layer
+    l and query head h; the attention temperature softplus(attn_scale[l, h]) (attn_scale_eff
+    :302-305) multiplies both the query and the bias (_phase2_q_bias,
+    qwen3_flex_attention.py:433-473, per-head branch).  Top-K ranks the raw score: the
+    reference's selection key (aggregate :387-399) is a positive multiple of it."""
+    w1: torch.Tensor            # (256, 2048) bf16
+    b1: torch.Tensor            # (256,) fp32
+    w2: torch.Tensor            # (256,) fp32
+    b2: float
+    gate_scale: torch.Tensor    # (n_phase2_layers, H) fp32, pre-softplus
+    attn_scale: Optional[torch.Tensor] = None   # (n_phase2_layers, H) fp32, pre-softplus
+
+    def scores(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        return score_mlp(x, self.w1, self.b1, self.w2, self.b2, out=out)
+
+    def layer_coefficients(self, softmax_scale: float) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """(bias coefficient in raw-score units, per-head query scale) per (layer, head):
+        raw bias of key j = normalised score_j * softplus(gate_scale) * temperature / softmax_scale."""
+        coef = torch.nn.functional.softplus(self.gate_scale.float())
+        qs = None
+        if self.attn_scale is not None:
+            qs = torch.nn.functional.softplus(self.attn_scale.float()).contiguous()
+            coef = coef * qs
+        return (coef / softmax_scale).contiguous(), qs
+
+
+def random_head(n_layers: int, n_heads: int, seed: int = 5, device="cuda", d_in: int = 2048, d_hidden: int = 256,
+                gate_scale: Optional[float] = None, temperature: bool = True) -> ScoringHead:
+    """Seeded head: Xavier-uniform W1 / w2, zero b1 / b2; gate_scale = softplus^-1(1.0) (or a
+    given value) plus a small seeded spread per (layer, head); attn_scale = softplus^-1(1), the
+    identity temperature E2EGate starts from."""
+    import math
+    g = torch.Generator(device=device).manual_seed(seed)
+    a1 = math.sqrt(6.0 / (d_in + d_hidden))
+    w1 = ((torch.rand(d_hidden, d_in, generator=g, device=device) * 2 - 1) * a1).to(torch.bfloat16)
+    w2 = (torch.rand(d_hidden, generator=g, device=device) * 2 - 1) * math.sqrt(6.0 / (d_hidden + 1))
+    b1 = torch.zeros(d_hidden, device=device)
+    base = math.log(math.expm1(1.0)) if gate_scale is None else gate_scale
+    gs = base + 0.1 * torch.randn(n_layers, n_heads, generator=g, device=device)
+    at = torch.full((n_layers, n_heads), math.log(math.expm1(1.0)), device=device) if temperature else None
+    return ScoringHead(w1, b1, w2, 0.0, gs, at)

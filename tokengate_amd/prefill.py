@@ -1,0 +1,165 @@
+"""Gated prefill of a ragged batch: Phase 1 -> score -> top-K keep -> pack -> Phase 2 -> first token.
+
+Follows prefill_batch_for_decode (tokengate/e2e_gate/gate_module/gate_forward.py:1280-1580):
+layers 0..gate_layer run over every prompt token (:1334-1366); the gate scores the gate layer's
+hidden state and keeps, per sequence, its prefix, the K_clamped = max(1, min(K, n_art))
+highest-scoring state tokens in original order, and its suffix (:1378-1421); the kept hidden rows,
+their original positions and their gate bias are gathered (:1435-1470); layers gate_layer+1..
+run on the kept rows with RoPE at the original positions and the per-(layer, head) gate bias
+(:1478-1560, _apply_gate_bias :588-662); the first token is the argmax of the LM head at each
+sequence's last row (:1560-1580).  Layers at or below the gate keep their full Phase-1 KV cache
+(prune_below_gate=False, the reference default); prune_below_gate=True packs it down to the kept
+rows in the same launch that packs the hidden states.
+
+MI355X layout: the batch is never padded.  Phase 1 packs all prompts back to back (cu_seqlens)
+and runs one varlen attention launch per layer; the keep lists of all sequences come from one
+top-K launch and every gather from one pack launch; Phase 2 runs the packed kept rows, with
+the -1e9 pad-slot bias of the reference replaced by the cu_seqlens boundaries.  Every size is
+known on the host from the prompt lengths, spans and K, so nothing synchronises before the
+first token.
+"""
+import math
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+from tokengate_amd import gate as G
+from tokengate_amd.decoder import (DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, h2d, logits_last,
+                                   run_layers)
+
+
+@dataclass
+class PrefillResult:
+    first_tokens: torch.Tensor        # (B,) int64 on the device
+    kept_positions: torch.Tensor      # (total_kept,) int64, packed (cu_kept layout)
+    cu_kept: List[int]
+    n_kept: List[int]
+    k_clamped: List[int]
+    kv: List[LayerKV]                 # per layer: Phase-1 rows (cu_prompt) at/below the gate, kept rows above
+    cu_prompt: List[int]
+    kept_bias: torch.Tensor           # (total_kept,) fp32 normalised gate score (0 on prefix / suffix)
+    phase_ms: Dict[str, float] = field(default_factory=dict)
+    capture: Optional[dict] = None
+
+
+def _cat_ids(ids_list: Sequence, device) -> torch.Tensor:
+    if all(torch.is_tensor(x) for x in ids_list):
+        return torch.cat([x.reshape(-1).to(device=device, dtype=torch.long) for x in ids_list])
+    flat = [int(t) for ids in ids_list for t in (ids.tolist() if torch.is_tensor(ids) else ids)]
+    return h2d(torch.tensor(flat, dtype=torch.long), device)
+
+
+@torch.no_grad()
+def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, art_starts: Sequence[int],
+                  art_ends: Sequence[int], gate_layer: int, K, prune_below_gate: bool = False,
+                  phase_timing: bool = False, capture: bool = False, mlp_rows: int = 131072) -> PrefillResult:
+    """ids_list: B prompts (lists of ints or 1-D tensors); the state span of prompt b is
+    [art_starts[b], art_ends[b]); K: scalar or per-prompt list."""
+    shape = wts.shape
+    dev = wts.device
+    B = len(ids_list)
+    if B == 0:
+        raise ValueError("empty batch")
+    n_layers = shape.n_layers
+    if not 0 <= gate_layer < n_layers - 1:
+        raise ValueError(f"gate_layer {gate_layer} must leave at least one layer above it")
+    if head.gate_scale.shape != (n_layers - gate_layer - 1, shape.n_heads):
+        raise ValueError("head.gate_scale must be (layers above the gate, num_heads)")
+    lens = [int(x.numel()) if torch.is_tensor(x) else len(x) for x in ids_list]
+    if min(lens) < 1:
+        raise ValueError("every prompt needs at least one token")
+    ev = [] if phase_timing else None
+
+    def mark(name):
+        if ev is not None:
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            ev.append((name, e))
+
+    cap = {"phase1": [], "phase2": []} if capture else None
+    mark("phase1")
+    ids = _cat_ids(ids_list, dev)
+    geo1 = Ragged.from_lengths(lens, dev)
+    T = geo1.total
+    x = torch.nn.functional.embedding(ids, wts.embed)
+    ws1 = Workspace(shape, T, dev, mlp_rows=mlp_rows)
+    kv: List[Optional[LayerKV]] = [None] * n_layers
+    for i in range(gate_layer + 1):
+        kv[i] = alloc_kv(shape, T, dev)
+    h = run_layers(wts, range(gate_layer + 1), x, geo1, ws1, kv, capture=cap["phase1"] if cap else None)
+    del x
+
+    mark("score+select")
+    scores = head.scores(h)
+    p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
+    keep, sumsq = G.select_keep(scores, p)
+
+    mark("pack")
+    T2 = p.total_kept
+    hs = torch.empty(T2, shape.d_model, dtype=h.dtype, device=dev)
+    kept_pos = torch.empty(T2, dtype=torch.int64, device=dev)
+    kept_bias = torch.empty(T2, dtype=torch.float32, device=dev)
+    pairs = [(h, hs)]
+    if prune_below_gate:
+        for i in range(gate_layer + 1):
+            nk = alloc_kv(shape, T2, dev)
+            pairs += [(kv[i].k, nk.k), (kv[i].v, nk.v)]
+            kv[i] = nk
+    G.pack(keep, p, pairs, positions=kept_pos, bias_src=scores, sumsq=sumsq, bias_out=kept_bias)
+    if cap is not None:
+        cap["h1"] = h
+    del h, ws1, pairs
+
+    mark("phase2")
+    max_kept = max(p.n_kept)
+    # per-sequence padded view of the packed bias: row b, column t <- packed row cu_kept[b] + t
+    t_ = torch.arange(max_kept, dtype=torch.int64)
+    st = torch.tensor(p.cu_kept[:-1], dtype=torch.int64)[:, None]
+    en = torch.tensor(p.cu_kept[1:], dtype=torch.int64)[:, None] - 1
+    idx = torch.minimum(st + t_[None, :], en)
+    bias_pad = kept_bias[h2d(idx, dev)]                     # (B, max_kept)
+    coef, qscale = head.layer_coefficients(1.0 / math.sqrt(shape.head_dim))  # (L2, H)
+    biases_all = coef[:, None, :, None] * bias_pad[None, :, None, :]       # (L2, B, H, max_kept)
+    geo2 = Ragged(p.cu_kept, h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev), kept_pos,
+                  max_kept)
+    above = list(range(gate_layer + 1, n_layers))
+    biases = {l: biases_all[j] for j, l in enumerate(above)}
+    qs = {l: qscale[j] for j, l in enumerate(above)} if qscale is not None else None
+    for l in above:
+        kv[l] = alloc_kv(shape, T2, dev)
+    ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
+    h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
+                    capture=cap["phase2"] if cap else None)
+
+    mark("head")
+    last = h2d(torch.tensor(p.cu_kept[1:], dtype=torch.int64).sub_(1), dev)
+    logits = logits_last(wts, h2, last)
+    first = logits.argmax(-1)
+    mark("end")
+    phase_ms = {}
+    if ev is not None:
+        torch.cuda.synchronize()
+        for (n0, e0), (_, e1) in zip(ev[:-1], ev[1:]):
+            phase_ms[n0] = e0.elapsed_time(e1)
+    if cap is not None:
+        cap.update(scores=scores, keep=keep, hs_packed=hs, h2=h2, logits=logits, biases_all=biases_all,
+                   qscale=qscale, bias_pad=bias_pad)
+    return PrefillResult(first, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, phase_ms, cap)
+
+
+def ttft_ms(fn, reps: int = 5, warmup: int = 1) -> List[float]:
+    """Time-to-first-token protocol of the reference's TTFT bench (bench_ttft.py:312-359): device
+    sync, perf_counter, the whole prefill, device sync; warmup calls first, then `reps` timed
+    calls back to back.  Returns every repeat in ms."""
+    for _ in range(warmup):
+        fn()
+    out = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        out.append((time.perf_counter() - t0) * 1e3)
+    return out
