@@ -39,7 +39,7 @@ struct BwdArgs {
   int64_t bias_bs, bias_hs, dbias_bs, dbias_hs;
   int64_t lse_total;       // varlen: lse / softmax_d are (H, total)
   int batch, sq, sk, h, hkv, group;
-  int n_tiles;             // grid decomposition (q tiles for dQ, key tiles for dK/dV)
+  int n_tiles;             // grid decomposition (q tiles for dQ, key tiles for dK/dV; set per launch)
   float scale, scale_log2;
 };
 
@@ -126,8 +126,9 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   const int per_q = a.hkv * hgroups;
   const int x = blockIdx.x % per_q, rest = blockIdx.x / per_q;
   const int kh = x % a.hkv, hg = x / a.hkv;
-  const int b = rest % a.batch;
-  const int qt = a.n_tiles - 1 - rest / a.batch;
+  // varlen: sequence-major (resident workgroups share one sequence's K/V in L2 / MALL)
+  const int b = VARLEN ? rest / a.n_tiles : rest % a.batch;
+  const int qt = a.n_tiles - 1 - (VARLEN ? rest % a.n_tiles : rest / a.batch);
   const Seq sq_ = seq_of<VARLEN>(a, b);
   const int sq = sq_.sq, sk = sq_.sk;
   const int64_t row0 = sq_.row0;
@@ -314,8 +315,8 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
   // heaviest first: under the causal mask the first key tiles see the most queries
   const int kh = blockIdx.x % a.hkv;
   const int rest = blockIdx.x / a.hkv;
-  const int b = rest % a.batch;
-  const int kt = rest / a.batch;
+  const int b = VARLEN ? rest / a.n_tiles : rest % a.batch;   // varlen: sequence-major
+  const int kt = VARLEN ? rest % a.n_tiles : rest / a.batch;
   const Seq sq_ = seq_of<VARLEN>(a, b);
   const int sq = sq_.sq, sk = sq_.sk;
   const int64_t row0 = sq_.row0;
@@ -502,6 +503,7 @@ void launch_bwd(const BwdArgs &a0, bool causal, bool has_bias, int64_t nrows, hi
   TG_DQ(1, true, true) TG_DQ(1, true, false) TG_DQ(1, false, true) TG_DQ(1, false, false)
 #undef TG_DQ
   const int nkt = (a.sk + kKBlock - 1) / kKBlock;
+  a.n_tiles = nkt;
   const unsigned nk = (unsigned)((int64_t)nkt * a.batch * a.hkv);
 #define TG_DKV(C, B)                                                                                   \
   if (causal == C && has_bias == B)                                                                    \

@@ -103,8 +103,11 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
   const int rest = bid / per_q;
   const int kh = x % a.hkv;
   const int hg = x / a.hkv;
-  const int b = rest % a.batch;
-  const int qt = a.n_qtiles - 1 - rest / a.batch;
+  // Dense: heaviest q tile of every batch row first.  Varlen: sequence-major (all tiles of
+  // sequence b before sequence b+1, heaviest first within it), so the workgroups resident at one
+  // time share one sequence's K/V in L2 / MALL instead of streaming every sequence's K/V at once.
+  const int b = VARLEN ? rest / a.n_qtiles : rest % a.batch;
+  const int qt = a.n_qtiles - 1 - (VARLEN ? rest % a.n_qtiles : rest / a.batch);
 
   int sq = a.sq, sk = a.sk;
   int64_t row0 = 0;
