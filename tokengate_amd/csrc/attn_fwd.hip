@@ -227,14 +227,21 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
         for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
       }
     }
+    // all 16 K fragments of the tile are read before the first MFMA, so LDS latency is paid once
+    bf16x8 kfr[8][2];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int lr = 32 * kb + lq;
-        const bf16x8 kf = lds_load16(ks[buf], lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
-        sacc[kb] = mfma32(kf, qf[s], sacc[kb]);
+        kfr[s][kb] = lds_load16(ks[buf], lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) sacc[kb] = mfma32(kfr[s][kb], qf[s], sacc[kb]);
     }
 
     // ---- online softmax: one (head, query) column per lane, 32 keys per lane ----
@@ -260,7 +267,7 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
       m8[i] = fmaxf(fmaxf(tv[i >> 2][4 * (i & 3)], tv[i >> 2][4 * (i & 3) + 1]),
                     fmaxf(tv[i >> 2][4 * (i & 3) + 2], tv[i >> 2][4 * (i & 3) + 3]));
     float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
-    mx = pair_max(mx) * a.scale_log2;     // tile max in log2 units (-inf if fully masked)
+    mx = half_swap_max(mx) * a.scale_log2;   // tile max in log2 units (-inf if fully masked)
     if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleTau) != 0) {
       const float m_new = fmaxf(mrun, mx);
       // 0 on the first visible tile; rows that have seen no key yet (m_new = -inf) keep 1.

@@ -63,6 +63,13 @@ __device__ __forceinline__ u32x4 gload16(const bf16_t *p, bool valid) {
 
 // Combine a value held by lane l and lane l^32 (the two halves of a wave64).
 __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+// Same as pair_max without the LDS crossbar: v_permlane32_swap(x, x) returns (lower half in both
+// halves, upper half in both halves), so the max of the two is max(x[l], x[l^32]) in every lane.
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                   false, false);
+  return fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1]));
+}
 __device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
 
 // ---- buffer resources and LDS DMA (gfx950) --------------------------------------------------
