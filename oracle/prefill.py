@@ -154,3 +154,73 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
     logits = rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()
     return dict(first_tokens=logits.argmax(-1), logits=logits, keep=keeps, h_gate=h_gate, h_last=xx,
                 kept_bias=biases)
+
+
+def layer_with_past(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, k_past: torch.Tensor,
+                    v_past: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
+                    q_temp: Optional[torch.Tensor] = None):
+    """One decoder layer for new rows x (1, n, d) at positions pos (1, n) that attend over cached
+    keys / values k_past, v_past (1, m, Hkv, D) and then over themselves causally; bias_logit
+    (1, H, m + n) per key (past then new) or None.  Returns (x_out, k_new, v_new)."""
+    s = W.shape
+    L = W.layers[i]
+    _, n, _ = x.shape
+    H, Hkv, D = s.n_heads, s.n_kv_heads, s.head_dim
+    h = rms(x, L["ln1"], s.rms_eps)
+    q = rms((h @ L["wq"].t()).view(1, n, H, D), L["q_norm"], s.rms_eps)
+    k = rms((h @ L["wk"].t()).view(1, n, Hkv, D), L["k_norm"], s.rms_eps)
+    v = (h @ L["wv"].t()).view(1, n, Hkv, D)
+    cos, sin = rope_cos_sin(pos, W.inv_freq)
+    cos, sin = cos[:, :, None, :], sin[:, :, None, :]
+    q = q * cos + rotate_half(q) * sin
+    k = k * cos + rotate_half(k) * sin
+    scale = 1.0 / math.sqrt(D)
+    braw = None
+    if bias_logit is not None:
+        bl = bias_logit * q_temp[None, :, None] if q_temp is not None else bias_logit
+        braw = bl / scale
+    if q_temp is not None:
+        q = q * q_temp[None, None, :, None]
+    attn, _ = oat.fwd(q, torch.cat([k_past, k], 1), torch.cat([v_past, v], 1), braw, scale, causal=True)
+    x = x + attn.reshape(1, n, H * D) @ L["wo"].t()
+    h = rms(x, L["ln2"], s.rms_eps)
+    x = x + (F.silu(h @ L["wg"].t()) * (h @ L["wu"].t())) @ L["wd"].t()
+    return x, k, v
+
+
+def decode_logits(W: Weights, head, ids: Sequence[int], art_start: int, art_end: int, gate_layer: int,
+                  keep: np.ndarray, gen: Sequence[int], prune_below_gate: bool = False):
+    """Teacher-forced logits of the reference's decode for one sample (generate_batch,
+    gate_decode.py:88-262, default form): the generated tokens, at positions last kept position
+    + 1, + 2, ..., go through layers 0..gate_layer attending over the prompt's cache at those
+    layers (every prompt row, or only the kept rows with prune_below_gate) and through the layers
+    above over the kept rows, where prompt keys keep their gate bias and generated keys carry 0.
+    Returns (1 + len(gen), vocab): the logits after the last kept row (the first token) and after
+    each generated token."""
+    s = W.shape
+    L, g = len(ids), len(gen)
+    kp = torch.as_tensor(np.asarray(keep, dtype=np.int64))
+    nxt = int(kp[-1]) + 1
+    gpos = (nxt + torch.arange(g))[None]
+    x = W.embed[torch.as_tensor(list(ids), dtype=torch.long)][None]
+    xg = W.embed[torch.as_tensor(list(gen), dtype=torch.long)][None]
+    pos = torch.arange(L)[None]
+    for i in range(gate_layer + 1):
+        xn, k, v = layer(W, i, x, pos)
+        if prune_below_gate:
+            k, v = k[:, kp], v[:, kp]
+        if g:
+            xg, _, _ = layer_with_past(W, i, xg, gpos, k, v)
+        x = xn
+    sc = head_scores(head, x[0, art_start:art_end])
+    kb = torch.as_tensor(og.gate_bias(sc, np.asarray(keep), art_start, art_end), dtype=torch.float32)
+    gb = torch.cat([kb, torch.zeros(g)])
+    xx = torch.cat([x[0, kp], xg[0]])[None]
+    pos2 = torch.cat([kp[None], gpos], 1)
+    gs = F.softplus(head.gate_scale.float().cpu())
+    at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
+    for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
+        bl = gb[None, None, :] * gs[j][None, :, None]
+        xx, _, _ = layer(W, i, xx, pos2, bias_logit=bl, q_temp=at[j] if at is not None else None)
+    rows = xx[0, len(kp) - 1:]
+    return rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()

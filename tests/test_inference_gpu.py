@@ -1,0 +1,105 @@
+"""GPU checks of load_model().generate(): the greedy decode over the pruned caches against the
+oracle's teacher-forced decode (oracle.prefill.decode_logits: generated tokens through layers
+0..gate over the full prompt and through the layers above over the kept rows, prompt keys
+keeping their gate bias), logits within max-abs 2e-2 (relative to max(1, |ref|)) and rel-L2
+3e-2 (several bf16 layers); and the generate() contract: first-EOS truncation, the streamer,
+kept positions, per-sequence K, prune_below_gate."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import prefill as op
+from tests.attn_util import assert_close_grad, to_np
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=4, d_model=2048, n_heads=16, n_kv_heads=8, head_dim=128, d_ff=1024, vocab=512)
+
+
+def _model(cuda, seed=3):
+    from tokengate_amd import decoder as dec
+    from tokengate_amd import inference as I
+    return I.load_model(f"random:{seed}", gate_layer=1, device=cuda, shape=dec.DecoderShape(**SMALL))
+
+
+def _prompts(lens, spans, seed):
+    from tokengate_amd import inference as I
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for n, (s, e) in zip(lens, spans):
+        ids = torch.randint(3, SMALL["vocab"], (n,), generator=g).tolist()
+        out.append(ids[:s] + [I.STATE_START_ID] + ids[s:e] + [I.STATE_END_ID] + ids[e:])
+    return out
+
+
+@pytest.mark.parametrize("prune_below_gate", [False, True])
+def test_decode_matches_oracle(cuda, prune_below_gate):
+    from tokengate_amd import inference as I
+    from tokengate_amd.decode import DecodeState
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    m = _model(cuda)
+    lens, spans, Ks = [600, 333], [(20, 500), (0, 300)], [64, 1000]
+    split = [I.split_state_span(p) for p in _prompts(lens, spans, 5)]
+    pf = m.prefill(split, Ks, prune_below_gate=prune_below_gate)
+    steps = 4
+    st = DecodeState(m.weights, m.gate, m.gate_layer, pf, steps + 1, prune_below_gate)
+    cur = pf.first_tokens
+    toks, logits = [cur], []
+    for _ in range(steps):
+        cur = st.step(cur)
+        toks.append(cur)
+        logits.append(st.last_logits.float().cpu())
+    torch.cuda.synchronize()
+    W = op.Weights(m.weights)
+    kp = pf.kept_positions.cpu().numpy()
+    for b, (clean, s, e) in enumerate(split):
+        keep = kp[pf.cu_kept[b]:pf.cu_kept[b + 1]]
+        gen = [int(t[b]) for t in toks[:steps]]      # tokens fed to the decode steps
+        ref = op.decode_logits(W, m.gate, clean, s, e, m.gate_layer, keep, gen, prune_below_gate)
+        for i in range(steps):
+            assert_close_grad(f"seq {b} step {i}", to_np(logits[i][b]), to_np(ref[1 + i]), rel_l2=3e-2)
+            assert int(toks[i + 1][b]) == int(logits[i][b].argmax())
+
+
+class _Tok:
+    def __init__(self, eos):
+        self.eos_token_id = eos
+
+    def decode(self, ids, skip_special_tokens=True):
+        return " ".join(str(i) for i in ids)
+
+
+class _Streamer:
+    def __init__(self):
+        self.rows, self.ended = [], False
+
+    def put(self, t):
+        self.rows.append(t.clone())
+
+    def end(self):
+        self.ended = True
+
+
+def test_generate_contract(cuda):
+    from tokengate_amd import inference as I
+    m = _model(cuda, seed=4)
+    prompts = _prompts([400, 250], [(10, 380), (5, 240)], 9)
+    free = m.generate(prompts, None, max_new_tokens=6, max_kept_prefill_tokens=[50, 10_000])
+    assert free.answers == ["", ""] and all(len(t) == 6 for t in free.token_ids)
+    assert free.n_state == [370, 235]
+    assert free.n_kept == [10 + 50 + 20, 250]
+    for b, (clean, s, e) in enumerate(I.split_state_span(p) for p in prompts):
+        kp = free.kept_pos[b]
+        assert kp == sorted(kp) and kp[:s] == list(range(s)) and kp[len(kp) - (len(clean) - e):] == list(range(e, len(clean)))
+    # EOS = the token sequence 0 produced at step 2: its row stops there, the batch runs on
+    eos = free.token_ids[0][2]
+    streamer = _Streamer()
+    out = m.generate(prompts, _Tok(eos), max_new_tokens=6, max_kept_prefill_tokens=[50, 10_000], streamer=streamer)
+    assert out.token_ids[0] == free.token_ids[0][:free.token_ids[0].index(eos) + 1]
+    assert out.answers[0] == " ".join(str(t) for t in free.token_ids[0][:free.token_ids[0].index(eos)])
+    assert streamer.ended and all(r.shape == (2, 1) for r in streamer.rows)
+    got = [int(r[0, 0]) for r in streamer.rows]
+    assert got == free.token_ids[0][:len(got)] and len(got) > free.token_ids[0].index(eos)
+    assert out.prefill_s > 0 and out.decode_s >= 0
+    with pytest.raises(ValueError):
+        m.generate([[1, 2, 3]], None)

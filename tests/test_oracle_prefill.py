@@ -205,3 +205,32 @@ def test_keep_lists_and_bias_follow_gate_oracle():
         assert np.array_equal(kp, r["keep"][b])
         assert len(kp) == starts[b] + og.k_clamped(Ks[b], ends[b] - starts[b]) + lens[b] - ends[b]
         np.testing.assert_allclose(r["kept_bias"][b], og.gate_bias(sc, kp, starts[b], ends[b]))
+
+
+def test_decode_oracle_first_row_equals_prefill_and_past_form():
+    """decode_logits' first row is the prefill's first-token logits; with no pruning below the gate
+    and K >= the span, its rows equal a plain causal pass over prompt ++ generated."""
+    s = Shape(n_layers=3)
+    W = op.Weights(_wts(s, seed=10))
+    head = _head(s, seed=11)
+    head.gate_scale = torch.randn(2, s.n_heads) * 0.3
+    head.attn_scale = torch.randn(2, s.n_heads) * 0.3
+    ids = _prompts([50], s.vocab, 12)[0]
+    r = op.prefill(W, head, [ids], [5], [40], 0, [10])
+    keep = r["keep"][0]
+    gen = [7, 3, 9]
+    for prune in (False, True):
+        d = op.decode_logits(W, head, ids, 5, 40, 0, keep, gen, prune_below_gate=prune)
+        assert _rel(d[0], r["logits"][0]) < 1e-5
+    # K >= span and zero gate bias: the gated decode is the plain model on prompt ++ generated
+    head.gate_scale = torch.full((2, s.n_heads), -30.0)
+    head.attn_scale = None
+    full = op.prefill(W, head, [ids], [5], [40], 0, [1000])
+    keep = full["keep"][0]
+    d = op.decode_logits(W, head, ids, 5, 40, 0, keep, gen)
+    x = W.embed[torch.as_tensor(ids + gen)][None]
+    pos = torch.arange(len(ids) + len(gen))[None]
+    for i in range(s.n_layers):
+        x, _, _ = op.layer(W, i, x, pos)
+    ref = op.rms(x[0, len(ids) - 1:], W.final_norm, s.rms_eps) @ W.lm_head.t()
+    assert _rel(d, ref) < 1e-5
