@@ -74,11 +74,31 @@ def test_heavy_ties(cuda, kind):
 
 
 def test_long_article_global_path(cuda):
-    """Articles longer than the LDS-resident limit (32768 keys) take the global-memory variant."""
+    """Articles longer than the register-resident limit (65536 keys) take the streaming variant
+    (32768-key chunks re-read on every pass)."""
     rng = np.random.default_rng(2)
     L = 100_000
     s = torch.from_numpy(rng.standard_normal(2 * L).astype(np.float32)).to(torch.bfloat16).float().numpy()
     seqs = [(0, L, 64, L - 256, 4000), (L, L, 0, L, 50_000)]
+    _check_select(s, seqs, cuda)
+
+
+@pytest.mark.parametrize("kind", ["few_values", "bf16_normal"])
+def test_streaming_ties_across_chunks(cuda, kind):
+    """Ties at the threshold spread over several 32768-key chunks (the compaction carries the tie
+    and output counts from chunk to chunk); a ragged batch whose longest article forces the
+    streaming variant on every sequence, short ones included."""
+    rng = np.random.default_rng(4)
+    lens = [200_003, 70_000, 5, 40_000]
+    n = sum(lens)
+    if kind == "few_values":
+        s = rng.integers(0, 7, n).astype(np.float32)
+    else:
+        s = torch.from_numpy(rng.standard_normal(n).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    seqs, r0 = [], 0
+    for L, K in zip(lens, [60_000, 9_999, 2, 35_000]):
+        seqs.append((r0, L, 1, L - 1 if L > 2 else L, K))
+        r0 += L
     _check_select(s, seqs, cuda)
 
 

@@ -134,7 +134,6 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
 // ---------------------------------------------------------------------------------------------
 constexpr int kTThreads = 1024;
 constexpr int kTWaves = kTThreads / 64;
-constexpr int kTLdsKeys = 32768;
 
 // float -> uint32 whose unsigned order is the float order; -0 == +0; NaN above +inf.  Branch-free
 // (selects only) so that it can run over register-resident key arrays.
@@ -148,172 +147,6 @@ __device__ __forceinline__ uint32_t order_key(float f) {
 
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
-template <bool IN_LDS>
-__global__ __launch_bounds__(kTThreads, 1) void gate_topk_kernel(const float *scores, const int32_t *geom,
-                                                                 int64_t *keep, float *sumsq) {
-  __shared__ uint32_t keys_lds[IN_LDS ? kTLdsKeys : 1];
-  __shared__ int hist[kTWaves][256];
-  __shared__ int htot[256];
-  __shared__ int wgt[kTWaves], weq[kTWaves];
-  __shared__ uint32_t sel[2];   // prefix, k_rem
-  __shared__ float red[kTWaves];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int32_t *gm = geom + 6 * blockIdx.x;
-  const int64_t row_start = gm[0];
-  const int seq_len = gm[1], s = gm[2], e = gm[3], kc = gm[4];
-  const int64_t kept0 = gm[5];
-  const int n = e - s;
-  const float *sc = scores + row_start + s;
-
-  // prefix and suffix positions
-  for (int i = tid; i < s; i += kTThreads) keep[kept0 + i] = i;
-  for (int i = tid; i < seq_len - e; i += kTThreads) keep[kept0 + s + kc + i] = e + i;
-  if (n <= 0 || kc <= 0) {
-    if (tid == 0 && sumsq) sumsq[blockIdx.x] = 0.f;
-    return;
-  }
-
-  // keys (LDS-resident when they fit) and the article's sum of squares.  The LDS variant issues
-  // every score load as LDS DMA at once (n / 1024 per thread in flight), then converts in place.
-  float ss = 0.f;
-  if constexpr (IN_LDS) {
-    const brsrc_t srs = make_rsrc(sc, (uint32_t)n * 4u);
-    for (int base = 0; base < n; base += kTThreads)
-      dma4(srs, &keys_lds[base + 64 * wave], (uint32_t)(base + tid) * 4u);
-    wait_all_mem();
-    __syncthreads();
-    for (int i = tid; i < n; i += kTThreads) {
-      const float f = __builtin_bit_cast(float, keys_lds[i]);
-      ss = fmaf(f, f, ss);
-      keys_lds[i] = order_key(f);
-    }
-  } else {
-    for (int base = 0; base < n; base += 8 * kTThreads) {
-      float f[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int i = base + k * kTThreads + tid;
-        f[k] = i < n ? sc[i] : 0.f;
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) ss = fmaf(f[k], f[k], ss);
-    }
-  }
-  auto key_at = [&](int i) -> uint32_t {
-    if constexpr (IN_LDS) return keys_lds[i];
-    else return order_key(sc[i]);
-  };
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  if (lane == 0) red[wave] = ss;
-  if (tid == 0) { sel[0] = 0u; sel[1] = (uint32_t)kc; }
-  __syncthreads();
-  if (tid == 0 && sumsq) {
-    float t = 0.f;
-    for (int w = 0; w < kTWaves; ++w) t += red[w];
-    sumsq[blockIdx.x] = t;
-  }
-
-  // Radix select of the kc-th largest key, 8 bits per pass from the top.  The first digit (sign
-  // and high exponent bits) is concentrated on a few values, so its counts are aggregated per
-  // wave (one LDS atomic per distinct digit in the wave) instead of one atomic per key.
-  uint32_t mask = 0u;
-  for (int shift = 24; shift >= 0; shift -= 8) {
-    for (int i = lane; i < 256; i += 64) hist[wave][i] = 0;
-    __syncthreads();
-    const uint32_t prefix = sel[0];
-    for (int base = 0; base < n; base += kTThreads) {
-      const int i = base + tid;
-      const uint32_t u = i < n ? key_at(i) : 0u;
-      bool active = i < n && (u & mask) == prefix;
-      const uint32_t d = (u >> shift) & 255u;
-      if (shift == 24) {
-        uint64_t act = __builtin_amdgcn_ballot_w64(active);
-        while (act) {
-          const int leader = __builtin_ctzll(act);
-          const uint32_t ld = __shfl(d, leader);
-          const uint64_t same = __builtin_amdgcn_ballot_w64(active && d == ld);
-          if (lane == leader) hist[wave][ld] += __builtin_popcountll(same);
-          act &= ~same;
-          active = active && d != ld;
-        }
-      } else if (active) {
-        atomicAdd(&hist[wave][d], 1);
-      }
-    }
-    __syncthreads();
-    if (tid < 256) {
-      int t = 0;
-      for (int w = 0; w < kTWaves; ++w) t += hist[w][tid];
-      htot[tid] = t;
-    }
-    __syncthreads();
-    if (wave == 0) {
-      // lane l owns digits 255-4l .. 252-4l (descending)
-      int c[4], lt = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) { c[j] = htot[255 - 4 * lane - j]; lt += c[j]; }
-      int incl = lt;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-      }
-      const int before = incl - lt;
-      const int krem = (int)sel[1];
-      if (before < krem && krem <= incl) {
-        int acc = before, d = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; break; }
-          acc += c[j];
-        }
-        sel[0] = prefix | ((uint32_t)d << shift);
-        sel[1] = (uint32_t)(krem - acc);
-      }
-    }
-    mask |= 255u << shift;
-    __syncthreads();
-  }
-  const uint32_t T = sel[0];
-  const int k_eq = (int)sel[1];   // ties at T to keep, lowest positions first
-
-  // Index-order compaction: wave w owns the contiguous chunk [w*C, (w+1)*C), read 64 consecutive
-  // keys at a time; ballots rank the ties and place the kept positions.
-  const int C = ((n + kTWaves - 1) / kTWaves + 63) / 64 * 64;
-  const int c0 = min(n, wave * C), c1 = min(n, c0 + C);
-  int n_gt = 0, n_eq = 0;
-  for (int base = c0; base < c1; base += 64) {
-    const int i = base + lane;
-    const uint32_t u = i < c1 ? key_at(i) : 0u;   // 0 is below every key order_key produces
-    n_gt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < c1 && u > T));
-    n_eq += __builtin_popcountll(__builtin_amdgcn_ballot_w64(i < c1 && u == T));
-  }
-  if (lane == 0) { wgt[wave] = n_gt; weq[wave] = n_eq; }
-  __syncthreads();
-  int eq_before = 0, keep_before = 0;
-  for (int w = 0; w < wave; ++w) {
-    const int te = min(weq[w], max(0, k_eq - eq_before));
-    keep_before += wgt[w] + te;
-    eq_before += weq[w];
-  }
-  int64_t *out = keep + kept0 + s;
-  int run_eq = eq_before, run_keep = keep_before;
-  for (int base = c0; base < c1; base += 64) {
-    const int i = base + lane;
-    const uint32_t u = i < c1 ? key_at(i) : 0u;
-    const bool valid = i < c1;
-    const bool eq = valid && u == T;
-    const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
-    const bool take = valid && (u > T || (eq && run_eq + lanes_below(eqm) < k_eq));
-    const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
-    if (take) out[run_keep + lanes_below(tm)] = s + i;
-    run_eq += __builtin_popcountll(eqm);
-    run_keep += __builtin_popcountll(tm);
-  }
 }
 
 // Register-resident variant for articles of at most 1024 * KPT tokens: thread t holds keys
@@ -486,6 +319,194 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
   }
 }
 
+// Streaming variant for articles longer than the register-resident limit: the article is
+// processed in chunks of 32 * 1024 keys (thread t holds keys c*32768 + 1024 r + t of chunk c, all
+// 32 loads in flight), re-read from L2 on every pass — the same windowed radix select and
+// 64-key-block compaction as gate_topk_reg_kernel, with the compaction's tie and output counts
+// carried from chunk to chunk.
+constexpr int kTChunk = 32;                 // keys per thread per chunk
+constexpr int kTChunkKeys = kTChunk * kTThreads;
+
+__global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const float *scores, const int32_t *geom,
+                                                                      int64_t *keep, float *sumsq) {
+  constexpr int NB = kTChunk * kTWaves;   // 64-key blocks per chunk
+  __shared__ int hist[2][kTWaves][256];
+  __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
+  __shared__ uint32_t sel[4];             // lo, hi, k_rem
+  __shared__ int carry[2];                // ties seen, rows kept: over the chunks before this one
+  __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
+  __shared__ float red[kTWaves];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t *gm = geom + 6 * blockIdx.x;
+  const int64_t row_start = gm[0];
+  const int seq_len = gm[1], s = gm[2], e = gm[3], kc = gm[4];
+  const int64_t kept0 = gm[5];
+  const int n = e - s;
+  const float *sc = scores + row_start + s;
+
+  for (int i = tid; i < s; i += kTThreads) keep[kept0 + i] = i;
+  for (int i = tid; i < seq_len - e; i += kTThreads) keep[kept0 + s + kc + i] = e + i;
+  if (n <= 0 || kc <= 0) {
+    if (tid == 0 && sumsq) sumsq[blockIdx.x] = 0.f;
+    return;
+  }
+  const int n_chunks = (n + kTChunkKeys - 1) / kTChunkKeys;
+  const brsrc_t srs = make_rsrc(sc, (uint32_t)n * 4u);
+  uint32_t key[kTChunk];
+  // order keys of chunk c (0 past the article)
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r)
+      key[r] = __builtin_amdgcn_raw_buffer_load_b32(srs, (uint32_t)(c * kTChunkKeys + r * kTThreads + tid) * 4u, 0, 0);
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r) {
+      const bool valid = c * kTChunkKeys + r * kTThreads + tid < n;
+      key[r] = valid ? order_key(__builtin_bit_cast(float, key[r])) : 0u;
+    }
+  };
+
+  float ss = 0.f;
+  uint32_t kmin = 0xffffffffu, kmax = 0u;
+  for (int c = 0; c < n_chunks; ++c) {
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r)
+      key[r] = __builtin_amdgcn_raw_buffer_load_b32(srs, (uint32_t)(c * kTChunkKeys + r * kTThreads + tid) * 4u, 0, 0);
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r) {
+      const bool valid = c * kTChunkKeys + r * kTThreads + tid < n;
+      const float f = __builtin_bit_cast(float, key[r]);
+      ss = valid ? fmaf(f, f, ss) : ss;
+      const uint32_t u = valid ? order_key(f) : 0u;
+      kmin = min(kmin, valid ? u : 0xffffffffu);
+      kmax = max(kmax, u);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o);
+    kmin = min(kmin, (uint32_t)__shfl_xor((int)kmin, o));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+  }
+  if (lane == 0) { red[wave] = ss; wmin[wave] = kmin; wmax[wave] = kmax; }
+  for (int i = lane; i < 256; i += 64) hist[0][wave][i] = 0;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.f;
+    uint32_t lo = 0xffffffffu, hi = 0u;
+    for (int w = 0; w < kTWaves; ++w) { t += red[w]; lo = min(lo, wmin[w]); hi = max(hi, wmax[w]); }
+    if (sumsq) sumsq[blockIdx.x] = t;
+    sel[0] = lo; sel[1] = hi; sel[2] = (uint32_t)kc;
+    carry[0] = 0; carry[1] = 0;
+  }
+  __syncthreads();
+
+  int pb = 0;
+  while (true) {
+    const uint32_t lo = sel[0], hi = sel[1];
+    if (lo == hi) break;                             // block-uniform
+    const uint32_t span = hi - lo;
+    const int shift = span < 256u ? 0 : 32 - __builtin_clz(span >> 8);
+    for (int i = lane; i < 256; i += 64) hist[pb ^ 1][wave][i] = 0;
+    for (int c = 0; c < n_chunks; ++c) {
+      load_chunk(c);
+#pragma unroll
+      for (int r = 0; r < kTChunk; ++r) {
+        const uint32_t u = key[r];
+        if (u != 0u && u >= lo && u <= hi) atomicAdd(&hist[pb][wave][(u - lo) >> shift], 1);
+      }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      int c4[4], lt = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        int t = 0;
+#pragma unroll
+        for (int w = 0; w < kTWaves; ++w) t += hist[pb][w][255 - 4 * lane - j];
+        c4[j] = t;
+        lt += t;
+      }
+      int incl = lt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        if (lane >= o) incl += y;
+      }
+      const int before = incl - lt;
+      const int krem = (int)sel[2];
+      if (before < krem && krem <= incl) {
+        int acc = before, d = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (acc + c4[j] >= krem) { d = 255 - 4 * lane - j; break; }
+          acc += c4[j];
+        }
+        const uint32_t nlo = lo + ((uint32_t)d << shift);
+        const uint32_t nhi_raw = nlo + ((1u << shift) - 1u);
+        sel[0] = nlo;
+        sel[1] = (nhi_raw < nlo || nhi_raw > hi) ? hi : nhi_raw;
+        sel[2] = (uint32_t)(krem - acc);
+      }
+    }
+    __syncthreads();
+    pb ^= 1;
+  }
+  const uint32_t T = sel[0];
+  const int k_eq = (int)sel[2];
+
+  int64_t *out = keep + kept0 + s;
+  for (int c = 0; c < n_chunks; ++c) {
+    load_chunk(c);
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r) {
+      const uint64_t gtm = __builtin_amdgcn_ballot_w64(key[r] > T);
+      const uint64_t eqm = __builtin_amdgcn_ballot_w64(key[r] == T);
+      if (lane == 0) { bgt[r * kTWaves + wave] = (int)__builtin_popcountll(gtm); beq[r * kTWaves + wave] = (int)__builtin_popcountll(eqm); }
+    }
+    __syncthreads();
+    if (wave == 0) {
+      constexpr int PER = NB / 64;
+      const int ceq = carry[0], ckeep = carry[1];
+      int eqv[PER], gtv[PER], ge = 0, gk = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) { eqv[j] = beq[lane * PER + j]; gtv[j] = bgt[lane * PER + j]; ge += eqv[j]; }
+      int ie = ge;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) { const int y = __shfl_up(ie, o); if (lane >= o) ie += y; }
+      int eb = ceq + ie - ge;
+      int kl[PER];
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int te = min(eqv[j], max(0, k_eq - eb));
+        beq0[lane * PER + j] = eb;
+        eb += eqv[j];
+        kl[j] = gtv[j] + te;
+        gk += kl[j];
+      }
+      int ik = gk;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) { const int y = __shfl_up(ik, o); if (lane >= o) ik += y; }
+      int kb = ckeep + ik - gk;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) { bkeep0[lane * PER + j] = kb; kb += kl[j]; }
+      if (lane == 63) { carry[0] = eb; carry[1] = kb; }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kTChunk; ++r) {
+      const uint32_t u = key[r];
+      const bool eq = u == T;
+      const uint64_t eqm = __builtin_amdgcn_ballot_w64(eq);
+      const int e0 = beq0[r * kTWaves + wave], k0 = bkeep0[r * kTWaves + wave];
+      const bool take = u > T || (eq && e0 + lanes_below(eqm) < k_eq);
+      const uint64_t tm = __builtin_amdgcn_ballot_w64(take);
+      if (take) out[k0 + lanes_below(tm)] = s + c * kTChunkKeys + r * kTThreads + tid;
+    }
+    __syncthreads();   // the block tables are rewritten by the next chunk
+  }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Pack.  Kept row j (0 <= j < total_kept) of sequence b reads source row
 // row_start[b] + keep[j] of every stream and writes destination row j.
@@ -614,7 +635,7 @@ extern "C" int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32
   else if (max_article_len <= 64 * kTThreads)
     hipLaunchKernelGGL(gate_topk_reg_kernel<64>, grid, block, 0, stream, scores, geom, keep, sumsq);
   else
-    hipLaunchKernelGGL(gate_topk_kernel<false>, grid, block, 0, stream, scores, geom, keep, sumsq);
+    hipLaunchKernelGGL(gate_topk_stream_kernel, grid, block, 0, stream, scores, geom, keep, sumsq);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }
