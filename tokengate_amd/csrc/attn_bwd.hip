@@ -17,6 +17,8 @@
 // Tiles that are read both row-major (MFMA A operand, sigma-permuted rows) and transposed
 // (ds_read_b64_tr_b16) are stored in natural row order with the swizzle dual_swz(), which is
 // bank-conflict free for both access patterns.
+#include <type_traits>
+
 #include "tg_common.h"
 #include "../../include/tokengate_hip.h"
 
@@ -306,10 +308,15 @@ constexpr int kQTileBytes = kQT * kRow; // 8 KiB
 
 template <bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char qs[2][kQTileBytes];    // natural rows, dual_swz
-  __shared__ __attribute__((aligned(1024))) char dos[2][kQTileBytes];
-  __shared__ __attribute__((aligned(128))) float ls[2][kQT];            // lse (natural log)
-  __shared__ __attribute__((aligned(128))) float dsh[2][kQT];           // D
+  // one __shared__ object per ring slot: Q / dO natural rows with dual_swz, lse (natural log), D
+  __shared__ __attribute__((aligned(1024))) char qs0[kQTileBytes], qs1[kQTileBytes];
+  __shared__ __attribute__((aligned(1024))) char dos0[kQTileBytes], dos1[kQTileBytes];
+  __shared__ __attribute__((aligned(128))) float ls0[kQT], ls1[kQT];
+  __shared__ __attribute__((aligned(128))) float dsh0[kQT], dsh1[kQT];
+  auto qslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return qs0; else return qs1; };
+  auto doslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return dos0; else return dos1; };
+  auto lslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return ls0; else return ls1; };
+  auto dslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return dsh0; else return dsh1; };
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
   // heaviest first: under the causal mask the first key tiles see the most queries
@@ -377,25 +384,24 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (kvalid) bk = a.bias[(int64_t)b * a.bias_bs + (int64_t)hh * a.bias_hs + key];
     float dbacc = 0.f;
 
-    auto issue_tile = [&](int m0, int buf) {
+    auto issue_tile = [&](int m0, auto buf_c) {
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
-        dma16(qrs, qs[buf] + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff[it]);
-        dma16(dors, dos[buf] + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff[it]);
+        dma16(qrs, qslot(buf_c) + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff[it]);
+        dma16(dors, doslot(buf_c) + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff[it]);
       }
-      if (wave == 0 && lane < kQT) dma4(lrs, &ls[buf][0], (uint32_t)(m0 + lane) * 4);
-      if (wave == 1 && lane < kQT) dma4(drs, &dsh[buf][0], (uint32_t)(m0 + lane) * 4);
+      if (wave == 0 && lane < kQT) dma4(lrs, lslot(buf_c), (uint32_t)(m0 + lane) * 4);
+      if (wave == 1 && lane < kQT) dma4(drs, dslot(buf_c), (uint32_t)(m0 + lane) * 4);
     };
 
-    __syncthreads();   // previous head's last tile fully consumed before its buffers are reused
-    if (n_qt > 0) issue_tile(m_start, 0);
-    for (int t = 0; t < n_qt; ++t) {
-      const int buf = t & 1;
+    // two-slot ring unrolled by two (compile-time slots), as in the dQ kernel
+    auto tile_step = [&](int t, auto buf_c) {
+      constexpr int BUF = decltype(buf_c)::value;
       const int m0 = m_start + t * kQT;
-      wait_all_mem();
-      __syncthreads();
-      if (t + 1 < n_qt) issue_tile(m0 + kQT, buf ^ 1);
-      if (!wave_has_keys || (CAUSAL && m0 + kQT - 1 + off < kw0)) continue;
+      wait_vm<0>();
+      ring_barrier();
+      if (t + 1 < n_qt) issue_tile(m0 + kQT, std::integral_constant<int, 1 - BUF>());
+      if (!wave_has_keys || (CAUSAL && m0 + kQT - 1 + off < kw0)) return;
 
       // S = Q K^T and dP = dO V^T: A operands are sigma rows of the Q / dO tiles
       f32x16 sacc, pacc;
@@ -405,12 +411,12 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         const uint32_t o16 = srow * kRow + (((uint32_t)(2 * s + g) ^ dual_swz(srow)) << 4);
-        sacc = mfma32(lds_load16(qs[buf], o16), kf[s], sacc);
-        pacc = mfma32(lds_load16(dos[buf], o16), vf[s], pacc);
+        sacc = mfma32(lds_load16(qslot(buf_c), o16), kf[s], sacc);
+        pacc = mfma32(lds_load16(doslot(buf_c), o16), vf[s], pacc);
       }
       // rows of the accumulators: queries m0 + 16g + v
-      const f32x4 *lp = reinterpret_cast<const f32x4 *>(&ls[buf][16 * g]);
-      const f32x4 *dp = reinterpret_cast<const f32x4 *>(&dsh[buf][16 * g]);
+      const f32x4 *lp = reinterpret_cast<const f32x4 *>(lslot(buf_c) + 16 * g);
+      const f32x4 *dp = reinterpret_cast<const f32x4 *>(dslot(buf_c) + 16 * g);
       const bool need_mask = (m0 + kQT > sq) || (kw0 + 32 > sk) || (CAUSAL && kw0 + 31 > m0 + off);
       uint32_t pk[8], dk8[8];
 #pragma unroll
@@ -451,16 +457,26 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
           const int r0 = q0r + tr_row, r1 = q0r + 4 + tr_row;
           const uint32_t o0 = r0 * kRow + (((uint32_t)c ^ dual_swz(r0)) << 4) + tr_half;
           const uint32_t o1 = r1 * kRow + (((uint32_t)c ^ dual_swz(r1)) << 4) + tr_half;
-          const bf16x8 dot_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(dos[buf] + o0),
-                                                                                 lds_read_tr16(dos[buf] + o1),
+          const bf16x8 dot_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(doslot(buf_c) + o0),
+                                                                                 lds_read_tr16(doslot(buf_c) + o1),
                                                                                  0, 1, 2, 3, 4, 5, 6, 7));
           dvacc[dblk] = mfma32(dot_, pop, dvacc[dblk]);
-          const bf16x8 qt_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qs[buf] + o0),
-                                                                                lds_read_tr16(qs[buf] + o1),
+          const bf16x8 qt_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qslot(buf_c) + o0),
+                                                                                lds_read_tr16(qslot(buf_c) + o1),
                                                                                 0, 1, 2, 3, 4, 5, 6, 7));
           dkacc[dblk] = mfma32(qt_, dop, dkacc[dblk]);
         }
       }
+    };
+    ring_barrier();   // previous head's last tile fully consumed before its slots are reused
+    if (n_qt > 0) issue_tile(m_start, std::integral_constant<int, 0>());
+    {
+      int t = 0;
+      for (; t + 1 < n_qt; t += 2) {
+        tile_step(t, std::integral_constant<int, 0>());
+        tile_step(t + 1, std::integral_constant<int, 1>());
+      }
+      if (t < n_qt) tile_step(t, std::integral_constant<int, 0>());
     }
     if constexpr (HAS_BIAS) {
       const float tot = pair_sum(dbacc);

@@ -25,6 +25,8 @@
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
+#include <type_traits>
+
 #include "tg_common.h"
 #include "../../include/tokengate_hip.h"
 
@@ -82,10 +84,18 @@ template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
   constexpr int QW = qpw<HP>();
   constexpr int BM = bm<HP>();
-  __shared__ __attribute__((aligned(1024))) char ks[kStages][kKTileBytes];
-  __shared__ __attribute__((aligned(1024))) char vs[kStages][kKTileBytes];
+  // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads only
+  // across distinct objects, so the DMA of tile t+1 does not hold up the reads of tile t.
+  static_assert(kStages == 2, "two named LDS objects per operand");
+  __shared__ __attribute__((aligned(1024))) char ks0[kKTileBytes], ks1[kKTileBytes];
+  __shared__ __attribute__((aligned(1024))) char vs0[kKTileBytes], vs1[kKTileBytes];
   // bias rows padded by 4 floats so that the two heads' rows fall on different banks
-  __shared__ __attribute__((aligned(256))) float bs[kStages][HP][kBN + 4];
+  __shared__ __attribute__((aligned(256))) float bs0[HP][kBN + 4], bs1[HP][kBN + 4];
+  auto kslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return ks0; else return ks1; };
+  auto vslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return vs0; else return vs1; };
+  auto bslot = [&](auto b) -> float (*)[kBN + 4] {
+    if constexpr (decltype(b)::value == 0) return bs0; else return bs1;
+  };
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -167,16 +177,18 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
     const int vc = (lane & 15) ^ (4 * (vkey & 3));
     voff[it] = (uint32_t)(vkey * a.v_rs * 2 + vc * 16);
   }
-  auto issue_tile = [&](int tile, int buf) {
+  auto issue_tile = [&](int tile, auto buf_c) {
     const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
     const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
+    char *kd = kslot(buf_c), *vd = vslot(buf_c);
 #pragma unroll
     for (int it = 0; it < kLoads; ++it) {
-      dma16(krs, ks[buf] + (wave + it * kWaves) * 1024, kb0 + koff[it]);
-      dma16(vrs, vs[buf] + (wave + it * kWaves) * 1024, vb0 + voff[it]);
+      dma16(krs, kd + (wave + it * kWaves) * 1024, kb0 + koff[it]);
+      dma16(vrs, vd + (wave + it * kWaves) * 1024, vb0 + voff[it]);
     }
     if constexpr (HAS_BIAS) {
-      if (wave < HP) dma4(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
+      if (wave < HP)
+        dma4(brs, &bslot(buf_c)[wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
     }
   };
 
@@ -194,20 +206,17 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) oacc[d][v] = 0.f;
 
-  // ring of kStages tiles: tile t lives in buffer t % kStages; tiles t+1 .. t+kStages-2 stay in
-  // flight while tile t is computed, and tile t+kStages-1 is issued into the buffer tile t-1 left.
-  const int ops_per_tile = 2 * kLoads + ((HAS_BIAS && wave < HP) ? 1 : 0);   // this wave's DMA ops
-  for (int t0 = 0; t0 < kStages - 1 && t0 < n_tiles; ++t0) issue_tile(t0, t0);
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int buf = t % kStages;
+  // Two-slot ring, unrolled by two so that every slot index is a compile-time constant: tile t
+  // lives in slot t % 2; at the top of tile t this wave's DMA for t is complete (nothing later
+  // is in flight yet), the barrier makes every wave's part visible and frees the slot of t-1,
+  // and tile t+1 is issued into it while tile t is computed.
+  auto tile_step = [&](int t, auto buf_c) {
+    constexpr int BUF = decltype(buf_c)::value;
     const int n0 = t * kBN;
-    // wait until this wave's DMA for tile t is done; later tiles may stay in flight
-    const int later = min(kStages - 2, n_tiles - 1 - t);
-    wait_vm_outstanding(later * ops_per_tile);
-    __syncthreads();                       // tile t resident in every wave's view; buffer of t-1 free
-    if (t + kStages - 1 < n_tiles) issue_tile(t + kStages - 1, (t + kStages - 1) % kStages);
-    if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
+    wait_vm<0>();
+    ring_barrier();
+    if (t + 1 < n_tiles) issue_tile(t + 1, std::integral_constant<int, 1 - BUF>());
+    if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) return;
 
     // ---- S^T = K Q^T + bias: 2 key blocks x 8 d-steps.  The accumulators start from the bias of
     // their keys (raw-score units), so the bias add costs no VALU work. ----
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       if constexpr (HAS_BIAS) {
-        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
+        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bslot(buf_c)[hl][32 * kb + 16 * g]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const f32x4 bb = bp[i];
@@ -234,7 +243,7 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const int lr = 32 * kb + lq;
-        kfr[s][kb] = lds_load16(ks[buf], lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
+        kfr[s][kb] = lds_load16(kslot(buf_c), lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -305,14 +314,21 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int dblk = 0; dblk < 4; ++dblk) {
           const uint32_t ch = (uint32_t)((4 * (dblk ^ v_swz) + v_cpart) << 4);
-          const s16x4 lo = lds_read_tr16(vs[buf] + krow + ch);
-          const s16x4 hi = lds_read_tr16(vs[buf] + krow + 4 * kKRowBytes + ch);
+          const s16x4 lo = lds_read_tr16(vslot(buf_c) + krow + ch);
+          const s16x4 hi = lds_read_tr16(vslot(buf_c) + krow + 4 * kKRowBytes + ch);
           const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
           oacc[dblk] = mfma32(vf, pb, oacc[dblk]);
         }
       }
     }
+  };
+  if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>());
+  int t = 0;
+  for (; t + 1 < n_tiles; t += 2) {
+    tile_step(t, std::integral_constant<int, 0>());
+    tile_step(t + 1, std::integral_constant<int, 1>());
   }
+  if (t < n_tiles) tile_step(t, std::integral_constant<int, 0>());
 
   // ---- epilogue: normalise, write O (bf16) and LSE (natural log) ----
   const float l = pair_sum(lrun);

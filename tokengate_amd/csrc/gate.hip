@@ -23,6 +23,8 @@
 //   gate_pack_kernel   — one launch gathers every kept row for any number of row streams (hidden
 //                        states, per-layer K and V, head-chunked rows) in 16-byte units, plus the
 //                        kept positions and the kept rows' gate bias.
+#include <type_traits>
+
 #include "tg_common.h"
 #include "../../include/tokengate_hip.h"
 
@@ -32,8 +34,9 @@ namespace {
 // ---------------------------------------------------------------------------------------------
 // Scoring head: s = w2 . silu(W1 x + b1) + b2, x in R^2048 (bf16), W1 (256 x 2048) bf16.
 // Workgroup: 4 waves, 128 rows; wave w owns rows 32w..32w+31 and all 256 hidden units
-// (8 column blocks of 32).  K loop over the 2048 inputs in steps of 32, double-buffered through
-// LDS: X tile 128 x 32 (8 KiB), W1 tile 256 x 32 (16 KiB).  Accumulators are C^T blocks
+// (8 column blocks of 32).  K loop over the 2048 inputs in steps of 32 through a 4-deep LDS ring
+// (X tile 128 x 32 = 8 KiB, W1 tile 256 x 32 = 16 KiB per stage), unrolled so that every ring slot
+// index is a compile-time constant.  Accumulators are C^T blocks
 // (hidden unit = MFMA row, token = column) so each lane ends with one token's 16 hidden units
 // per block and the SiLU . w2 reduction is in-lane plus one cross-half exchange.
 // ---------------------------------------------------------------------------------------------
@@ -42,6 +45,7 @@ constexpr int kDh = 256;
 constexpr int kSRows = 128;
 constexpr int kSK = 32;
 constexpr int kSThreads = 256;
+constexpr int kSStages = 4;
 
 struct ScoreArgs {
   const bf16_t *x;
@@ -55,8 +59,23 @@ struct ScoreArgs {
 
 __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
   // X tile: 128 rows x 64 B, W tile: 256 rows x 64 B; 16-byte chunks, 4 per row, XOR-swizzled
-  __shared__ __attribute__((aligned(1024))) char xs[2][kSRows * kSK * 2];
-  __shared__ __attribute__((aligned(1024))) char ws[2][kDh * kSK * 2];
+  // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads
+  // only across distinct objects, so slot s+3's DMA does not hold up the reads of slot s.
+  __shared__ __attribute__((aligned(1024))) char xs0[kSRows * kSK * 2], xs1[kSRows * kSK * 2],
+      xs2[kSRows * kSK * 2], xs3[kSRows * kSK * 2];
+  __shared__ __attribute__((aligned(1024))) char ws0[kDh * kSK * 2], ws1[kDh * kSK * 2], ws2[kDh * kSK * 2],
+      ws3[kDh * kSK * 2];
+  static_assert(kSStages == 4, "one named LDS object per ring slot");
+  auto xsl = [&](auto b) -> char * {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return xs0; else if constexpr (B == 1) return xs1; else if constexpr (B == 2) return xs2;
+    else return xs3;
+  };
+  auto wsl = [&](auto b) -> char * {
+    constexpr int B = decltype(b)::value;
+    if constexpr (B == 0) return ws0; else if constexpr (B == 1) return ws1; else if constexpr (B == 2) return ws2;
+    else return ws3;
+  };
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
   const int64_t r0 = (int64_t)blockIdx.x * kSRows;
 
@@ -65,22 +84,31 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
   const brsrc_t wrs = make_rsrc(a.w1, (uint32_t)(kDh * kDin * 2));
   // DMA slots: X tile = 512 chunks (2 per thread... 256 threads x 16 B = 4 KiB per issue): 2 issues;
   // W tile = 1024 chunks: 4 issues.  LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).
-  auto issue = [&](int kstep, int buf) {
-    const int k0 = kstep * kSK;
+  // per-lane source offsets (bytes) within a k step; the step's byte offset is added per issue
+  uint32_t xoff[2], woff[4];
 #pragma unroll
-    for (int it = 0; it < 2; ++it) {
-      const int slot = (wave * 2 + it) * 64 + lane;        // 0..511
-      const int r = slot >> 2, p = slot & 3;
-      const int c = p ^ ((r >> 1) & 3);
-      dma16(xrs, xs[buf] + (wave * 2 + it) * 1024, (uint32_t)((r * a.x_rs + k0 + 8 * c) * 2));
-    }
+  for (int it = 0; it < 2; ++it) {
+    const int slot = (wave * 2 + it) * 64 + lane;        // 0..511
+    const int r = slot >> 2, p = slot & 3;
+    const int c = p ^ ((r >> 1) & 3);
+    xoff[it] = (uint32_t)((r * a.x_rs + 8 * c) * 2);
+  }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int slot = (wave * 4 + it) * 64 + lane;        // 0..1023
-      const int r = slot >> 2, p = slot & 3;
-      const int c = p ^ ((r >> 1) & 3);
-      dma16(wrs, ws[buf] + (wave * 4 + it) * 1024, (uint32_t)((r * kDin + k0 + 8 * c) * 2));
-    }
+  for (int it = 0; it < 4; ++it) {
+    const int slot = (wave * 4 + it) * 64 + lane;        // 0..1023
+    const int r = slot >> 2, p = slot & 3;
+    const int c = p ^ ((r >> 1) & 3);
+    woff[it] = (uint32_t)((r * kDin + 8 * c) * 2);
+  }
+  // DMA slots: X tile = 512 chunks (two 1 KiB issues per wave), W tile = 1024 chunks (four);
+  // LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).
+  auto issue = [&](int kstep, auto buf_c) {
+    const uint32_t k0b = (uint32_t)(kstep * kSK * 2);
+    char *xd = xsl(buf_c), *wd = wsl(buf_c);
+#pragma unroll
+    for (int it = 0; it < 2; ++it) dma16(xrs, xd + (wave * 2 + it) * 1024, xoff[it] + k0b);
+#pragma unroll
+    for (int it = 0; it < 4; ++it) dma16(wrs, wd + (wave * 4 + it) * 1024, woff[it] + k0b);
   };
 
   f32x16 acc[8];
@@ -90,26 +118,58 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
 
   constexpr int nk = kDin / kSK;
-  issue(0, 0);
-  for (int ks = 0; ks < nk; ++ks) {
-    const int buf = ks & 1;
-    wait_all_mem();
-    __syncthreads();
-    if (ks + 1 < nk) issue(ks + 1, buf ^ 1);
+  constexpr int kOps = 6;   // DMA ops per thread per step (2 X + 4 W)
+  static_assert(nk % kSStages == 0, "the k loop is unrolled by the ring depth");
+  // One k step with a compile-time ring slot: reads of slot BUF and the DMA into slot
+  // (BUF + kSStages - 1) % kSStages are then provably disjoint, so the compiler does not make the
+  // reads wait for that DMA (with a run-time slot index it waits for every DMA in flight).
+  // WAITN: DMA ops this wave may leave in flight (the steps after ks already issued).
+  auto step = [&](int ks, auto buf_c, auto waitn_c) {
+    constexpr int BUF = decltype(buf_c)::value;
+    constexpr int NXT = (BUF + kSStages - 1) % kSStages;
+    wait_vm<decltype(waitn_c)::value>();   // step ks resident for this wave
+    ring_barrier();                        // ... for every wave; the slot of step ks-1 is free
+    if (ks + kSStages - 1 < nk) issue(ks + kSStages - 1, std::integral_constant<int, NXT>());
     // B operand: X^T column (token) = lane's row 32*wave + lq; k = 16*s + 8g + j
+    const char *xb_lds = xsl(buf_c), *wb_lds = wsl(buf_c);
     const int xr = 32 * wave + lq;
+    bf16x8 xb[2], wa[2][8];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int c = 2 * s + g;
-      const bf16x8 xb = lds_load16(xs[buf], xr * 64 + (((uint32_t)c ^ ((xr >> 1) & 3)) << 4));
+      xb[s] = lds_load16(xb_lds, xr * 64 + (((uint32_t)c ^ ((xr >> 1) & 3)) << 4));
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int wr = 32 * j + lq;   // A operand: W1 row (hidden unit)
-        const bf16x8 wa = lds_load16(ws[buf], wr * 64 + (((uint32_t)c ^ ((wr >> 1) & 3)) << 4));
-        acc[j] = mfma32(wa, xb, acc[j]);
+        wa[s][j] = lds_load16(wb_lds, wr * 64 + (((uint32_t)c ^ ((wr >> 1) & 3)) << 4));
       }
     }
+    __builtin_amdgcn_sched_barrier(0);   // all 18 reads in flight before the first MFMA
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = mfma32(wa[s][j], xb[s], acc[j]);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  using W2 = std::integral_constant<int, 2 * kOps>;
+  using W1 = std::integral_constant<int, kOps>;
+  issue(0, I0());
+  issue(1, I1());
+  issue(2, I2());
+  int ks = 0;
+  for (; ks < nk - kSStages; ks += kSStages) {   // steady state: two later steps in flight
+    step(ks, I0(), W2());
+    step(ks + 1, I1(), W2());
+    step(ks + 2, I2(), W2());
+    step(ks + 3, I3(), W2());
   }
+  step(ks, I0(), W2());
+  step(ks + 1, I1(), W2());
+  step(ks + 2, I2(), W1());
+  step(ks + 3, I3(), I0());
   // epilogue: lane holds token (32*wave + lq), hidden units 32j + 8(v/4) + 4g + v%4
   float part = 0.f;
 #pragma unroll

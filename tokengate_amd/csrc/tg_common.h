@@ -98,15 +98,34 @@ __device__ __forceinline__ s16x4 lds_read_tr16(const void *lds_addr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)lds_addr);
 }
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
-// Wait until at most n (0..15) vector-memory operations of this wave are outstanding (vmcnt),
-// leaving the LDS and export counters unconstrained.
+// Wait for this wave's outstanding vector-memory operations down to N (compile-time, 0..63).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+// Workgroup barrier for LDS ring buffers filled by LDS DMA: this wave's LDS reads are complete
+// (lgkmcnt 0) and every wave has arrived.  Unlike __syncthreads() it does not make the wave wait
+// for its own DMA still in flight into other ring slots (those are waited for by count, wait_vm);
+// the empty asm statements keep the compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0); vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// Wait until at most n (0..63) vector-memory operations of this wave are outstanding (vmcnt: low
+// four bits in [3:0], high two in [15:14]), leaving the LDS and export counters unconstrained.
 __device__ __forceinline__ void wait_vm_outstanding(int n) {
-#define TG_VMCNT(N) case N: __builtin_amdgcn_s_waitcnt((N) | 0x0F70); break;
+#define TG_VMCNT(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x0F70); break;
+#define TG_VMCNT8(B) TG_VMCNT(B) TG_VMCNT(B + 1) TG_VMCNT(B + 2) TG_VMCNT(B + 3) TG_VMCNT(B + 4) TG_VMCNT(B + 5) \
+  TG_VMCNT(B + 6) TG_VMCNT(B + 7)
   switch (n) {
-    TG_VMCNT(0) TG_VMCNT(1) TG_VMCNT(2) TG_VMCNT(3) TG_VMCNT(4) TG_VMCNT(5) TG_VMCNT(6) TG_VMCNT(7)
-    TG_VMCNT(8) TG_VMCNT(9) TG_VMCNT(10) TG_VMCNT(11) TG_VMCNT(12) TG_VMCNT(13) TG_VMCNT(14)
-    default: __builtin_amdgcn_s_waitcnt(15 | 0x0F70); break;
+    TG_VMCNT8(0) TG_VMCNT8(8) TG_VMCNT8(16) TG_VMCNT8(24) TG_VMCNT8(32) TG_VMCNT8(40) TG_VMCNT8(48)
+    TG_VMCNT(56) TG_VMCNT(57) TG_VMCNT(58) TG_VMCNT(59) TG_VMCNT(60) TG_VMCNT(61) TG_VMCNT(62)
+    default: __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | 0x0F70); break;
   }
+#undef TG_VMCNT8
 #undef TG_VMCNT
 }
 
