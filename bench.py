@@ -217,6 +217,15 @@ def bench_ttft(dev, reps=5):
         out[name] = {"ttft_ms": round(statistics.median(times), 3), "reps_ms": [round(t, 3) for t in times],
                      "prompt_tokens": sum(lens), "kept_tokens": r.cu_kept[-1],
                      "phase_ms": {k: round(v, 3) for k, v in r.phase_ms.items()}}
+        if r.cu_kept[-1] <= 32768:
+            # Phase 2 replayed from a captured graph (captured during the warm-up call)
+            graphs = P.Phase2Graphs()
+            fg = lambda: P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, phase2_graphs=graphs)
+            tg = P.ttft_ms(fg, reps=reps, warmup=1)
+            rg = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, phase_timing=True, phase2_graphs=graphs)
+            out[name]["ttft_ms_phase2_graph"] = round(statistics.median(tg), 3)
+            out[name]["phase2_ms_graph"] = round(rg.phase_ms["phase2"], 3)
+            del graphs, rg
         if len(lens) > 1:
             out[name]["lens"] = lens
             out[name]["K"] = Ks

@@ -51,12 +51,87 @@ def _cat_ids(ids_list: Sequence, device) -> torch.Tensor:
     return h2d(torch.tensor(flat, dtype=torch.long), device)
 
 
+class Phase2Graphs:
+    """Captured HIP graphs of the Phase-2 layer loop (the reference's whole-loop graph replay,
+    phase2_graph.py:170-223, with bucketed sizes as set_phase2_bucket, gate_forward.py:531-546).
+
+    One graph per (number of sequences, rows rounded up to `bucket_rows`, longest sequence rounded
+    up to `bucket_len`): its static inputs are the packed kept rows, their positions, cu_seqlens,
+    the per-layer bias table and the per-layer query scales; the varlen attention reads
+    cu_seqlens from device memory, so every batch of that geometry replays the same graph.  Rows
+    past the last sequence are zero and belong to no sequence (attention never visits them).
+    Replays are stream-ordered on the current stream; the returned tensors are views of the
+    graph's static buffers, valid until the next replay of the same graph."""
+
+    def __init__(self, bucket_rows: int = 64, bucket_len: int = 64):
+        self.bucket_rows = bucket_rows
+        self.bucket_len = bucket_len
+        self.graphs = {}
+
+    @staticmethod
+    def _up(n: int, b: int) -> int:
+        return (n + b - 1) // b * b
+
+    def run(self, wts: DecoderWeights, layer_ids: List[int], hs: torch.Tensor, positions: torch.Tensor,
+            cu_dev: torch.Tensor, coef: torch.Tensor, bias_pad: torch.Tensor, qscale: Optional[torch.Tensor],
+            mlp_rows: int):
+        shape = wts.shape
+        dev = hs.device
+        nseq = cu_dev.numel() - 1
+        T2, max_kept = hs.shape[0], bias_pad.shape[1]
+        Tb, Lb = self._up(T2, self.bucket_rows), self._up(max_kept, self.bucket_len)
+        key = (nseq, Tb, Lb, tuple(layer_ids), qscale is not None)
+        ent = self.graphs.get(key)
+        if ent is None:
+            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, qscale is not None, mlp_rows, dev)
+            self.graphs[key] = ent
+        ent["x"][:T2].copy_(hs)
+        ent["x"][T2:].zero_()
+        ent["pos"][:T2].copy_(positions)
+        ent["pos"][T2:].zero_()
+        ent["cu"].copy_(cu_dev)
+        torch.mul(coef[:, None, :, None], bias_pad[None, :, None, :], out=ent["bias"][..., :max_kept])
+        if qscale is not None:
+            ent["qs"].copy_(qscale)
+        ent["graph"].replay()
+        return ent["out"][:T2], {l: LayerKV(ent["kv"][l].k[:T2], ent["kv"][l].v[:T2]) for l in layer_ids}
+
+    def _capture(self, wts, layer_ids, nseq, Tb, Lb, with_qs, mlp_rows, dev):
+        shape = wts.shape
+        L2 = len(layer_ids)
+        x = torch.zeros(Tb, shape.d_model, dtype=torch.bfloat16, device=dev)
+        pos = torch.zeros(Tb, dtype=torch.int64, device=dev)
+        cu = torch.zeros(nseq + 1, dtype=torch.int32, device=dev)
+        cu[-1] = Tb
+        bias = torch.zeros(L2, nseq, shape.n_heads, Lb, dtype=torch.float32, device=dev)
+        qs = torch.ones(L2, shape.n_heads, dtype=torch.float32, device=dev) if with_qs else None
+        kv: List[Optional[LayerKV]] = [None] * shape.n_layers
+        for l in layer_ids:
+            kv[l] = alloc_kv(shape, Tb, dev)
+        ws = Workspace(shape, Tb, dev, mlp_rows=mlp_rows)
+        geo = Ragged([0, Tb], cu, pos, Lb)
+        biases = {l: bias[j] for j, l in enumerate(layer_ids)}
+        q_scales = {l: qs[j] for j, l in enumerate(layer_ids)} if with_qs else None
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales)   # warm-up
+        torch.cuda.current_stream(dev).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales)
+        return dict(graph=g, x=x, pos=pos, cu=cu, bias=bias, qs=qs, kv=kv, ws=ws, out=out)
+
+
 @torch.no_grad()
 def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, art_starts: Sequence[int],
                   art_ends: Sequence[int], gate_layer: int, K, prune_below_gate: bool = False,
-                  phase_timing: bool = False, capture: bool = False, mlp_rows: int = 131072) -> PrefillResult:
+                  phase_timing: bool = False, capture: bool = False, mlp_rows: int = 131072,
+                  phase2_graphs: Optional[Phase2Graphs] = None) -> PrefillResult:
     """ids_list: B prompts (lists of ints or 1-D tensors); the state span of prompt b is
-    [art_starts[b], art_ends[b]); K: scalar or per-prompt list."""
+    [art_starts[b], art_ends[b]); K: scalar or per-prompt list.  phase2_graphs: replay Phase 2
+    from captured graphs (captured on first use per geometry); the Phase-2 KV caches are then views
+    of the graph's buffers, valid until its next replay."""
     shape = wts.shape
     dev = wts.device
     B = len(ids_list)
@@ -121,17 +196,23 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
     idx = torch.minimum(st + t_[None, :], en)
     bias_pad = kept_bias[h2d(idx, dev)]                     # (B, max_kept)
     coef, qscale = head.layer_coefficients(1.0 / math.sqrt(shape.head_dim))  # (L2, H)
-    biases_all = coef[:, None, :, None] * bias_pad[None, :, None, :]       # (L2, B, H, max_kept)
-    geo2 = Ragged(p.cu_kept, h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev), kept_pos,
-                  max_kept)
+    cu2_dev = h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev)
     above = list(range(gate_layer + 1, n_layers))
-    biases = {l: biases_all[j] for j, l in enumerate(above)}
-    qs = {l: qscale[j] for j, l in enumerate(above)} if qscale is not None else None
-    for l in above:
-        kv[l] = alloc_kv(shape, T2, dev)
-    ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
-    h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
-                    capture=cap["phase2"] if cap else None)
+    biases_all = None
+    if phase2_graphs is not None and cap is None:
+        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, coef, bias_pad, qscale, mlp_rows)
+        for l in above:
+            kv[l] = kv2[l]
+    else:
+        biases_all = coef[:, None, :, None] * bias_pad[None, :, None, :]       # (L2, B, H, max_kept)
+        geo2 = Ragged(p.cu_kept, cu2_dev, kept_pos, max_kept)
+        biases = {l: biases_all[j] for j, l in enumerate(above)}
+        qs = {l: qscale[j] for j, l in enumerate(above)} if qscale is not None else None
+        for l in above:
+            kv[l] = alloc_kv(shape, T2, dev)
+        ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
+        h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
+                        capture=cap["phase2"] if cap else None)
 
     mark("head")
     last = h2d(torch.tensor(p.cu_kept[1:], dtype=torch.int64).sub_(1), dev)
