@@ -162,17 +162,18 @@ int tg_rmsnorm(const void *x, int64_t x_row_stride, const void *residual, int64_
                int64_t out_row_stride, int64_t n_rows, int32_t dim, float eps, hipStream_t stream);
 
 /* Per-head q/k RMSNorm + rotary embedding (Qwen3Attention q_norm / k_norm, rotate-half RoPE,
- * qwen3_flex_attention.py:533-544), with the Phase-2 per-head query scale
- * (_phase2_q_bias :433-473, attn_scale branch) folded in.  qkv rows hold [q heads | k heads |
- * v heads] x head_dim (=128) bf16.  For token t at position positions[t] (int64):
- * angle_i = float(positions[t]) * inv_freq[i] (fp32, i < 64); q head h -> q_out row t (may alias
- * qkv), scaled by q_head_scale[h] when that is non-NULL; k head g -> k_out row t (the layer's
- * KV cache, (rows, num_heads_k, 128)); v head g copied to v_out row t. */
+ * qwen3_flex_attention.py:533-544), with the Phase-2 query scale of _phase2_q_bias (:433-473)
+ * folded in: per head (attn_scale) and per row (the scaled-softmax ratio r_q, :417-431).
+ * qkv rows hold [q heads | k heads | v heads] x head_dim (=128) bf16.  For token t at position
+ * positions[t] (int64): angle_i = float(positions[t]) * inv_freq[i] (fp32, i < 64); q head h ->
+ * q_out row t (may alias qkv), times q_head_scale[h] and q_row_scale[t] where those are non-NULL;
+ * k head g -> k_out row t (the layer's KV cache, (rows, num_heads_k, 128)); v head g copied to
+ * v_out row t. */
 int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const int64_t *positions, int64_t n_tokens,
                     int32_t num_heads, int32_t num_heads_k, int32_t head_dim, const void *q_norm_weight,
                     const void *k_norm_weight, float eps, const float *inv_freq, const float *q_head_scale,
-                    void *q_out, int64_t q_row_stride, void *k_out, int64_t k_row_stride, void *v_out,
-                    int64_t v_row_stride, hipStream_t stream);
+                    const float *q_row_scale, void *q_out, int64_t q_row_stride, void *k_out,
+                    int64_t k_row_stride, void *v_out, int64_t v_row_stride, hipStream_t stream);
 
 /* out[r, i] = bf16(silu(gate_up[r, i]) * gate_up[r, inter + i]) (Qwen3MLP act_fn(gate) * up on
  * the fused gate/up projection). */

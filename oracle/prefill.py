@@ -8,7 +8,8 @@ Restates, for a Qwen3-shaped decoder given as float32 weights:
     q/k RMSNorm -> RoPE (cos/sin of fp32 angles position * inv_freq) -> causal GQA attention with
     an additive per-key logit bias -> o_proj -> residual -> RMSNorm -> down(silu(gate) * up) ->
     residual.  Phase 2's temperature multiplies the query and the bias per head
-    (_phase2_q_bias :433-473).
+    (_phase2_q_bias :433-473); in scaled-softmax mode the query is scaled by gamma_h * r_q and the
+    bias by mean_h(gamma) * r_k, r = _ssmax_ratio (gate_forward.py:574-585).
   * prefill_batch_for_decode (gate_forward.py:1280-1580) in its own layout: prompts right-padded
     to the longest, layers 0..gate_layer over every position, per-sample scoring and top-K
     (K_clamped, keep = prefix + sorted top-K + suffix), kept rows gathered into a zero-padded
@@ -65,10 +66,13 @@ class Weights:
 
 
 def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
-          q_temp: Optional[torch.Tensor] = None):
+          q_temp: Optional[torch.Tensor] = None, q_row: Optional[torch.Tensor] = None):
     """One decoder layer on a batch x (B, n, d) float32 at positions pos (B, n); bias_logit
-    (B, H, n) per-key logit bias (before the temperature) or None; q_temp (H,) or None.
-    Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE."""
+    (B, H, n) per-key logit bias or None; q_temp (H,) per-head temperature or None.  Without
+    q_row the temperature multiplies the query and the bias per head (_phase2_q_bias, attn_scale
+    branch); with q_row (B, n) — the scaled-softmax mode — the query is scaled by
+    q_temp[h] * q_row[b, i] and bias_logit is used as given (the caller folds in
+    mean_h(temperature) * r_k).  Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE."""
     s = W.shape
     L = W.layers[i]
     B, n, _ = x.shape
@@ -87,11 +91,13 @@ def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Op
     braw = None
     if bias_logit is not None:
         bl = bias_logit
-        if q_temp is not None:
+        if q_temp is not None and q_row is None:
             bl = bl * q_temp[None, :, None]
         braw = bl / scale
     if q_temp is not None:
         q = q * q_temp[None, None, :, None]
+    if q_row is not None:
+        q = q * q_row[:, :, None, None]
     attn, _ = oat.fwd(q, k, v, braw, scale, causal=True)
     x = x + attn.reshape(B, n, H * D) @ L["wo"].t()
     h = rms(x, L["ln2"], s.rms_eps)
@@ -144,11 +150,16 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
         raise ValueError("gate_scale must be (layers above the gate, heads)")
     gs = F.softplus(head.gate_scale.float().cpu())                  # (L2, H)
     at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
+    ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
+    r = torch.as_tensor(og.ssmax_ratio(kpos.numpy()), dtype=torch.float32) if ssmax else None   # (B, n_alloc)
     xx = hp
     for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
-        bl = gb.float()[:, None, :] * gs[j][None, :, None]
+        if ssmax:
+            bl = gb.float()[:, None, :] * gs[j][None, :, None] * at[j].mean() * r[:, None, :]
+        else:
+            bl = gb.float()[:, None, :] * gs[j][None, :, None]
         bl = torch.where(gb[:, None, :] <= -1e8, torch.full_like(bl, -1e9), bl)
-        xx, _, _ = layer(W, i, xx, kpos, bias_logit=bl, q_temp=at[j] if at is not None else None)
+        xx, _, _ = layer(W, i, xx, kpos, bias_logit=bl, q_temp=at[j] if at is not None else None, q_row=r)
     last = torch.tensor([len(k) - 1 for k in keeps])
     rows = xx[torch.arange(B), last]
     logits = rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()
@@ -219,8 +230,14 @@ def decode_logits(W: Weights, head, ids: Sequence[int], art_start: int, art_end:
     pos2 = torch.cat([kp[None], gpos], 1)
     gs = F.softplus(head.gate_scale.float().cpu())
     at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
+    ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
+    # scaled softmax: the ratio over kept ++ generated slots (a generated token's slot is n_kept + 1 + i)
+    r = torch.as_tensor(og.ssmax_ratio(pos2.numpy()), dtype=torch.float32) if ssmax else None
     for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
-        bl = gb[None, None, :] * gs[j][None, :, None]
-        xx, _, _ = layer(W, i, xx, pos2, bias_logit=bl, q_temp=at[j] if at is not None else None)
+        if ssmax:
+            bl = gb[None, None, :] * gs[j][None, :, None] * at[j].mean() * r[:, None, :]
+        else:
+            bl = gb[None, None, :] * gs[j][None, :, None]
+        xx, _, _ = layer(W, i, xx, pos2, bias_logit=bl, q_temp=at[j] if at is not None else None, q_row=r)
     rows = xx[0, len(kp) - 1:]
     return rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()

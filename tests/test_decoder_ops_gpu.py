@@ -1,7 +1,7 @@
 """GPU parity of the decoder ops of the gated prefill against float32 torch evaluations of the same
 math (the oracle's Qwen3 layer pieces, pinned against transformers by test_oracle_prefill.py):
-residual add + RMSNorm, per-head q/k RMSNorm + RoPE (positions up to 2^17, per-head query scale,
-k/v cache writes), SiLU(gate) * up.  Bound: max-abs <= 2e-2 relative to max(1, |ref|) and
+residual add + RMSNorm, per-head q/k RMSNorm + RoPE (positions up to 2^17, per-head and per-row
+query scales, k/v cache writes), SiLU(gate) * up.  Bound: max-abs <= 2e-2 relative to max(1, |ref|) and
 rel-L2 <= 1e-2 (one bf16 rounding of the output)."""
 import math
 
@@ -66,9 +66,10 @@ def test_qk_norm_rope(cuda, T, H, Hkv, maxpos, scaled):
                           _bf(1 + 0.3 * torch.randn(D, generator=g, device=cuda)), None, None, None, None)
     inv = dec.rope_inv_freq(shape, cuda)
     qs = (0.5 + torch.rand(H, generator=g, device=cuda)) if scaled else None
+    rs = torch.rand(T, generator=g, device=cuda) if scaled else None      # per-row (scaled-softmax r)
     k = torch.empty(T, Hkv, D, dtype=torch.bfloat16, device=cuda)
     v = torch.empty_like(k)
-    q = dec.qk_norm_rope(qkv, pos, lw, shape, inv, k, v, qs)
+    q = dec.qk_norm_rope(qkv, pos, lw, shape, inv, k, v, qs, rs)
     torch.cuda.synchronize()
     x = qkv0.float()
     qr = op.rms(x[:, :H * D].view(T, H, D), lw.q_norm.float(), 1e-6)
@@ -78,7 +79,7 @@ def test_qk_norm_rope(cuda, T, H, Hkv, maxpos, scaled):
     qr = qr * cos + op.rotate_half(qr) * sin
     kr = kr * cos + op.rotate_half(kr) * sin
     if qs is not None:
-        qr = qr * qs[None, :, None]
+        qr = qr * qs[None, :, None] * rs[:, None, None]
     assert_close_grad("q", to_np(q), to_np(qr))
     assert_close_grad("k", to_np(k), to_np(kr))
     assert torch.equal(v.view(T, -1), qkv0[:, (H + Hkv) * D:])

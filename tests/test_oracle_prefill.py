@@ -234,3 +234,36 @@ def test_decode_oracle_first_row_equals_prefill_and_past_form():
         x, _, _ = op.layer(W, i, x, pos)
     ref = op.rms(x[0, len(ids) - 1:], W.final_norm, s.rms_eps) @ W.lm_head.t()
     assert _rel(d, ref) < 1e-5
+
+
+def test_scaled_softmax_reduces_to_mean_temperature_without_pruning():
+    """Scaled-softmax mode with nothing pruned: every kept slot sits at its own position, so
+    r = 1 on every row and the mode equals a uniform temperature mean_h(gamma) on the bias with
+    per-head gamma on the query."""
+    s = Shape(n_layers=3)
+    W = op.Weights(_wts(s, seed=20))
+    head = _head(s, seed=21)
+    head.gate_scale = torch.randn(2, s.n_heads) * 0.3
+    head.attn_scale = torch.randn(2, s.n_heads) * 0.4
+    ids = _prompts([64], s.vocab, 22)
+    head.scaled_softmax = True
+    a = op.prefill(W, head, ids, [4], [60], 0, [1000])          # K >= span: no pruning
+    assert list(a["keep"][0]) == list(range(64))
+    r = og.ssmax_ratio(np.arange(64))
+    assert np.allclose(r, 1.0)
+    # the same run by hand: bias * mean(gamma), query * gamma_h
+    g = torch.nn.functional.softplus(head.attn_scale)
+    gs = torch.nn.functional.softplus(head.gate_scale)
+    x = W.embed[torch.as_tensor(ids[0])][None]
+    pos = torch.arange(64)[None]
+    x, _, _ = op.layer(W, 0, x, pos)
+    kb = torch.as_tensor(a["kept_bias"][0], dtype=torch.float32)
+    for j, i in enumerate(range(1, 3)):
+        bl = kb[None, None, :] * gs[j][None, :, None] * g[j].mean()
+        x, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_temp=g[j], q_row=torch.ones(1, 64))
+    ref = op.rms(x[0, -1], W.final_norm, s.rms_eps) @ W.lm_head.t()
+    assert _rel(a["logits"][0], ref) < 1e-5
+    # and it differs from the per-head temperature mode
+    head.scaled_softmax = False
+    b = op.prefill(W, head, ids, [4], [60], 0, [1000])
+    assert _rel(a["logits"][0], b["logits"][0]) > 1e-4

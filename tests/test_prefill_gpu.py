@@ -30,12 +30,12 @@ pytestmark = pytest.mark.gpu
 SHAPE_KW = dict(n_layers=4, d_model=2048, n_heads=16, n_kv_heads=8, head_dim=128, d_ff=1024, vocab=512)
 
 
-def _setup(cuda, seed=0):
+def _setup(cuda, seed=0, ssmax=False):
     from tokengate_amd import decoder as dec
     from tokengate_amd import gate as G
     shape = dec.DecoderShape(**SHAPE_KW)
     wts = dec.random_decoder(shape, seed=seed, device=cuda, std=0.02, norm_jitter=0.2)
-    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=seed + 5, device=cuda)
+    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=seed + 5, device=cuda, scaled_softmax=ssmax)
     # a visible per-(layer, head) spread of gate scale and temperature
     g = torch.Generator(device=cuda).manual_seed(seed + 9)
     head.gate_scale = head.gate_scale + 0.5 * torch.randn(head.gate_scale.shape, generator=g, device=cuda)
@@ -49,12 +49,12 @@ CASES = {
 }
 
 
-@pytest.mark.parametrize("case", list(CASES))
-def test_prefill_matches_oracle(cuda, case):
+@pytest.mark.parametrize("case,ssmax", [("ragged3", False), ("one", False), ("ragged3", True)])
+def test_prefill_matches_oracle(cuda, case, ssmax):
     from tokengate_amd import prefill as P
     torch.set_num_threads(min(16, torch.get_num_threads()))
     lens, starts, ends, Ks = CASES[case]
-    shape, wts, head = _setup(cuda)
+    shape, wts, head = _setup(cuda, ssmax=ssmax)
     g = torch.Generator().manual_seed(11)
     ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
     r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, capture=True)
@@ -100,7 +100,11 @@ def test_prefill_matches_oracle(cuda, case):
             sc = scores[cu1[b] + starts[b]:cu1[b] + ends[b]]
             bl = torch.as_tensor(og.gate_bias(sc, keeps[b], starts[b], ends[b]), dtype=torch.float32)
             bl = bl[None, None, :] * gs[j][None, :, None]
-            ref, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_temp=at[j])
+            q_row = None
+            if ssmax:
+                q_row = torch.as_tensor(og.ssmax_ratio(keeps[b]), dtype=torch.float32)[None]
+                bl = bl * at[j].mean() * q_row[:, None, :]
+            ref, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_temp=at[j], q_row=q_row)
             assert_close_grad(f"phase2 layer {i} seq {b}", to_np(ins2[j + 1][cu2[b]:cu2[b + 1]]), to_np(ref[0]))
     last = torch.tensor(cu2[1:]) - 1
     ref_logits = op.rms(h2[last], W.final_norm, shape.rms_eps) @ W.lm_head.t()
@@ -113,7 +117,7 @@ def test_prefill_matches_oracle(cuda, case):
         n = r.n_kept[b]
         d = float((h2[cu2[b]:cu2[b + 1]] - e2e["h_last"][b, :n]).norm() / e2e["h_last"][b, :n].norm())
         dl = float((cap["logits"][b].cpu() - e2e["logits"][b]).norm() / e2e["logits"][b].norm())
-        print(f"[e2e] {case} seq {b}: rel-L2 hidden {d:.2e} logits {dl:.2e}", flush=True)
+        print(f"[e2e] {case} ssmax={ssmax} seq {b}: rel-L2 hidden {d:.2e} logits {dl:.2e}", flush=True)
         assert d <= 3e-2 and dl <= 3e-2
 
 

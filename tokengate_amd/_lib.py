@@ -33,7 +33,7 @@ SIGNATURES = {
     "tg_gate_topk_keep": [vp, vp, i32, i32, vp, vp, vp],
     "tg_gate_pack": [vp, i32, vp, vp, i32, i64, vp, vp, vp, f32, vp, vp],
     "tg_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, f32, vp],
-    "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, i64, vp, i64, vp, i64, vp],
+    "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp],
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p}

@@ -88,7 +88,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
                                                       int Hkv, const bf16_t *__restrict__ qw,
                                                       const bf16_t *__restrict__ kw, float eps,
                                                       const float *__restrict__ inv_freq,
-                                                      const float *__restrict__ q_head_scale, bf16_t *q_out,
+                                                      const float *__restrict__ q_head_scale,
+                                                      const float *__restrict__ q_row_scale, bf16_t *q_out,
                                                       int64_t q_rs, bf16_t *__restrict__ k_out, int64_t k_rs,
                                                       bf16_t *__restrict__ v_out, int64_t v_rs) {
   __shared__ float cs[kRopeTok][kHeadDim / 2][2];
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = wf[e] * (x[e] * rinv);
     const float sgn = j < 8 ? -1.f : 1.f;
-    const float hs = (is_q && q_head_scale) ? q_head_scale[rr] : 1.f;
+    const float hs = is_q ? (q_head_scale ? q_head_scale[rr] : 1.f) * (q_row_scale ? q_row_scale[t] : 1.f) : 1.f;
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -221,8 +222,8 @@ extern "C" int tg_rmsnorm(const void *x, int64_t x_row_stride, const void *resid
 extern "C" int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const int64_t *positions, int64_t n_tokens,
                                int32_t num_heads, int32_t num_heads_k, int32_t head_dim, const void *q_norm_weight,
                                const void *k_norm_weight, float eps, const float *inv_freq, const float *q_head_scale,
-                               void *q_out, int64_t q_row_stride, void *k_out, int64_t k_row_stride, void *v_out,
-                               int64_t v_row_stride, hipStream_t stream) {
+                               const float *q_row_scale, void *q_out, int64_t q_row_stride, void *k_out,
+                               int64_t k_row_stride, void *v_out, int64_t v_row_stride, hipStream_t stream) {
   clear_error();
   TG_CHECK(qkv && positions && q_norm_weight && k_norm_weight && inv_freq && q_out && k_out && v_out,
            "qk_norm_rope: null pointer");
@@ -246,7 +247,7 @@ extern "C" int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const in
   hipLaunchKernelGGL(qk_rope_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const bf16_t *>(qkv), qkv_row_stride, positions, n_tokens, num_heads, num_heads_k,
                      static_cast<const bf16_t *>(q_norm_weight), static_cast<const bf16_t *>(k_norm_weight), eps,
-                     inv_freq, q_head_scale, static_cast<bf16_t *>(q_out), q_row_stride,
+                     inv_freq, q_head_scale, q_row_scale, static_cast<bf16_t *>(q_out), q_row_stride,
                      static_cast<bf16_t *>(k_out), k_row_stride, static_cast<bf16_t *>(v_out), v_row_stride);
   TG_HIP_CHECK(hipGetLastError());
   return 0;

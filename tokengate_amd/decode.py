@@ -65,12 +65,19 @@ class DecodeState:
                 cap = max(n) + max_new_tokens
                 bias = torch.zeros(B, shape.n_heads, cap, dtype=torch.float32, device=dev)
                 for b in range(B):
-                    bias[b, :, :n[b]] = coef[j][:, None] * kept_bias[pf.cu_kept[b]:pf.cu_kept[b + 1]][None, :]
+                    kb = kept_bias[pf.cu_kept[b]:pf.cu_kept[b + 1]]
+                    if pf.kept_ratio is not None:            # scaled softmax: keys keep their prefill r
+                        kb = kb * pf.kept_ratio[pf.cu_kept[b]:pf.cu_kept[b + 1]]
+                    bias[b, :, :n[b]] = coef[j][:, None] * kb[None, :]
                 lc.bias = bias
                 lc.qscale = qs[j].contiguous() if qs is not None else None
             self.layers.append(lc)
         last = torch.tensor([pf.cu_kept[b + 1] - 1 for b in range(B)], dtype=torch.int64)
         self.next_pos = pf.kept_positions.index_select(0, h2d(last, dev)) + 1
+        self.gate_layer = gate_layer
+        self.ssmax = pf.kept_ratio is not None
+        self.n_kept_f = h2d(torch.tensor([float(x) for x in pf.n_kept], dtype=torch.float32), dev)
+        self.steps = 0
 
     def _attend(self, lc: _LayerCache, q: torch.Tensor, out: torch.Tensor) -> None:
         """q (B, H, D) -> out (B, H, D): sequence b attends over its segment's n[b] rows."""
@@ -104,6 +111,11 @@ class DecodeState:
         kn = torch.empty(B, s.n_kv_heads, s.head_dim, dtype=x.dtype, device=dev)
         vn = torch.empty_like(kn)
         att = torch.empty(B, s.n_heads, s.head_dim, dtype=x.dtype, device=dev)
+        r_dec = None
+        if self.ssmax:   # the new token's own ratio: slot n_kept + 1 + step at position next_pos
+            m = (self.n_kept_f + 1.0 + self.steps).clamp(min=2.0)
+            p = (self.next_pos.to(torch.float32) + 1.0).clamp(min=2.0)
+            r_dec = (torch.log(m) / torch.log(p)).clamp(max=1.0)
         for l, lc in enumerate(self.layers):
             lw = w.layers[l]
             if l == 0:
@@ -111,7 +123,8 @@ class DecodeState:
             else:
                 rmsnorm(hid, lw.ln1, s.rms_eps, residual=res, residual_out=res, out=normed)
             torch.matmul(normed, lw.w_qkv.t(), out=qkv)
-            q = qk_norm_rope(qkv, self.next_pos, lw, s, w.inv_freq, kn, vn, lc.qscale)
+            q = qk_norm_rope(qkv, self.next_pos, lw, s, w.inv_freq, kn, vn, lc.qscale,
+                             r_dec if (r_dec is not None and l > self.gate_layer) else None)
             rows = torch.tensor([lc.seg[b] + lc.n[b] for b in range(B)], dtype=torch.int64)
             rows = h2d(rows, dev)
             lc.k.index_copy_(0, rows, kn)
@@ -126,6 +139,7 @@ class DecodeState:
             torch.matmul(act, lw.w_down.t(), out=hid)
         h = hid + res
         self.next_pos = self.next_pos + 1
+        self.steps += 1
         logits = logits_last(w, h, torch.arange(B, device=dev))
         self.last_logits = logits
         return logits.argmax(-1)

@@ -132,16 +132,21 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, residual: Optional[tor
 
 def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, lw: LayerWeights, shape: DecoderShape,
                  inv_freq: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor,
-                 q_head_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 q_head_scale: Optional[torch.Tensor] = None,
+                 q_row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Normalises and rotates q in place inside qkv (returned as a (T, H, D) view) and writes the
-    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous)."""
+    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous).  q is scaled by
+    q_head_scale (H,) and q_row_scale (T,) fp32 when given."""
     T = qkv.shape[0]
     H, Hkv, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
     if positions.dtype != torch.int64 or positions.numel() != T:
         raise RuntimeError("qk_norm_rope: positions must be int64 with one entry per token")
+    if q_row_scale is not None and (q_row_scale.dtype != torch.float32 or q_row_scale.numel() < T):
+        raise RuntimeError("qk_norm_rope: q_row_scale must be fp32 with one entry per token")
     _lib.call("tg_qk_norm_rope", qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), T, H, Hkv, D,
               lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), float(shape.rms_eps), inv_freq.data_ptr(),
               q_head_scale.data_ptr() if q_head_scale is not None else None,
+              q_row_scale.data_ptr() if q_row_scale is not None else None,
               qkv.data_ptr(), qkv.stride(0), k_out.data_ptr(), k_out.stride(0), v_out.data_ptr(), v_out.stride(0),
               _stream(qkv))
     return qkv[:, :H * D].view(T, H, D) if qkv.is_contiguous() else qkv[:, :H * D].unflatten(1, (H, D))
@@ -233,11 +238,13 @@ class Workspace:
 
 
 def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws: Workspace,
-               kv: List[Optional[LayerKV]], biases=None, q_scales=None, capture: Optional[list] = None) -> torch.Tensor:
+               kv: List[Optional[LayerKV]], biases=None, q_scales=None, capture: Optional[list] = None,
+               q_row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Runs decoder layers `layer_ids` over the packed rows x (T, d) and returns the hidden state
     after the last of them (T, d).  kv[i] receives layer i's cache rows.  biases[i] / q_scales[i]
     (optional): Phase-2 raw-unit key bias (nseq, H, >= max_len) and per-head query scale (H,)
-    fp32 of layer i.  capture: optional list that receives each layer's input hidden state."""
+    fp32 of layer i; q_row_scale (T,) fp32: a per-row query scale for every layer (the
+    scaled-softmax ratio).  capture: optional list that receives each layer's input hidden state."""
     shape = wts.shape
     T = geo.total
     if x.shape != (T, shape.d_model):
@@ -259,7 +266,7 @@ def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws:
             capture.append(res.clone())
         torch.matmul(normed, lw.w_qkv.t(), out=qkv)
         q = qk_norm_rope(qkv, geo.positions, lw, shape, wts.inv_freq, kv[i].k, kv[i].v,
-                         q_scales[i] if q_scales is not None else None)
+                         q_scales[i] if q_scales is not None else None, q_row_scale)
         varlen_attention(q, kv[i].k, kv[i].v, geo.cu_dev, geo.max_len, scale,
                          biases[i] if biases is not None else None, out=attn, lse=lse)
         torch.matmul(attn.view(T, -1), lw.w_o.t(), out=hid)

@@ -197,23 +197,51 @@ class ScoringHead:
     b2: float
     gate_scale: torch.Tensor    # (n_phase2_layers, H) fp32, pre-softplus
     attn_scale: Optional[torch.Tensor] = None   # (n_phase2_layers, H) fp32, pre-softplus
+    # scaled-softmax mode (E2EGate.scaled_softmax_scale, e2e_gate_module.py:229): the temperature
+    # becomes gamma_h * r_q per query and the bias is scaled by mean_h(gamma) * r_k per key, with
+    # r = min(1, ln max(slot, 2) / ln max(position + 1, 2)) (_ssmax_ratio, gate_forward.py:574-585;
+    # _phase2_q_bias, qwen3_flex_attention.py:433-473).  Needs attn_scale.
+    scaled_softmax: bool = False
 
     def scores(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         return score_mlp(x, self.w1, self.b1, self.w2, self.b2, out=out)
 
+    @property
+    def ssmax(self) -> bool:
+        return self.scaled_softmax and self.attn_scale is not None
+
     def layer_coefficients(self, softmax_scale: float) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
         """(bias coefficient in raw-score units, per-head query scale) per (layer, head):
-        raw bias of key j = normalised score_j * softplus(gate_scale) * temperature / softmax_scale."""
+        raw bias of key j = normalised score_j * coef[l, h] (* r_j in scaled-softmax mode), where
+        coef = softplus(gate_scale) * temperature / softmax_scale; the temperature is
+        softplus(attn_scale) per head, or its mean over heads in scaled-softmax mode."""
         coef = torch.nn.functional.softplus(self.gate_scale.float())
         qs = None
         if self.attn_scale is not None:
             qs = torch.nn.functional.softplus(self.attn_scale.float()).contiguous()
-            coef = coef * qs
+            coef = coef * (qs.mean(1, keepdim=True) if self.scaled_softmax else qs)
         return (coef / softmax_scale).contiguous(), qs
 
 
+def ssmax_ratio_rows(kept_pos: torch.Tensor, cu_kept: Sequence[int]) -> torch.Tensor:
+    """r per packed kept row: min(1, ln max(m, 2) / ln max(p + 1, 2)), m the row's 1-based slot
+    within its sequence and p its original position (_ssmax_ratio, gate_forward.py:574-585);
+    fp32 on the rows' device, built without a host synchronisation."""
+    dev = kept_pos.device
+    T = int(cu_kept[-1])
+    n = torch.tensor([cu_kept[b + 1] - cu_kept[b] for b in range(len(cu_kept) - 1)], dtype=torch.int64)
+    st = torch.tensor(list(cu_kept[:-1]), dtype=torch.int64)
+    if dev.type == "cuda":
+        n, st = n.pin_memory().to(dev, non_blocking=True), st.pin_memory().to(dev, non_blocking=True)
+    slot = torch.arange(T, device=dev) - torch.repeat_interleave(st, n, output_size=T) + 1
+    m = slot.to(torch.float32).clamp(min=2.0)
+    pos = (kept_pos.to(torch.float32) + 1.0).clamp(min=2.0)
+    return (torch.log(m) / torch.log(pos)).clamp(max=1.0)
+
+
 def random_head(n_layers: int, n_heads: int, seed: int = 5, device="cuda", d_in: int = 2048, d_hidden: int = 256,
-                gate_scale: Optional[float] = None, temperature: bool = True) -> ScoringHead:
+                gate_scale: Optional[float] = None, temperature: bool = True,
+                scaled_softmax: bool = False) -> ScoringHead:
     """Seeded head: Xavier-uniform W1 / w2, zero b1 / b2; gate_scale = softplus^-1(1.0) (or a
     given value) plus a small seeded spread per (layer, head); attn_scale = softplus^-1(1), the
     identity temperature E2EGate starts from."""
@@ -226,4 +254,4 @@ def random_head(n_layers: int, n_heads: int, seed: int = 5, device="cuda", d_in:
     base = math.log(math.expm1(1.0)) if gate_scale is None else gate_scale
     gs = base + 0.1 * torch.randn(n_layers, n_heads, generator=g, device=device)
     at = torch.full((n_layers, n_heads), math.log(math.expm1(1.0)), device=device) if temperature else None
-    return ScoringHead(w1, b1, w2, 0.0, gs, at)
+    return ScoringHead(w1, b1, w2, 0.0, gs, at, scaled_softmax)

@@ -259,6 +259,7 @@ def save_head(head: G.ScoringHead, path: str) -> None:
          "gate_scale": head.gate_scale.cpu()}
     if head.attn_scale is not None:
         t["attn_scale"] = head.attn_scale.cpu()
+    t["scaled_softmax"] = torch.tensor([1 if head.scaled_softmax else 0], dtype=torch.int32)
     save_file({k: v.contiguous() for k, v in t.items()}, path)
 
 
@@ -268,7 +269,8 @@ def load_head(path: str, device) -> G.ScoringHead:
     return G.ScoringHead(t["w1"].to(device, torch.bfloat16), t["b1"].to(device, torch.float32),
                          t["w2"].to(device, torch.float32), float(t["b2"].item()),
                          t["gate_scale"].to(device, torch.float32),
-                         t["attn_scale"].to(device, torch.float32) if "attn_scale" in t else None)
+                         t["attn_scale"].to(device, torch.float32) if "attn_scale" in t else None,
+                         bool(int(t["scaled_softmax"].item())) if "scaled_softmax" in t else False)
 
 
 def load_model(checkpoint: str = "random", base_model: Optional[str] = None, gate_layer: Optional[int] = None,

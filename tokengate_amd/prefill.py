@@ -40,6 +40,7 @@ class PrefillResult:
     kv: List[LayerKV]                 # per layer: Phase-1 rows (cu_prompt) at/below the gate, kept rows above
     cu_prompt: List[int]
     kept_bias: torch.Tensor           # (total_kept,) fp32 normalised gate score (0 on prefix / suffix)
+    kept_ratio: Optional[torch.Tensor] = None   # (total_kept,) fp32 scaled-softmax ratio r (ssmax heads)
     phase_ms: Dict[str, float] = field(default_factory=dict)
     capture: Optional[dict] = None
 
@@ -74,17 +75,20 @@ class Phase2Graphs:
 
     def run(self, wts: DecoderWeights, layer_ids: List[int], hs: torch.Tensor, positions: torch.Tensor,
             cu_dev: torch.Tensor, coef: torch.Tensor, bias_pad: torch.Tensor, qscale: Optional[torch.Tensor],
-            mlp_rows: int):
+            mlp_rows: int, row_scale: Optional[torch.Tensor] = None):
         shape = wts.shape
         dev = hs.device
         nseq = cu_dev.numel() - 1
         T2, max_kept = hs.shape[0], bias_pad.shape[1]
         Tb, Lb = self._up(T2, self.bucket_rows), self._up(max_kept, self.bucket_len)
-        key = (nseq, Tb, Lb, tuple(layer_ids), qscale is not None)
+        key = (nseq, Tb, Lb, tuple(layer_ids), qscale is not None, row_scale is not None)
         ent = self.graphs.get(key)
         if ent is None:
-            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, qscale is not None, mlp_rows, dev)
+            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, qscale is not None, row_scale is not None, mlp_rows,
+                                dev)
             self.graphs[key] = ent
+        if row_scale is not None:
+            ent["rs"][:T2].copy_(row_scale)
         ent["x"][:T2].copy_(hs)
         ent["x"][T2:].zero_()
         ent["pos"][:T2].copy_(positions)
@@ -96,7 +100,7 @@ class Phase2Graphs:
         ent["graph"].replay()
         return ent["out"][:T2], {l: LayerKV(ent["kv"][l].k[:T2], ent["kv"][l].v[:T2]) for l in layer_ids}
 
-    def _capture(self, wts, layer_ids, nseq, Tb, Lb, with_qs, mlp_rows, dev):
+    def _capture(self, wts, layer_ids, nseq, Tb, Lb, with_qs, with_rs, mlp_rows, dev):
         shape = wts.shape
         L2 = len(layer_ids)
         x = torch.zeros(Tb, shape.d_model, dtype=torch.bfloat16, device=dev)
@@ -105,6 +109,7 @@ class Phase2Graphs:
         cu[-1] = Tb
         bias = torch.zeros(L2, nseq, shape.n_heads, Lb, dtype=torch.float32, device=dev)
         qs = torch.ones(L2, shape.n_heads, dtype=torch.float32, device=dev) if with_qs else None
+        rs = torch.ones(Tb, dtype=torch.float32, device=dev) if with_rs else None
         kv: List[Optional[LayerKV]] = [None] * shape.n_layers
         for l in layer_ids:
             kv[l] = alloc_kv(shape, Tb, dev)
@@ -115,12 +120,12 @@ class Phase2Graphs:
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales)   # warm-up
+            run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales, q_row_scale=rs)   # warm-up
         torch.cuda.current_stream(dev).wait_stream(side)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            out = run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales)
-        return dict(graph=g, x=x, pos=pos, cu=cu, bias=bias, qs=qs, kv=kv, ws=ws, out=out)
+            out = run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales, q_row_scale=rs)
+        return dict(graph=g, x=x, pos=pos, cu=cu, bias=bias, qs=qs, rs=rs, kv=kv, ws=ws, out=out)
 
 
 @torch.no_grad()
@@ -194,13 +199,18 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
     st = torch.tensor(p.cu_kept[:-1], dtype=torch.int64)[:, None]
     en = torch.tensor(p.cu_kept[1:], dtype=torch.int64)[:, None] - 1
     idx = torch.minimum(st + t_[None, :], en)
-    bias_pad = kept_bias[h2d(idx, dev)]                     # (B, max_kept)
+    idx_d = h2d(idx, dev)
+    bias_pad = kept_bias[idx_d]                                               # (B, max_kept)
+    ratio = None
+    if head.ssmax:
+        ratio = G.ssmax_ratio_rows(kept_pos, p.cu_kept)                       # (T2,)
+        bias_pad = bias_pad * ratio[idx_d]
     coef, qscale = head.layer_coefficients(1.0 / math.sqrt(shape.head_dim))  # (L2, H)
     cu2_dev = h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev)
     above = list(range(gate_layer + 1, n_layers))
     biases_all = None
     if phase2_graphs is not None and cap is None:
-        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, coef, bias_pad, qscale, mlp_rows)
+        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, coef, bias_pad, qscale, mlp_rows, ratio)
         for l in above:
             kv[l] = kv2[l]
     else:
@@ -212,7 +222,7 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
             kv[l] = alloc_kv(shape, T2, dev)
         ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
         h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
-                        capture=cap["phase2"] if cap else None)
+                        capture=cap["phase2"] if cap else None, q_row_scale=ratio)
 
     mark("head")
     last = h2d(torch.tensor(p.cu_kept[1:], dtype=torch.int64).sub_(1), dev)
@@ -227,7 +237,8 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
     if cap is not None:
         cap.update(scores=scores, keep=keep, hs_packed=hs, h2=h2, logits=logits, biases_all=biases_all,
                    qscale=qscale, bias_pad=bias_pad)
-    return PrefillResult(first, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, phase_ms, cap)
+    return PrefillResult(first, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, ratio, phase_ms,
+                         cap)
 
 
 def ttft_ms(fn, reps: int = 5, warmup: int = 1) -> List[float]:
