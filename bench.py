@@ -195,7 +195,10 @@ def bench_ttft(dev, reps=5):
     RoPE theta 1e6, bf16), gate at layer 1 (scoring head Linear(2048->256)->SiLU->Linear(256->1)),
     prompts of uniform random ids already on the device, state span = prompt minus a 64-token
     prefix and a 256-token suffix.  Protocol of the reference's TTFT bench: sync, perf_counter,
-    prefill through the first token, sync; median of `reps` after one warmup."""
+    prefill through the first token, sync; median of `reps` after one warmup.  The "_branch" line
+    runs the finalized gate instead: the MLP scoring branch (a copy of the gate layer's SwiGLU, I
+    6144, with an absorbed (1, I) readout row) on the gate layer's attention boundary, the gate
+    layer's MLP on the kept rows only, scaled softmax in Phase 2."""
     import statistics
     import torch
     from tokengate_amd import decoder as dec
@@ -207,7 +210,9 @@ def bench_ttft(dev, reps=5):
     g = torch.Generator().manual_seed(7)
     out = {}
 
-    def run(name, lens, Ks):
+    branch = G.random_branch_head(wts, 1, seed=5)
+
+    def run(name, lens, Ks, head=head):
         ids = [torch.randint(0, shape.vocab, (n,), generator=g).to(dev) for n in lens]
         starts = [64] * len(lens)
         ends = [n - 256 for n in lens]
@@ -235,6 +240,7 @@ def bench_ttft(dev, reps=5):
     for K in (100, 2000):
         run(f"32k_K{K}", [32768], [K])
     run("32k_Kall", [32768], [10_000_000])
+    run("32k_K2000_branch", [32768], [2000], head=branch)
     rng = torch.Generator().manual_seed(17)
     lens = [int(x) for x in torch.randint(16384, 131073, (8,), generator=rng)]
     Ks = [[100, 500, 2000, 4000][int(i)] for i in torch.randint(0, 4, (8,), generator=rng)]

@@ -180,6 +180,14 @@ int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const int64_t *posi
 int tg_silu_mul(const void *gate_up, int64_t gate_up_row_stride, int64_t n_rows, int32_t inter,
                 void *out, int64_t out_row_stride, hipStream_t stream);
 
+/* The finalized gate's scoring readout on the fused gate/up projection of its MLP branch:
+ * scores[r] = bf16(w_row . bf16(bf16(silu(gate_up[r, :inter])) * gate_up[r, inter:])) as fp32 —
+ * the branch Qwen3MLP whose down_proj is the absorbed (1, inter) row (gate_branch_hs,
+ * gate_forward.py:491-524; build_gate_branch :261-342; load_gate e2e_gate_module.py:497-514), fed
+ * z = post_attention_layernorm(a) of the gate layer's attention boundary a.  w_row: inter bf16. */
+int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_stride, int64_t n_rows, int32_t inter,
+                           const void *w_row, float *scores, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

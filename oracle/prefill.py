@@ -16,8 +16,13 @@ Restates, for a Qwen3-shaped decoder given as float32 weights:
     (B, n_alloc) batch whose pad slots carry a -1e9 bias, layers above the gate on that batch
     with RoPE at the kept original positions, first token = argmax of the LM head at each
     sample's last kept row.
-Pinned by tests/test_oracle_prefill.py against transformers' own Qwen3DecoderLayer (same
-weights, float32, eager attention) and by padded-vs-per-sequence equivalence.
+  * the finalized gate's MLP scoring branch (gate_branch_hs, gate_forward.py:491-524): score =
+    w_row . (silu(W_gate z) * (W_up z)), z = post_attention_layernorm(a) of the gate layer's
+    attention boundary a; with it the oracle still runs the gate layer whole on every row and
+    gathers the kept rows afterwards — the unsplit form the split prefill must equal.
+Pinned by tests/test_oracle_prefill.py against transformers' own Qwen3DecoderLayer and Qwen3MLP
+(same weights, float32, eager attention; the branch as load_gate rebuilds it, a Qwen3MLP with a
+(1, I) down_proj, e2e_gate_module.py:497-514) and by padded-vs-per-sequence equivalence.
 """
 import math
 from typing import List, Optional, Sequence
@@ -66,13 +71,14 @@ class Weights:
 
 
 def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
-          q_temp: Optional[torch.Tensor] = None, q_row: Optional[torch.Tensor] = None):
+          q_temp: Optional[torch.Tensor] = None, q_row: Optional[torch.Tensor] = None, boundary: Optional[list] = None):
     """One decoder layer on a batch x (B, n, d) float32 at positions pos (B, n); bias_logit
     (B, H, n) per-key logit bias or None; q_temp (H,) per-head temperature or None.  Without
     q_row the temperature multiplies the query and the bias per head (_phase2_q_bias, attn_scale
     branch); with q_row (B, n) — the scaled-softmax mode — the query is scaled by
     q_temp[h] * q_row[b, i] and bias_logit is used as given (the caller folds in
-    mean_h(temperature) * r_k).  Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE."""
+    mean_h(temperature) * r_k).  Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE;
+    boundary (a list), if given, receives the attention residual a = x + o_proj(attn)."""
     s = W.shape
     L = W.layers[i]
     B, n, _ = x.shape
@@ -100,15 +106,42 @@ def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Op
         q = q * q_row[:, :, None, None]
     attn, _ = oat.fwd(q, k, v, braw, scale, causal=True)
     x = x + attn.reshape(B, n, H * D) @ L["wo"].t()
-    h = rms(x, L["ln2"], s.rms_eps)
-    x = x + (F.silu(h @ L["wg"].t()) * (h @ L["wu"].t())) @ L["wd"].t()
-    return x, k, v
+    if boundary is not None:
+        boundary.append(x)
+    return mlp_half(W, i, x), k, v
+
+
+def mlp_half(W: Weights, i: int, a: torch.Tensor) -> torch.Tensor:
+    """Layer i's MLP half: a + down(silu(gate) * up)(post_attention_layernorm(a))."""
+    L = W.layers[i]
+    h = rms(a, L["ln2"], W.shape.rms_eps)
+    return a + (F.silu(h @ L["wg"].t()) * (h @ L["wu"].t())) @ L["wd"].t()
 
 
 def head_scores(head, h: torch.Tensor) -> np.ndarray:
     """The scoring head on rows h (n, d), float64."""
     return og.score_mlp(h.double().numpy(), head.w1.float().cpu().numpy(), head.b1.cpu().numpy(),
                         head.w2.cpu().numpy(), head.b2)
+
+
+def branch_scores(head, a: torch.Tensor, ln2: torch.Tensor, eps: float) -> torch.Tensor:
+    """The finalized gate's scoring branch on boundary rows a (n, d), float32:
+    w_row . (silu(W_gate z) * (W_up z)), z = rms(a) * ln2 (gate_branch_hs, absorbed readout)."""
+    wg, wu = head.w_gu.float().cpu().chunk(2, 0)
+    z = rms(a.float(), ln2.float(), eps)
+    return (F.silu(z @ wg.t()) * (z @ wu.t())) @ head.w_row.float().cpu()
+
+
+def _is_branch(head) -> bool:
+    return bool(getattr(head, "split_gate_layer", False))
+
+
+def gate_scores(W: Weights, head, gate_layer: int, a: torch.Tensor, h: torch.Tensor) -> np.ndarray:
+    """Scores of state rows, float64: the branch on the gate layer's boundary rows a, or the
+    synthetic head on its output rows h."""
+    if _is_branch(head):
+        return branch_scores(head, a, W.layers[gate_layer]["ln2"], W.shape.rms_eps).double().numpy()
+    return head_scores(head, h)
 
 
 def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art_ends, gate_layer: int, K,
@@ -126,14 +159,17 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
         ids[b, :lens[b]] = torch.as_tensor(list(x), dtype=torch.long)
     x = W.embed[ids]
     pos = torch.arange(S)[None, :].expand(B, S)
+    bnd = []
     for i in range(gate_layer + 1):
-        x, _, _ = layer(W, i, x, pos)
+        x, _, _ = layer(W, i, x, pos, boundary=bnd)
+    a = bnd[-1]
     Ks = K if isinstance(K, (list, tuple)) else [K] * B
     keeps, biases, h_gate = [], [], []
     for b in range(B):
         st, en = art_starts[b], art_ends[b]
         h_gate.append(x[b, :lens[b]].clone())
-        sc = scores_override[b] if scores_override is not None else head_scores(head, x[b, st:en])
+        sc = (scores_override[b] if scores_override is not None
+              else gate_scores(W, head, gate_layer, a[b, st:en], x[b, st:en]))
         kp = keep_override[b] if keep_override is not None else og.keep_indices(sc, Ks[b], st, en, lens[b])
         keeps.append(np.asarray(kp, dtype=np.int64))
         biases.append(og.gate_bias(sc, keeps[-1], st, en))
@@ -148,7 +184,7 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
         gb[b, :len(kt)] = torch.as_tensor(biases[b])
     if tuple(head.gate_scale.shape) != (s.n_layers - gate_layer - 1, s.n_heads):
         raise ValueError("gate_scale must be (layers above the gate, heads)")
-    gs = F.softplus(head.gate_scale.float().cpu())                  # (L2, H)
+    gs = F.softplus(head.gate_scale.float().cpu()) * float(getattr(head, "bias_gain", 1.0))   # (L2, H)
     at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
     ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
     r = torch.as_tensor(og.ssmax_ratio(kpos.numpy()), dtype=torch.float32) if ssmax else None   # (B, n_alloc)
@@ -216,19 +252,20 @@ def decode_logits(W: Weights, head, ids: Sequence[int], art_start: int, art_end:
     x = W.embed[torch.as_tensor(list(ids), dtype=torch.long)][None]
     xg = W.embed[torch.as_tensor(list(gen), dtype=torch.long)][None]
     pos = torch.arange(L)[None]
+    bnd = []
     for i in range(gate_layer + 1):
-        xn, k, v = layer(W, i, x, pos)
+        xn, k, v = layer(W, i, x, pos, boundary=bnd)
         if prune_below_gate:
             k, v = k[:, kp], v[:, kp]
         if g:
             xg, _, _ = layer_with_past(W, i, xg, gpos, k, v)
         x = xn
-    sc = head_scores(head, x[0, art_start:art_end])
+    sc = gate_scores(W, head, gate_layer, bnd[-1][0, art_start:art_end], x[0, art_start:art_end])
     kb = torch.as_tensor(og.gate_bias(sc, np.asarray(keep), art_start, art_end), dtype=torch.float32)
     gb = torch.cat([kb, torch.zeros(g)])
     xx = torch.cat([x[0, kp], xg[0]])[None]
     pos2 = torch.cat([kp[None], gpos], 1)
-    gs = F.softplus(head.gate_scale.float().cpu())
+    gs = F.softplus(head.gate_scale.float().cpu()) * float(getattr(head, "bias_gain", 1.0))
     at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
     ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
     # scaled softmax: the ratio over kept ++ generated slots (a generated token's slot is n_kept + 1 + i)

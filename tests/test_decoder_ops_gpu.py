@@ -99,6 +99,28 @@ def test_silu_mul(cuda, rows, inter):
     assert_close_grad("silu_mul", to_np(out), to_np(ref))
 
 
+@pytest.mark.parametrize("rows,inter", [(1, 8), (777, 6144), (130, 1000)])
+def test_branch_readout(cuda, rows, inter):
+    """The scoring branch's readout against torch's own bf16 evaluation of the absorbed branch
+    (F.silu and the product in bf16, as an eager bf16 Qwen3MLP computes them; the (1, I) down row
+    as an fp32-accumulated dot rounded to bf16): equal up to one bf16 ulp from the summation
+    order, and equal on nearly every row."""
+    from tokengate_amd import gate as G
+    g = torch.Generator(device=cuda).manual_seed(rows + inter)
+    gu = _bf(torch.randn(rows, 2 * inter + 16, generator=g, device=cuda) * 2)[:, :2 * inter]   # padded rows
+    w = _bf(torch.randn(inter, generator=g, device=cuda) * inter ** -0.5)
+    got = G.branch_readout(gu, w)
+    torch.cuda.synchronize()
+    act = torch.nn.functional.silu(gu[:, :inter]) * gu[:, inter:]          # bf16, torch's roundings
+    exact = act.double() @ w.double()
+    ref = exact.to(torch.bfloat16).float()
+    assert torch.equal(got, got.to(torch.bfloat16).float())                # bf16 values
+    ulp = torch.finfo(torch.bfloat16).eps * ref.abs().clamp(min=1e-30)
+    assert bool(((got - ref).abs() <= ulp + 1e-6).all())
+    assert float((got == ref).float().mean()) >= 0.95    # a skipped bf16 rounding of silu or of the
+    #                                                       product moves ~1/4 of the rows by an ulp
+
+
 def test_decoder_op_errors(cuda):
     from tokengate_amd import decoder as dec
     x = torch.zeros(4, 2050, dtype=torch.bfloat16, device=cuda)

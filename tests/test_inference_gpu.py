@@ -16,10 +16,13 @@ pytestmark = pytest.mark.gpu
 SMALL = dict(n_layers=4, d_model=2048, n_heads=16, n_kv_heads=8, head_dim=128, d_ff=1024, vocab=512)
 
 
-def _model(cuda, seed=3, ssmax=False):
+def _model(cuda, seed=3, ssmax=False, branch=False):
     from tokengate_amd import decoder as dec
+    from tokengate_amd import gate as G
     from tokengate_amd import inference as I
     m = I.load_model(f"random:{seed}", gate_layer=1, device=cuda, shape=dec.DecoderShape(**SMALL))
+    if branch:      # the finalized gate: MLP scoring branch, split gate layer
+        m.gate = G.random_branch_head(m.weights, 1, seed=seed + 40)
     m.gate.scaled_softmax = ssmax
     if ssmax:   # a visible temperature spread, so r and gamma both matter
         g = torch.Generator(device=cuda).manual_seed(seed)
@@ -37,12 +40,13 @@ def _prompts(lens, spans, seed):
     return out
 
 
-@pytest.mark.parametrize("prune_below_gate,ssmax", [(False, False), (True, False), (False, True)])
-def test_decode_matches_oracle(cuda, prune_below_gate, ssmax):
+@pytest.mark.parametrize("prune_below_gate,ssmax,branch", [(False, False, False), (True, False, False),
+                                                             (False, True, False), (True, True, True)])
+def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch):
     from tokengate_amd import inference as I
     from tokengate_amd.decode import DecodeState
     torch.set_num_threads(min(16, torch.get_num_threads()))
-    m = _model(cuda, ssmax=ssmax)
+    m = _model(cuda, ssmax=ssmax, branch=branch)
     lens, spans, Ks = [600, 333], [(20, 500), (0, 300)], [64, 1000]
     split = [I.split_state_span(p) for p in _prompts(lens, spans, 5)]
     pf = m.prefill(split, Ks, prune_below_gate=prune_below_gate)

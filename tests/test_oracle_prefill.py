@@ -8,6 +8,10 @@
   right-padded Phase 1 equals the unpadded one, so the packed (cu_seqlens) layout of the product
   computes the same function.
 * The keep lists and kept bias follow oracle.gate on the oracle's own scores.
+* The finalized gate's scoring branch against transformers' Qwen3MLP with the (1, I) absorbed
+  down_proj that load_gate rebuilds (e2e_gate_module.py:497-514), fed Qwen3RMSNorm of the
+  gate layer's attention boundary; the boundary against the transformers layer with its MLP
+  output zeroed; and the split (MLP on kept rows only) against the whole layer's kept rows.
 """
 import math
 from dataclasses import dataclass
@@ -166,15 +170,71 @@ def _head(s: Shape, seed=3):
                 torch.randn(s.n_layers - 2, s.n_heads, generator=g) * 0.3 + math.log(math.expm1(1.0)))
 
 
+@dataclass
+class BHead:
+    w_gu: torch.Tensor
+    w_row: torch.Tensor
+    gate_scale: torch.Tensor
+    attn_scale: torch.Tensor
+    scaled_softmax: bool = True
+    bias_gain: float = 1.0
+    split_gate_layer = True
+
+
+def _bhead(s: Shape, n_above: int, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    return BHead(torch.randn(2 * s.d_ff, s.d_model, generator=g) * 0.05, torch.randn(s.d_ff, generator=g) * 0.1,
+                 torch.randn(n_above, s.n_heads, generator=g) * 0.3,
+                 torch.randn(n_above, s.n_heads, generator=g) * 0.3 + math.log(math.expm1(1.0)))
+
+
+def test_branch_scores_boundary_and_split_match_transformers():
+    from types import SimpleNamespace
+    s = Shape()
+    wts = _wts(s, seed=30)
+    W = op.Weights(wts)
+    head = _bhead(s, 1, seed=31)
+    g = torch.Generator().manual_seed(32)
+    B, n = 2, 50
+    x = torch.randn(B, n, s.d_model, generator=g)
+    pos = torch.arange(n)[None].expand(B, n).contiguous()
+    bnd = []
+    full, _, _ = op.layer(W, 1, x, pos, boundary=bnd)
+    a = bnd[0]
+    # boundary == the transformers layer with its MLP output zeroed (down_proj = 0)
+    lw = wts.layers[1]
+    zero_mlp = LW(lw.ln1, lw.w_qkv, lw.q_norm, lw.k_norm, lw.w_o, lw.ln2, lw.w_gu, torch.zeros_like(lw.w_down))
+    ref_a = _hf_run(s, zero_mlp, x, pos, _causal_mask(B, n))
+    assert _rel(a, ref_a) < 1e-5
+    # the branch: a stock Qwen3MLP whose down_proj is the (1, I) absorbed row, fed Qwen3RMSNorm(a)
+    mlp = mq.Qwen3MLP(SimpleNamespace(hidden_size=s.d_model, intermediate_size=s.d_ff, hidden_act="silu"))
+    mlp.down_proj = torch.nn.Linear(s.d_ff, 1, bias=False)
+    norm = mq.Qwen3RMSNorm(s.d_model, eps=s.rms_eps)
+    with torch.no_grad():
+        mlp.gate_proj.weight.copy_(head.w_gu[:s.d_ff])
+        mlp.up_proj.weight.copy_(head.w_gu[s.d_ff:])
+        mlp.down_proj.weight.copy_(head.w_row[None])
+        norm.weight.copy_(lw.ln2)
+        ref_sc = mlp(norm(ref_a))[..., 0]
+    ours_sc = op.branch_scores(head, a.reshape(-1, s.d_model), lw.ln2, s.rms_eps).view(B, n)
+    assert _rel(ours_sc, ref_sc) < 1e-5
+    assert float(ours_sc.std()) > 1e-3
+    # split: the MLP half on a subset of rows == the whole layer's output on those rows
+    keep = torch.tensor([0, 3, 4, 17, 49])
+    assert _rel(op.mlp_half(W, 1, a[:, keep]), full[:, keep]) < 1e-6
+    assert _rel(full, _hf_run(s, lw, x, pos, _causal_mask(B, n))) < 1e-5
+
+
 def _prompts(lens, vocab, seed):
     g = torch.Generator().manual_seed(seed)
     return [torch.randint(0, vocab, (n,), generator=g).tolist() for n in lens]
 
 
-def test_padded_batch_equals_per_sample():
+@pytest.mark.parametrize("branch", [False, True])
+def test_padded_batch_equals_per_sample(branch):
     s = Shape(n_layers=4)
     W = op.Weights(_wts(s, seed=4))
-    head = _head(s)
+    head = _bhead(s, 2) if branch else _head(s)
     head.gate_scale = torch.randn(2, s.n_heads) * 0.3
     head.attn_scale = torch.randn(2, s.n_heads) * 0.3 + 0.5
     lens, starts, ends, Ks = [90, 140, 61], [5, 10, 3], [80, 120, 50], [7, 200, 1]

@@ -89,7 +89,16 @@ def test_prefill_matches_oracle(cuda, case, ssmax):
             pos = torch.arange(lens[b])[None]
             ref, _, _ = op.layer(W, i, x, pos)
             assert_close_grad(f"phase1 layer {i} seq {b}", to_np(ins1[i + 1][cu1[b]:cu1[b + 1]]), to_np(ref[0]))
-    gs = torch.nn.functional.softplus(head.gate_scale.float().cpu())
+    _check_phase2_and_e2e(r, W, head, shape, ids, lens, starts, ends, Ks, keeps, scores, f"{case} ssmax={ssmax}")
+
+
+def _check_phase2_and_e2e(r, W, head, shape, ids, lens, starts, ends, Ks, keeps, scores, tag):
+    """Phase-2 layers teacher-forced against the oracle layer, the first-token logits, and the
+    oracle's float32 prefill from the ids on the same keep lists, end to end."""
+    cap = r.capture
+    cu1, cu2 = r.cu_prompt, r.cu_kept
+    ssmax = head.ssmax
+    gs = torch.nn.functional.softplus(head.gate_scale.float().cpu()) * float(getattr(head, "bias_gain", 1.0))
     at = torch.nn.functional.softplus(head.attn_scale.float().cpu())
     h2 = cap["h2"].float().cpu()
     ins2 = [t.float().cpu() for t in cap["phase2"]] + [h2]
@@ -117,8 +126,62 @@ def test_prefill_matches_oracle(cuda, case, ssmax):
         n = r.n_kept[b]
         d = float((h2[cu2[b]:cu2[b + 1]] - e2e["h_last"][b, :n]).norm() / e2e["h_last"][b, :n].norm())
         dl = float((cap["logits"][b].cpu() - e2e["logits"][b]).norm() / e2e["logits"][b].norm())
-        print(f"[e2e] {case} ssmax={ssmax} seq {b}: rel-L2 hidden {d:.2e} logits {dl:.2e}", flush=True)
+        print(f"[e2e] {tag} seq {b}: rel-L2 hidden {d:.2e} logits {dl:.2e}", flush=True)
         assert d <= 3e-2 and dl <= 3e-2
+
+
+@pytest.mark.parametrize("case", ["ragged3", "one"])
+def test_prefill_branch_head_split_matches_oracle(cuda, case):
+    """The finalized gate (MLP scoring branch, scaled softmax) with the split gate layer: Phase 1
+    ends at the gate layer's attention boundary, the branch scores it, the gate layer's MLP runs
+    on the kept rows only.  Checked: the boundary (teacher-forced), the bf16-valued branch scores
+    against the oracle branch on the pipeline's own boundary, the keep lists and packed boundary
+    rows bit-exact, the packed post-MLP rows against the oracle's whole gate layer gathered at the
+    kept rows (the unsplit form), then Phase 2, logits and end to end as above."""
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    lens, starts, ends, Ks = CASES[case]
+    shape, wts, _ = _setup(cuda, seed=2)
+    head = G.random_branch_head(wts, 1, seed=23)
+    g = torch.Generator(device=cuda).manual_seed(24)
+    head.gate_scale = head.gate_scale + 0.5 * torch.randn(head.gate_scale.shape, generator=g, device=cuda)
+    g = torch.Generator().manual_seed(13)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, capture=True)
+    torch.cuda.synchronize()
+    cap = r.capture
+    cu1, cu2 = r.cu_prompt, r.cu_kept
+    sc_t = cap["scores"]
+    assert bool(((sc_t.view(torch.int32) & 0xFFFF) == 0).all()), "branch scores must be bf16 values"
+    scores = sc_t.cpu().numpy().astype(np.float64)
+    W = op.Weights(wts)
+    a1 = cap["h1"].float().cpu()                                   # boundary rows of every prompt
+    ref_sc = op.branch_scores(head, a1, W.layers[1]["ln2"], shape.rms_eps)
+    assert_close_grad("branch scores", scores, to_np(ref_sc))
+    ins1 = [t.float().cpu() for t in cap["phase1"]]
+    hsb = cap["hs_boundary"].float().cpu()
+    hsp = cap["hs_packed"].float().cpu()
+    keep = cap["keep"].cpu().numpy()
+    kb = r.kept_bias.cpu().numpy()
+    keeps = []
+    for b in range(len(lens)):
+        x = ins1[1][cu1[b]:cu1[b + 1]][None]
+        pos = torch.arange(lens[b])[None]
+        bnd = []
+        ref_full, _, _ = op.layer(W, 1, x, pos, boundary=bnd)
+        assert_close_grad(f"gate boundary seq {b}", to_np(a1[cu1[b]:cu1[b + 1]]), to_np(bnd[0][0]))
+        sc = scores[cu1[b] + starts[b]:cu1[b] + ends[b]]
+        want = og.keep_indices(sc, Ks[b], starts[b], ends[b], lens[b])
+        assert np.array_equal(keep[cu2[b]:cu2[b + 1]], want), f"seq {b}: keep list differs"
+        assert torch.equal(hsb[cu2[b]:cu2[b + 1]], a1[cu1[b] + torch.as_tensor(want)])
+        np.testing.assert_allclose(kb[cu2[b]:cu2[b + 1]], og.gate_bias(sc, want, starts[b], ends[b]),
+                                   rtol=2e-6, atol=1e-7)
+        # the split: MLP on the packed kept boundary rows == the whole gate layer, then gathered
+        assert_close_grad(f"gate MLP on kept rows seq {b}", to_np(hsp[cu2[b]:cu2[b + 1]]),
+                          to_np(ref_full[0][torch.as_tensor(want)]))
+        keeps.append(want)
+    _check_phase2_and_e2e(r, W, head, shape, ids, lens, starts, ends, Ks, keeps, scores, f"{case} branch")
 
 
 def test_prefill_prune_below_gate(cuda):

@@ -35,6 +35,7 @@ SIGNATURES = {
     "tg_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, f32, vp],
     "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp],
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
+    "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p}
 

@@ -168,6 +168,38 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const bf16_t *__restrict_
   }
 }
 
+// ---- scoring-branch readout: one wave per row --------------------------------------------------
+// score[r] = bf16(sum_i bf16(bf16(silu(g_ri)) * u_ri) * w_i) stored as fp32: the finalized gate's
+// SwiGLU branch with its down projection absorbed into one (1, inter) row, evaluated with the
+// bf16 roundings of an eager bf16 Qwen3MLP (silu output, gate * up product, the GEMM's output);
+// the dot product accumulates in fp32.  silu uses the accurate expf, as torch's bf16 silu does.
+__global__ __launch_bounds__(256) void branch_readout_kernel(const bf16_t *__restrict__ gu, int64_t gu_rs,
+                                                             int64_t rows, int inter,
+                                                             const bf16_t *__restrict__ w,
+                                                             float *__restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = inter >> 3;
+  const bf16_t *g = gu + row * gu_rs;
+  const bf16_t *u = g + inter;
+  float acc = 0.f;
+#pragma unroll 4
+  for (int ch = lane; ch < nch; ch += 64) {
+    float gf[8], uf[8], wf[8];
+    unpack8(ld16(g + 8 * ch), gf);
+    unpack8(ld16(u + 8 * ch), uf);
+    unpack8(ld16(w + 8 * ch), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float sl = (float)(__bf16)(gf[e] / (1.f + expf(-gf[e])));
+      acc = fmaf((float)(__bf16)(sl * uf[e]), wf[e], acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) out[row] = (float)(__bf16)acc;
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -269,6 +301,24 @@ extern "C" int tg_silu_mul(const void *gate_up, int64_t gate_up_row_stride, int6
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const bf16_t *>(gate_up), gate_up_row_stride, n_rows, inter,
                      static_cast<bf16_t *>(out), out_row_stride);
+  TG_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+extern "C" int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_stride, int64_t n_rows,
+                                      int32_t inter, const void *w_row, float *scores, hipStream_t stream) {
+  clear_error();
+  TG_CHECK(gate_up && w_row && scores, "branch_readout: null pointer");
+  TG_CHECK(n_rows >= 0 && inter > 0 && inter % 8 == 0, "branch_readout: inter must be a positive multiple of 8");
+  TG_CHECK(gate_up_row_stride % 8 == 0 && gate_up_row_stride >= 2 * (int64_t)inter,
+           "branch_readout: gate_up row stride must be a multiple of 8 holding 2*inter elements");
+  TG_CHECK(aligned16(gate_up) && aligned16(w_row), "branch_readout: gate_up and w_row must be 16-byte aligned");
+  if (n_rows == 0) return 0;
+  const int64_t blocks = (n_rows + 3) / 4;
+  TG_CHECK(blocks < (1ll << 31), "branch_readout: too many rows");
+  hipLaunchKernelGGL(branch_readout_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const bf16_t *>(gate_up), gate_up_row_stride, n_rows, inter,
+                     static_cast<const bf16_t *>(w_row), scores);
   TG_HIP_CHECK(hipGetLastError());
   return 0;
 }

@@ -239,12 +239,15 @@ class Workspace:
 
 def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws: Workspace,
                kv: List[Optional[LayerKV]], biases=None, q_scales=None, capture: Optional[list] = None,
-               q_row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+               q_row_scale: Optional[torch.Tensor] = None, attn_only_last: bool = False) -> torch.Tensor:
     """Runs decoder layers `layer_ids` over the packed rows x (T, d) and returns the hidden state
     after the last of them (T, d).  kv[i] receives layer i's cache rows.  biases[i] / q_scales[i]
     (optional): Phase-2 raw-unit key bias (nseq, H, >= max_len) and per-head query scale (H,)
     fp32 of layer i; q_row_scale (T,) fp32: a per-row query scale for every layer (the
-    scaled-softmax ratio).  capture: optional list that receives each layer's input hidden state."""
+    scaled-softmax ratio).  capture: optional list that receives each layer's input hidden state.
+    attn_only_last: the last layer stops at its attention residual a = x + o_proj(attn) (the
+    split gate layer's boundary, attn_only_forward of gate_forward.py:372-413); its MLP half is
+    mlp_sublayer."""
     shape = wts.shape
     T = geo.total
     if x.shape != (T, shape.d_model):
@@ -254,7 +257,8 @@ def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws:
     res, normed, hid = ws.residual[:T], ws.normed[:T], ws.hidden[:T]
     qkv, attn, lse = ws.qkv[:T], ws.attn[:T], ws.lse[:shape.n_heads * T].view(shape.n_heads, T)
     first = True
-    for i in layer_ids:
+    layer_ids = list(layer_ids)
+    for n_done, i in enumerate(layer_ids):
         lw = wts.layers[i]
         if first:
             res.copy_(x)
@@ -270,15 +274,39 @@ def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws:
         varlen_attention(q, kv[i].k, kv[i].v, geo.cu_dev, geo.max_len, scale,
                          biases[i] if biases is not None else None, out=attn, lse=lse)
         torch.matmul(attn.view(T, -1), lw.w_o.t(), out=hid)
+        if attn_only_last and n_done == len(layer_ids) - 1:
+            break
         rmsnorm(hid, lw.ln2, eps, residual=res, residual_out=res, out=normed)
-        for r0 in range(0, T, ws.mlp_rows):
-            r1 = min(T, r0 + ws.mlp_rows)
-            gu = ws.gu[:r1 - r0]
-            torch.matmul(normed[r0:r1], lw.w_gu.t(), out=gu)
-            act = silu_mul(gu, out=ws.act[:r1 - r0])
-            torch.matmul(act, lw.w_down.t(), out=hid[r0:r1])
+        _mlp_rows(lw, normed, hid, ws)
     out = torch.empty_like(hid)
     torch.add(hid, res, out=out)
+    return out
+
+
+def _mlp_rows(lw: LayerWeights, normed: torch.Tensor, out: torch.Tensor, ws: Workspace) -> None:
+    """out = down(silu(gate) * up) of the normed rows, in chunks of ws.mlp_rows."""
+    T = normed.shape[0]
+    for r0 in range(0, T, ws.mlp_rows):
+        r1 = min(T, r0 + ws.mlp_rows)
+        gu = ws.gu[:r1 - r0]
+        torch.matmul(normed[r0:r1], lw.w_gu.t(), out=gu)
+        act = silu_mul(gu, out=ws.act[:r1 - r0])
+        torch.matmul(act, lw.w_down.t(), out=out[r0:r1])
+
+
+def mlp_sublayer(wts: DecoderWeights, i: int, a: torch.Tensor, ws: Workspace) -> torch.Tensor:
+    """Layer i's MLP half on rows a (T, d): a + down(silu(gate) * up)(post_attention_layernorm(a))
+    (_gate_layer_mlp_eager, gate_forward.py:422-437).  Position-wise, so running it on a subset of
+    rows equals running it on all rows and keeping that subset."""
+    T = a.shape[0]
+    if T > ws.rows:
+        raise RuntimeError("mlp_sublayer: workspace has fewer rows than the input")
+    lw = wts.layers[i]
+    normed, hid = ws.normed[:T], ws.hidden[:T]
+    rmsnorm(a, lw.ln2, wts.shape.rms_eps, out=normed)
+    _mlp_rows(lw, normed, hid, ws)
+    out = torch.empty_like(a)
+    torch.add(a, hid, out=out)
     return out
 
 

@@ -13,7 +13,7 @@ one launch per step for the whole batch.
 """
 import ctypes
 from dataclasses import dataclass
-from typing import List, Optional, Sequence, Tuple
+from typing import ClassVar, List, Optional, Sequence, Tuple
 
 import torch
 
@@ -179,8 +179,50 @@ def keep_indices(scores_art: torch.Tensor, K: int, article_start: int, article_e
     return keep
 
 
+def branch_readout(gu: torch.Tensor, w_row: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """scores[r] = bf16(w_row . bf16(bf16(silu(gu[r, :I])) * gu[r, I:])) as float32 for the fused
+    gate/up rows gu (rows, 2I) bf16 of the scoring branch; w_row (I,) bf16."""
+    if gu.dtype != torch.bfloat16 or w_row.dtype != torch.bfloat16 or gu.dim() != 2 or gu.stride(1) != 1:
+        raise RuntimeError("branch_readout: gu (rows, 2I) and w_row (I,) must be bf16 with contiguous rows")
+    n, inter = gu.shape[0], gu.shape[1] // 2
+    if w_row.numel() != inter or not w_row.is_contiguous():
+        raise RuntimeError("branch_readout: w_row must be contiguous with I = gu.shape[1] / 2 entries")
+    out = out if out is not None else torch.empty(n, dtype=torch.float32, device=gu.device)
+    if out.dtype != torch.float32 or out.numel() < n or not out.is_contiguous():
+        raise RuntimeError("branch_readout: out must be contiguous float32 with one entry per row")
+    if n:
+        _lib.call("tg_gate_branch_readout", gu.data_ptr(), gu.stride(0), n, inter, w_row.data_ptr(), out.data_ptr(),
+                  _stream(gu))
+    return out
+
+
+class _BiasScales:
+    """Per-(Phase-2 layer, head) bias magnitude and temperature shared by the scoring heads:
+    gate_scale (L2, H) and attn_scale (L2, H) or None, both pre-softplus, scaled_softmax flag and
+    the normalisation gain bias_gain."""
+    bias_gain: float = 1.0
+
+    @property
+    def ssmax(self) -> bool:
+        return self.scaled_softmax and self.attn_scale is not None
+
+    def layer_coefficients(self, softmax_scale: float) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        """(bias coefficient in raw-score units, per-head query scale) per (layer, head):
+        raw bias of key j = normalised score_j * coef[l, h] (* r_j in scaled-softmax mode), where
+        coef = bias_gain * softplus(gate_scale) * temperature / softmax_scale; the temperature is
+        softplus(attn_scale) per head, or its mean over heads in scaled-softmax mode."""
+        coef = torch.nn.functional.softplus(self.gate_scale.float())
+        if self.bias_gain != 1.0:
+            coef = coef * float(self.bias_gain)
+        qs = None
+        if self.attn_scale is not None:
+            qs = torch.nn.functional.softplus(self.attn_scale.float()).contiguous()
+            coef = coef * (qs.mean(1, keepdim=True) if self.scaled_softmax else qs)
+        return (coef / softmax_scale).contiguous(), qs
+
+
 @dataclass
-class ScoringHead:
+class ScoringHead(_BiasScales):
     """The gate's parameters for one prefill.
 
     Scoring: score_j = w2 . silu(W1 x_j + b1) + b2 on the gate layer's hidden state (the
@@ -202,25 +244,61 @@ class ScoringHead:
     # r = min(1, ln max(slot, 2) / ln max(position + 1, 2)) (_ssmax_ratio, gate_forward.py:574-585;
     # _phase2_q_bias, qwen3_flex_attention.py:433-473).  Needs attn_scale.
     scaled_softmax: bool = False
+    split_gate_layer: ClassVar[bool] = False      # scores the gate layer's full output
 
     def scores(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         return score_mlp(x, self.w1, self.b1, self.w2, self.b2, out=out)
 
-    @property
-    def ssmax(self) -> bool:
-        return self.scaled_softmax and self.attn_scale is not None
 
-    def layer_coefficients(self, softmax_scale: float) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-        """(bias coefficient in raw-score units, per-head query scale) per (layer, head):
-        raw bias of key j = normalised score_j * coef[l, h] (* r_j in scaled-softmax mode), where
-        coef = softplus(gate_scale) * temperature / softmax_scale; the temperature is
-        softplus(attn_scale) per head, or its mean over heads in scaled-softmax mode."""
-        coef = torch.nn.functional.softplus(self.gate_scale.float())
-        qs = None
-        if self.attn_scale is not None:
-            qs = torch.nn.functional.softplus(self.attn_scale.float()).contiguous()
-            coef = coef * (qs.mean(1, keepdim=True) if self.scaled_softmax else qs)
-        return (coef / softmax_scale).contiguous(), qs
+@dataclass
+class BranchHead(_BiasScales):
+    """The finalized gate (E2EGate, e2e_gate_module.py:204-399) with its MLP scoring branch.
+
+    Scoring (gate_branch_hs, gate_forward.py:491-524, absorbed readout without residual): on the
+    gate layer's attention boundary a_j, z = post_attention_layernorm(a_j) of the gate layer and
+    score_j = w_row . (silu(W_gate z) * (W_up z)) in bf16 — a clone of the gate layer's Qwen3MLP
+    whose down projection is the single absorbed row w_row (build_gate_branch :261-342; load_gate
+    e2e_gate_module.py:497-514).  Its presence splits the gate layer (split_gate_layer_mlp
+    :345-357): Phase 1 ends at a_j, and the gate layer's own MLP runs on the kept rows only at
+    Phase-2 entry (gate_layer_mlp :422-437, applied at :1476-1478).  Bias: the bf16 score,
+    RMS-normalised over the state span in float32 with gain bias_gain (b_norm, :296-300), times
+    softplus(gate_scale[l, h]) (forward :348-385); scaled softmax is the finalized default
+    (scaled_softmax_scale :229).  Top-K ranks the bf16 score: the selection key (aggregate,
+    mean over heads of layer 0's bias, :387-399) is a non-decreasing function of it."""
+    w_gu: torch.Tensor          # (2I, d) bf16: the branch's gate_proj rows, then its up_proj rows
+    w_row: torch.Tensor         # (I,) bf16: the absorbed down_proj row
+    gate_scale: torch.Tensor    # (n_phase2_layers, H) fp32, pre-softplus
+    attn_scale: Optional[torch.Tensor] = None
+    scaled_softmax: bool = True
+    bias_gain: float = 1.0
+    split_gate_layer: ClassVar[bool] = True
+
+    @property
+    def inter(self) -> int:
+        return self.w_row.numel()
+
+    def scores_from_boundary(self, a: torch.Tensor, ln2: torch.Tensor, eps: float,
+                             out: Optional[torch.Tensor] = None, normed: Optional[torch.Tensor] = None,
+                             chunk_rows: int = 65536) -> torch.Tensor:
+        """bf16-valued float32 scores of every row of the boundary a (T, d) bf16; ln2: the gate
+        layer's post_attention_layernorm weight.  The branch's gate/up GEMM runs in row chunks of
+        chunk_rows (the reference bounds its MLP workspace the same way, gate_forward.py:418-437)."""
+        from tokengate_amd.decoder import rmsnorm
+        T, d = a.shape
+        if self.w_gu.shape != (2 * self.inter, d):
+            raise RuntimeError("BranchHead: w_gu must be (2 * len(w_row), d_model)")
+        out = out if out is not None else torch.empty(T, dtype=torch.float32, device=a.device)
+        if T == 0:
+            return out
+        normed = normed[:T] if normed is not None else torch.empty_like(a)
+        rmsnorm(a, ln2, eps, out=normed)
+        cr = max(1, min(T, int(chunk_rows)))
+        gu = torch.empty(cr, 2 * self.inter, dtype=torch.bfloat16, device=a.device)
+        for r0 in range(0, T, cr):
+            r1 = min(T, r0 + cr)
+            torch.matmul(normed[r0:r1], self.w_gu.t(), out=gu[:r1 - r0])
+            branch_readout(gu[:r1 - r0], self.w_row, out=out[r0:r1])
+        return out
 
 
 def ssmax_ratio_rows(kept_pos: torch.Tensor, cu_kept: Sequence[int]) -> torch.Tensor:
@@ -255,3 +333,25 @@ def random_head(n_layers: int, n_heads: int, seed: int = 5, device="cuda", d_in:
     gs = base + 0.1 * torch.randn(n_layers, n_heads, generator=g, device=device)
     at = torch.full((n_layers, n_heads), math.log(math.expm1(1.0)), device=device) if temperature else None
     return ScoringHead(w1, b1, w2, 0.0, gs, at, scaled_softmax)
+
+
+def random_branch_head(wts, gate_layer: int, seed: int = 5, gate_scale: Optional[float] = None,
+                       row_std: Optional[float] = None) -> BranchHead:
+    """Seeded finalized-gate head on decoder weights wts: the branch starts as a copy of the gate
+    layer's gate/up projections (build_gate_branch, gate_forward.py:261-342); the absorbed row,
+    zero at initialisation there, is a seeded normal row of std row_std (default I^-1/2) standing
+    in for a trained one; gate_scale as random_head; attn_scale = softplus^-1(1) plus a seeded
+    spread; scaled softmax on."""
+    import math
+    dev = wts.device
+    shape = wts.shape
+    n_layers = shape.n_layers - gate_layer - 1
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w_gu = wts.layers[gate_layer].w_gu.clone()
+    inter = w_gu.shape[0] // 2
+    std = row_std if row_std is not None else inter ** -0.5
+    w_row = (torch.randn(inter, generator=g, device=dev) * std).to(torch.bfloat16)
+    base = math.log(math.expm1(1.0)) if gate_scale is None else gate_scale
+    gs = base + 0.1 * torch.randn(n_layers, shape.n_heads, generator=g, device=dev)
+    at = math.log(math.expm1(1.0)) + 0.1 * torch.randn(n_layers, shape.n_heads, generator=g, device=dev)
+    return BranchHead(w_gu, w_row, gs, at, True)

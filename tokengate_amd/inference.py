@@ -125,7 +125,7 @@ def _sync():
 class TokenGateModel:
     """Decoder weights + scoring head + gate layer behind one object (inference.py:72-150)."""
 
-    def __init__(self, weights: dec.DecoderWeights, head: G.ScoringHead, gate_layer: int, base_model: str):
+    def __init__(self, weights: dec.DecoderWeights, head, gate_layer: int, base_model: str):
         self.weights = weights
         self.gate = head
         self.gate_layer = gate_layer
@@ -252,38 +252,85 @@ def _load_hf_qwen3(path: str, device) -> Tuple[dec.DecoderWeights, str]:
     return w, path
 
 
-def save_head(head: G.ScoringHead, path: str) -> None:
-    """Writes the scoring head as safetensors (w1, b1, w2, b2, gate_scale[, attn_scale])."""
+def save_head(head, path: str) -> None:
+    """Writes a scoring head as safetensors: the synthetic head (w1, b1, w2, b2) or the branch
+    head (w_gu, w_row, bias_gain), with gate_scale[, attn_scale] and the scaled-softmax flag."""
     from safetensors.torch import save_file
-    t = {"w1": head.w1.cpu(), "b1": head.b1.cpu(), "w2": head.w2.cpu(), "b2": torch.tensor([head.b2]),
-         "gate_scale": head.gate_scale.cpu()}
+    if isinstance(head, G.BranchHead):
+        t = {"w_gu": head.w_gu.cpu(), "w_row": head.w_row.cpu(), "bias_gain": torch.tensor([float(head.bias_gain)])}
+    else:
+        t = {"w1": head.w1.cpu(), "b1": head.b1.cpu(), "w2": head.w2.cpu(), "b2": torch.tensor([head.b2])}
+    t["gate_scale"] = head.gate_scale.cpu()
     if head.attn_scale is not None:
         t["attn_scale"] = head.attn_scale.cpu()
     t["scaled_softmax"] = torch.tensor([1 if head.scaled_softmax else 0], dtype=torch.int32)
     save_file({k: v.contiguous() for k, v in t.items()}, path)
 
 
-def load_head(path: str, device) -> G.ScoringHead:
+def load_head(path: str, device):
+    """A head written by save_head."""
     from safetensors.torch import load_file
     t = load_file(path, device="cpu")
+    gs = t["gate_scale"].to(device, torch.float32)
+    at = t["attn_scale"].to(device, torch.float32) if "attn_scale" in t else None
+    if "w_gu" in t:
+        return G.BranchHead(t["w_gu"].to(device, torch.bfloat16), t["w_row"].to(device, torch.bfloat16), gs, at,
+                            bool(int(t["scaled_softmax"].item())) if "scaled_softmax" in t else True,
+                            float(t["bias_gain"].item()) if "bias_gain" in t else 1.0)
     return G.ScoringHead(t["w1"].to(device, torch.bfloat16), t["b1"].to(device, torch.float32),
-                         t["w2"].to(device, torch.float32), float(t["b2"].item()),
-                         t["gate_scale"].to(device, torch.float32),
-                         t["attn_scale"].to(device, torch.float32) if "attn_scale" in t else None,
+                         t["w2"].to(device, torch.float32), float(t["b2"].item()), gs, at,
                          bool(int(t["scaled_softmax"].item())) if "scaled_softmax" in t else False)
+
+
+def _is_gate_checkpoint(checkpoint: str) -> bool:
+    if checkpoint.endswith(".pt"):
+        return True
+    return os.path.isdir(checkpoint) and any(glob.glob(os.path.join(checkpoint, pat))
+                                             for pat in ("swa_gate_*.pt", "gate_final.pt", "gate_step*.pt"))
 
 
 def load_model(checkpoint: str = "random", base_model: Optional[str] = None, gate_layer: Optional[int] = None,
                gate_attn: str = "fa2", dtype=None, *, gate_path: Optional[str] = None, device="cuda",
                shape: Optional[dec.DecoderShape] = None) -> TokenGateModel:
-    """One model object (load_model, inference.py:127-180).  checkpoint: "random[:seed]" or a
-    local Qwen3 checkpoint directory; base_model: overrides the directory; gate_layer: default 1;
-    gate_attn: "fa2" (this package's key-bias kernels; the reference's "flex" / "sdpa" paths do
-    not exist here); dtype: bfloat16 only."""
+    """One model object (load_model, inference.py:137-180).
+
+    checkpoint: a trained gate in the reference's format — a gate *.pt file or a local run
+    directory holding gate_*.pt (swa_gate_* > gate_final > gate_step*) — whose metadata names
+    base_model and gate_layer (arguments override them); base_model must then be a local Qwen3
+    checkpoint directory, and the adapter saved beside the gate is folded into its weights.
+    Otherwise checkpoint is "random[:seed]" (a seeded Qwen3-1.7B-shaped decoder, or `shape`) or a
+    local Qwen3 directory, with the synthetic scoring head or the head saved by save_head at
+    gate_path; gate_layer defaults to 1 there.  gate_attn: "fa2" (this package's key-bias
+    kernels; the reference's "flex" / "sdpa" paths do not exist here); dtype: bfloat16 only.
+    Nothing is downloaded."""
     if dtype is not None and dtype != torch.bfloat16:
         raise ValueError("this build runs the decoder in torch.bfloat16 only")
     if gate_attn != "fa2":
         raise ValueError(f"gate_attn={gate_attn!r}: only 'fa2' (the key-bias HIP kernels) is available")
+    if not checkpoint.startswith("random") and _is_gate_checkpoint(checkpoint):
+        from tokengate_amd import checkpoint as C
+        gpath = C.resolve_gate_path(checkpoint)
+        head, meta = C.load_gate(gpath, device)
+        base_model = base_model or meta.get("base_model")
+        if not base_model:
+            raise ValueError(f"{gpath} records no base_model in its metadata; pass base_model= explicitly")
+        if gate_layer is None:
+            gate_layer = meta.get("gate_layer")
+            if gate_layer is None:
+                raise ValueError(f"{gpath} records no gate_layer in its metadata; pass gate_layer= explicitly")
+        gate_layer = int(gate_layer)
+        if not os.path.isdir(base_model):
+            raise FileNotFoundError(f"base_model {base_model!r} is not a local checkpoint directory "
+                                    "(nothing is downloaded)")
+        w, name = _load_hf_qwen3(base_model, device)
+        C.load_adapter_for(w, gpath, meta)
+        n2 = w.shape.n_layers - gate_layer - 1
+        if tuple(head.gate_scale.shape) != (n2, w.shape.n_heads):
+            raise ValueError(f"{gpath}: gate_scale {tuple(head.gate_scale.shape)} does not match (layers above "
+                             f"gate layer {gate_layer}, heads) = ({n2}, {w.shape.n_heads})")
+        if head.w_gu.shape[1] != w.shape.d_model:
+            raise ValueError(f"{gpath}: scoring branch width {head.w_gu.shape[1]} != d_model {w.shape.d_model}")
+        return TokenGateModel(w, head, gate_layer, name)
     gate_layer = 1 if gate_layer is None else int(gate_layer)
     src = base_model or checkpoint
     if src.startswith("random"):

@@ -9,7 +9,10 @@ run on the kept rows with RoPE at the original positions and the per-(layer, hea
 (:1478-1560, _apply_gate_bias :588-662); the first token is the argmax of the LM head at each
 sequence's last row (:1560-1580).  Layers at or below the gate keep their full Phase-1 KV cache
 (prune_below_gate=False, the reference default); prune_below_gate=True packs it down to the kept
-rows in the same launch that packs the hidden states.
+rows in the same launch that packs the hidden states.  With the finalized gate's MLP scoring
+branch (gate.BranchHead) the gate layer is split (split_gate_layer_mlp, gate_forward.py:345-357,
+:1362-1372): Phase 1 ends at the gate layer's attention residual, the branch scores that boundary,
+and the gate layer's own MLP runs on the packed kept rows only, at Phase-2 entry (:1476-1478).
 
 MI355X layout: the batch is never padded.  Phase 1 packs all prompts back to back (cu_seqlens)
 and runs one varlen attention launch per layer; the keep lists of all sequences come from one
@@ -27,7 +30,7 @@ import torch
 
 from tokengate_amd import gate as G
 from tokengate_amd.decoder import (DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, h2d, logits_last,
-                                   run_layers)
+                                   mlp_sublayer, run_layers)
 
 
 @dataclass
@@ -129,12 +132,13 @@ class Phase2Graphs:
 
 
 @torch.no_grad()
-def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, art_starts: Sequence[int],
+def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Sequence[int],
                   art_ends: Sequence[int], gate_layer: int, K, prune_below_gate: bool = False,
                   phase_timing: bool = False, capture: bool = False, mlp_rows: int = 131072,
                   phase2_graphs: Optional[Phase2Graphs] = None) -> PrefillResult:
     """ids_list: B prompts (lists of ints or 1-D tensors); the state span of prompt b is
-    [art_starts[b], art_ends[b]); K: scalar or per-prompt list.  phase2_graphs: replay Phase 2
+    [art_starts[b], art_ends[b]); K: scalar or per-prompt list; head: gate.ScoringHead or
+    gate.BranchHead (split gate layer).  phase2_graphs: replay Phase 2
     from captured graphs (captured on first use per geometry); the Phase-2 KV caches are then views
     of the graph's buffers, valid until its next replay."""
     shape = wts.shape
@@ -168,11 +172,17 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
     kv: List[Optional[LayerKV]] = [None] * n_layers
     for i in range(gate_layer + 1):
         kv[i] = alloc_kv(shape, T, dev)
-    h = run_layers(wts, range(gate_layer + 1), x, geo1, ws1, kv, capture=cap["phase1"] if cap else None)
+    split = bool(getattr(head, "split_gate_layer", False))
+    h = run_layers(wts, range(gate_layer + 1), x, geo1, ws1, kv, capture=cap["phase1"] if cap else None,
+                   attn_only_last=split)
     del x
 
     mark("score+select")
-    scores = head.scores(h)
+    if split:
+        scores = head.scores_from_boundary(h, wts.layers[gate_layer].ln2, shape.rms_eps, normed=ws1.normed,
+                                           chunk_rows=mlp_rows)
+    else:
+        scores = head.scores(h)
     p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
     keep, sumsq = G.select_keep(scores, p)
 
@@ -193,6 +203,12 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
     del h, ws1, pairs
 
     mark("phase2")
+    ws2 = None
+    if split:                       # the gate layer's MLP on the kept rows (Phase-2 entry)
+        ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
+        if cap is not None:
+            cap["hs_boundary"] = hs
+        hs = mlp_sublayer(wts, gate_layer, hs, ws2)
     max_kept = max(p.n_kept)
     # per-sequence padded view of the packed bias: row b, column t <- packed row cu_kept[b] + t
     t_ = torch.arange(max_kept, dtype=torch.int64)
@@ -220,7 +236,7 @@ def prefill_batch(wts: DecoderWeights, head: G.ScoringHead, ids_list: Sequence, 
         qs = {l: qscale[j] for j, l in enumerate(above)} if qscale is not None else None
         for l in above:
             kv[l] = alloc_kv(shape, T2, dev)
-        ws2 = Workspace(shape, T2, dev, mlp_rows=mlp_rows)
+        ws2 = ws2 if ws2 is not None else Workspace(shape, T2, dev, mlp_rows=mlp_rows)
         h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
                         capture=cap["phase2"] if cap else None, q_row_scale=ratio)
 
