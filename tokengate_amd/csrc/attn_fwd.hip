@@ -5,9 +5,9 @@
 //   lse[i]  = ln sum_j exp(z[i,j]);   out_i = sum_j exp(z[i,j] - lse[i]) v_j
 // with the query head h reading kv head h / (H / Hkv).
 //
-// Work decomposition (one workgroup = 8 waves = 512 threads, two waves per SIMD):
+// Work decomposition (one workgroup = 4 waves = 256 threads, one per SIMD; two workgroups per CU):
 //   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
-//     size is even) over 8 * 32/HP consecutive query positions; every K/V tile it streams
+//     size is even) over 4 * 32/HP consecutive query positions; every K/V tile it streams
 //     through LDS serves all HP heads;
 //   * each wave owns 32 MFMA columns = HP heads x 32/HP query positions; the KV sequence is
 //     streamed in 64-key tiles by LDS DMA (buffer_load ... lds: no staging registers, zero fill
@@ -21,7 +21,8 @@
 //     from row-major V through the transposing LDS read ds_read_b64_tr_b16;
 //   * O^T accumulates per lane for one column, so the per-query rescale is a scalar per lane, and
 //     it is applied lazily (only when the running max grows by more than 2^8);
-//   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work.
+//   * two waves per SIMD (one from each resident workgroup) let one wave's softmax (VALU) run
+//     under the other's matrix-core work.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
@@ -80,6 +81,14 @@ constexpr float kRescaleTau = 8.0f;
 //      -> the transposing reads (4 keys x 64 B per 16-lane group) spread over all banks.
 // Both are filled by LDS DMA straight from global memory (no staging registers); keys past Sk
 // read as zero through the buffer descriptor's range check.
+// v_max3_f32 without the canonicalising v_max the compiler adds in IEEE mode (the inputs are
+// MFMA results or -inf, never signalling NaNs).
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float d;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+  return d;
+}
+
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
   constexpr int QW = qpw<HP>();
@@ -269,13 +278,16 @@ __global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
         }
       }
     }
-    // tile max as a tree (short dependency chain)
-    float m8[8];
+    // tile max as a tree of v_max3 (short dependency chain, no canonicalising maxes)
+    float m11[11];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-      m8[i] = fmaxf(fmaxf(tv[i >> 2][4 * (i & 3)], tv[i >> 2][4 * (i & 3) + 1]),
-                    fmaxf(tv[i >> 2][4 * (i & 3) + 2], tv[i >> 2][4 * (i & 3) + 3]));
-    float mx = fmaxf(fmaxf(fmaxf(m8[0], m8[1]), fmaxf(m8[2], m8[3])), fmaxf(fmaxf(m8[4], m8[5]), fmaxf(m8[6], m8[7])));
+    for (int i = 0; i < 10; ++i) {
+      const int e0 = 3 * i, e1 = 3 * i + 1, e2 = 3 * i + 2;
+      m11[i] = vmax3(tv[e0 >> 4][e0 & 15], tv[e1 >> 4][e1 & 15], tv[e2 >> 4][e2 & 15]);
+    }
+    m11[10] = vmax3(tv[1][14], tv[1][15], tv[1][15]);
+    float mx = vmax3(vmax3(m11[0], m11[1], m11[2]), vmax3(m11[3], m11[4], m11[5]),
+                     vmax3(vmax3(m11[6], m11[7], m11[8]), m11[9], m11[10]));
     mx = half_swap_max(mx) * a.scale_log2;   // tile max in log2 units (-inf if fully masked)
     if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleTau) != 0) {
       const float m_new = fmaxf(mrun, mx);
