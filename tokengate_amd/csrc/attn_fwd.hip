@@ -5,9 +5,9 @@
 //   lse[i]  = ln sum_j exp(z[i,j]);   out_i = sum_j exp(z[i,j] - lse[i]) v_j
 // with the query head h reading kv head h / (H / Hkv).
 //
-// Work decomposition (one workgroup = 4 waves = 256 threads, one per SIMD; two workgroups per CU):
+// Work decomposition (one workgroup = 8 waves = 512 threads per CU, two waves per SIMD):
 //   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
-//     size is even) over 4 * 32/HP consecutive query positions; every K/V tile it streams
+//     size is even) over 8 * 32/HP consecutive query positions; every K/V tile it streams
 //     through LDS serves all HP heads;
 //   * each wave owns 32 MFMA columns = HP heads x 32/HP query positions; the KV sequence is
 //     streamed in 64-key tiles by LDS DMA (buffer_load ... lds: no staging registers, zero fill
@@ -21,8 +21,8 @@
 //     from row-major V through the transposing LDS read ds_read_b64_tr_b16;
 //   * O^T accumulates per lane for one column, so the per-query rescale is a scalar per lane, and
 //     it is applied lazily (only when the running max grows by more than 2^8);
-//   * two waves per SIMD (one from each resident workgroup) let one wave's softmax (VALU) run
-//     under the other's matrix-core work.
+//   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work;
+//     eight waves share every K/V tile, so each issues a quarter of the tile's LDS DMA.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
@@ -36,7 +36,7 @@ namespace {
 
 constexpr int kD = 128;        // head dim
 constexpr int kBN = 64;        // keys per tile
-constexpr int kWaves = 4;      // one per SIMD; two workgroups share a CU
+constexpr int kWaves = 8;      // two per SIMD (waves w and w + 4 share one), one workgroup per CU
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -90,7 +90,7 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
 }
 
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
-__global__ __launch_bounds__(kThreads, 2) void keybias_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
   constexpr int QW = qpw<HP>();
   constexpr int BM = bm<HP>();
   // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads only
