@@ -207,6 +207,12 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
   const uint32_t v_rowpart = (uint32_t)((r16 >> 2) * kKRowBytes + (r16 & 1) * 8);
   const int v_cpart = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
   const int v_swz = r16 >> 2;
+  // lane part of each d-block's read address (< 1 KB: the mask only tells the compiler so, which
+  // lets it see that these reads stay inside their ring slot and need not wait for DMA elsewhere)
+  uint32_t vch[4];
+#pragma unroll
+  for (int dblk = 0; dblk < 4; ++dblk)
+    vch[dblk] = (v_rowpart + (uint32_t)((4 * (dblk ^ v_swz) + v_cpart) << 4)) & 0x3F8u;
 
   f32x16 oacc[4];
   float mrun = -INFINITY, lrun = 0.f;
@@ -322,12 +328,11 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
       for (int s = 0; s < 2; ++s) {
         const u32x4 w = {pk[kb][4 * s], pk[kb][4 * s + 1], pk[kb][4 * s + 2], pk[kb][4 * s + 3]};
         const bf16x8 pb = __builtin_bit_cast(bf16x8, w);
-        const uint32_t krow = (uint32_t)((32 * kb + 16 * g + 8 * s) * kKRowBytes) + v_rowpart;
+        const uint32_t krow = (uint32_t)((32 * kb + 16 * g + 8 * s) * kKRowBytes);
 #pragma unroll
         for (int dblk = 0; dblk < 4; ++dblk) {
-          const uint32_t ch = (uint32_t)((4 * (dblk ^ v_swz) + v_cpart) << 4);
-          const s16x4 lo = lds_read_tr16(vslot(buf_c) + krow + ch);
-          const s16x4 hi = lds_read_tr16(vslot(buf_c) + krow + 4 * kKRowBytes + ch);
+          const s16x4 lo = lds_read_tr16(vslot(buf_c) + krow + vch[dblk]);
+          const s16x4 hi = lds_read_tr16(vslot(buf_c) + krow + 4 * kKRowBytes + vch[dblk]);
           const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
           oacc[dblk] = mfma32(vf, pb, oacc[dblk]);
         }
