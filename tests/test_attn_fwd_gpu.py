@@ -88,6 +88,25 @@ def test_unequal_lengths(cuda, Sq, Sk, causal):
     _check(q, k, v, bias_raw, scale, causal, tag=f"Sq={Sq} Sk={Sk}")
 
 
+@pytest.mark.parametrize("H,Hkv", [(16, 8), (6, 2), (4, 4)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_wide_grids(cuda, H, Hkv, causal):
+    """Batches large enough for the 8-wave workgroups (one per CU, 128 or 256 query rows): the
+    launch picks them when the grid holds at least two per compute unit; ragged S, per-head bias."""
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    hp = 2 if (H // Hkv) % 2 == 0 else 1
+    S = 1040
+    t8 = -(-S // (8 * 32 // hp))
+    B = -(-2 * cus // (t8 * (H // hp)))
+    assert t8 * B * (H // hp) >= 2 * cus
+    g = torch.Generator(device=cuda).manual_seed(H * 100 + Hkv + int(causal))
+    q, k, v = qkv(B, S, S, H, Hkv, g, cuda)
+    scale = 128 ** -0.5
+    bias_raw = (torch.randn(B, H, S, device=cuda, generator=g) * 2.0 / scale).contiguous()
+    rows = np.unique(np.concatenate([np.arange(0, 70), np.linspace(0, S - 1, 60).astype(int), np.arange(S - 70, S)]))
+    _check(q, k, v, bias_raw, scale, causal, rows=rows, tag=f"B={B} H={H}/{Hkv}")
+
+
 def test_config_4k(cuda):
     """Benchmark shape 1: B1, S4096, 16/8 heads, causal, bias log(sigmoid(z)), z~N(0,2)."""
     g = torch.Generator(device=cuda).manual_seed(0)
@@ -117,9 +136,12 @@ def test_config_32k_sampled_rows(cuda):
     assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
 
 
-def test_varlen_matches_oracle(cuda):
+@pytest.mark.parametrize("lens", [[1, 100, 0, 257, 1000, 64],
+                                  # 24 ragged sequences: a grid wide enough for the 8-wave workgroups
+                                  [int(x) for x in np.random.default_rng(5).integers(0, 1100, 24)]],
+                         ids=["six", "wide24"])
+def test_varlen_matches_oracle(cuda, lens):
     g = torch.Generator(device=cuda).manual_seed(3)
-    lens = [1, 100, 0, 257, 1000, 64]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     total, H, Hkv, D = int(cu[-1]), 16, 8, 128
     q = torch.randn(total, H, D, device=cuda, generator=g).to(torch.bfloat16)

@@ -5,9 +5,10 @@
 //   lse[i]  = ln sum_j exp(z[i,j]);   out_i = sum_j exp(z[i,j] - lse[i]) v_j
 // with the query head h reading kv head h / (H / Hkv).
 //
-// Work decomposition (one workgroup = 8 waves = 512 threads per CU, two waves per SIMD):
+// Work decomposition (one workgroup = 8 waves = 512 threads per CU, two waves per SIMD; 4-wave
+// workgroups, two per CU, when the grid is too small for 8-wave ones):
 //   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
-//     size is even) over 8 * 32/HP consecutive query positions; every K/V tile it streams
+//     size is even) over NW * 32/HP consecutive query positions; every K/V tile it streams
 //     through LDS serves all HP heads;
 //   * each wave owns 32 MFMA columns = HP heads x 32/HP query positions; the KV sequence is
 //     streamed in 64-key tiles by LDS DMA (buffer_load ... lds: no staging registers, zero fill
@@ -22,7 +23,7 @@
 //   * O^T accumulates per lane for one column, so the per-query rescale is a scalar per lane, and
 //     it is applied lazily (only when the running max grows by more than 2^8);
 //   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work;
-//     eight waves share every K/V tile, so each issues a quarter of the tile's LDS DMA.
+//     all NW waves share every K/V tile and each issues 1/NW of its LDS DMA.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
@@ -36,14 +37,13 @@ namespace {
 
 constexpr int kD = 128;        // head dim
 constexpr int kBN = 64;        // keys per tile
-constexpr int kWaves = 8;      // two per SIMD (waves w and w + 4 share one), one workgroup per CU
-constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-// A wave's 32 MFMA columns are HP heads x (32/HP) query positions; a workgroup covers
-// kWaves * 32/HP positions.
+// A wave's 32 MFMA columns are HP heads x (32/HP) query positions; a workgroup of NW waves covers
+// NW * 32/HP positions.  NW = 8 (two waves per SIMD, one workgroup per CU) unless the grid would
+// then be too small to fill the chip, where NW = 4 (two workgroups per CU) halves the query tile.
 template <int HP> constexpr int qpw() { return 32 / HP; }
-template <int HP> constexpr int bm() { return kWaves * qpw<HP>(); }
+template <int NW, int HP> constexpr int bm() { return NW * qpw<HP>(); }
 
 constexpr int kKRowBytes = kD * 2;      // one K or V row in LDS (256 B, 16 chunks of 16 B)
 constexpr int kKTileBytes = kBN * kKRowBytes;
@@ -89,10 +89,11 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return d;
 }
 
-template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
-__global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
+template <int NW, int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
+__global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a) {
+  constexpr int kWaves = NW;
   constexpr int QW = qpw<HP>();
-  constexpr int BM = bm<HP>();
+  constexpr int BM = bm<NW, HP>();
   // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads only
   // across distinct objects, so the DMA of tile t+1 does not hold up the reads of tile t.
   static_assert(kStages == 2, "two named LDS objects per operand");
@@ -373,17 +374,20 @@ __global__ __launch_bounds__(kThreads, 1) void keybias_fwd_kernel(FwdArgs a) {
   }
 }
 
-template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
+template <int NW, int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 void launch_fwd(const FwdArgs &a, int nblocks, hipStream_t stream) {
-  hipLaunchKernelGGL((keybias_fwd_kernel<HP, CAUSAL, HAS_BIAS, VARLEN>), dim3(nblocks), dim3(kThreads), 0,
+  hipLaunchKernelGGL((keybias_fwd_kernel<NW, HP, CAUSAL, HAS_BIAS, VARLEN>), dim3(nblocks), dim3(64 * NW), 0,
                      stream, a);
 }
 
 template <bool VARLEN>
-void dispatch_fwd(const FwdArgs &a, int hp, bool causal, bool has_bias, int nblocks, hipStream_t s) {
+void dispatch_fwd(const FwdArgs &a, int nw, int hp, bool causal, bool has_bias, int nblocks, hipStream_t s) {
 #define TG_FWD_CASE(HPV, C, B)                                              \
   if (hp == HPV && causal == C && has_bias == B) {                          \
-    launch_fwd<HPV, C, B, VARLEN>(a, nblocks, s);                           \
+    if (nw == 8)                                                            \
+      launch_fwd<8, HPV, C, B, VARLEN>(a, nblocks, s);                      \
+    else                                                                    \
+      launch_fwd<4, HPV, C, B, VARLEN>(a, nblocks, s);                      \
     return;                                                                 \
   }
   TG_FWD_CASE(2, true, true)
@@ -398,6 +402,29 @@ void dispatch_fwd(const FwdArgs &a, int hp, bool causal, bool has_bias, int nblo
 }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Compute units of the current device (cached per device id).
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Waves per workgroup and query tiles for a launch over `rows` query positions x `units` (sequence,
+// head group) pairs: 8-wave workgroups when that still gives at least two per CU, else 4-wave ones.
+void pick_tiling(int hp, int rows, int64_t units, int &nw, int &n_qtiles) {
+  const int bm8 = hp == 2 ? bm<8, 2>() : bm<8, 1>();
+  const int bm4 = hp == 2 ? bm<4, 2>() : bm<4, 1>();
+  const int64_t t8 = (rows + bm8 - 1) / bm8;
+  nw = t8 * units >= 2 * (int64_t)device_cus() ? 8 : 4;
+  n_qtiles = nw == 8 ? (int)t8 : (rows + bm4 - 1) / bm4;
+}
 
 int check_common(const void *q, const void *k, const void *v, const void *out, const float *lse,
                  int32_t num_heads, int32_t num_heads_k, int32_t head_dim) {
@@ -462,11 +489,11 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
   a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
-  const int block_m = hp == 2 ? bm<2>() : bm<1>();
-  a.n_qtiles = (seqlen_q + block_m - 1) / block_m;
+  int nw = 8;
+  pick_tiling(hp, seqlen_q, (int64_t)batch * (num_heads / hp), nw, a.n_qtiles);
   const int64_t nblocks = (int64_t)a.n_qtiles * batch * (num_heads / hp);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
-  dispatch_fwd<false>(a, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
+  dispatch_fwd<false>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }
@@ -510,11 +537,11 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
   a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
-  const int block_m = hp == 2 ? bm<2>() : bm<1>();
-  a.n_qtiles = (max_seqlen + block_m - 1) / block_m;
+  int nw = 8;
+  pick_tiling(hp, max_seqlen, (int64_t)num_seqs * (num_heads / hp), nw, a.n_qtiles);
   const int64_t nblocks = (int64_t)a.n_qtiles * num_seqs * (num_heads / hp);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
-  dispatch_fwd<true>(a, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
+  dispatch_fwd<true>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }
