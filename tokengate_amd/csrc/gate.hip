@@ -205,8 +205,58 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return k;
 }
 
+// The float an order key stands for (inverse of order_key; zero comes back as +0).
+__device__ __forceinline__ float key_value(uint32_t k) {
+  return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Bin of value v among 256 equal-width bins over [vmin, vmin + 256 / inv]: non-decreasing in v, so
+// every bin holds a contiguous range of the key order.
+__device__ __forceinline__ int value_bin(float v, float vmin, float inv) {
+  return min(255, (int)((v - vmin) * inv));
+}
+
 __device__ __forceinline__ int lanes_below(uint64_t m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Wave 0: over the 16 per-wave 256-bin histograms, find the bin d holding the sel[2]-th largest
+// element (bins counted from the top); sel[3] = d, sel[2] = its rank within the bin; for key-space
+// bins (width 2^shift from lo) also sel[0..1] = the bin's key range (clipped to the current hi).
+__device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *sel, uint32_t lo, int shift) {
+  // lane l owns bins 255-4l .. 252-4l (descending)
+  int c[4], lt = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kTWaves; ++w) t += h[w][255 - 4 * lane - j];
+    c[j] = t;
+    lt += t;
+  }
+  int incl = lt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  const int before = incl - lt;
+  const int krem = (int)sel[2];
+  if (before < krem && krem <= incl) {
+    int acc = before, d = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; break; }
+      acc += c[j];
+    }
+    const uint32_t hi = sel[1];
+    const uint32_t nlo = lo + ((uint32_t)d << shift);
+    const uint32_t nhi_raw = nlo + ((1u << shift) - 1u);
+    sel[0] = nlo;
+    sel[1] = (nhi_raw < nlo || nhi_raw > hi) ? hi : nhi_raw;
+    sel[2] = (uint32_t)(krem - acc);
+    sel[3] = (uint32_t)d;
+  }
 }
 
 // Register-resident variant for articles of at most 1024 * KPT tokens: thread t holds keys
@@ -216,10 +266,11 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 template <int KPT>
 __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float *scores, const int32_t *geom,
                                                                      int64_t *keep, float *sumsq) {
+  static_assert(KPT % 4 == 0, "bins are cached four per register");
   constexpr int NB = KPT * kTWaves;    // 64-key blocks
   __shared__ int hist[2][kTWaves][256];   // double-buffered: the next pass's copy is cleared early
   __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
-  __shared__ uint32_t sel[4];             // lo, hi, k_rem
+  __shared__ uint32_t sel[4];             // lo, hi, k_rem, chosen bin
   __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
   __shared__ float red[kTWaves];
 
@@ -274,11 +325,60 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
   }
   __syncthreads();
 
-  // Radix select of the kc-th largest key over the occupied key range [lo, hi]: each pass splits
-  // the current range into at most 256 power-of-two-wide bins.  Windowing the first pass to the
-  // data's own range spreads typical scores over many bins (a fixed top-byte digit would put
-  // most of them into a handful).
+  // First pass in value space: 256 equal-width bins over [min, max] of the scores spread typical
+  // score distributions evenly (their order keys crowd into a few power-of-two bins, where the
+  // histogram atomics of a wave would serialise).  The bin holding the kc-th largest score then
+  // narrows the key range to that bin's own [min, max] key for the key-space passes below.
+  // Skipped when the range is empty or not finite (infinities, NaN): the key passes alone are exact.
   int pb = 0;
+  {
+    const uint32_t lo = sel[0], hi = sel[1];
+    const float vmin = key_value(lo), vmax = key_value(hi);
+    const float inv = 256.f / (vmax - vmin);
+    if (lo != hi && __builtin_isfinite(vmin) && __builtin_isfinite(vmax) && __builtin_isfinite(inv) && inv > 0.f) {
+      for (int i = lane; i < 256; i += 64) hist[1][wave][i] = 0;
+      uint32_t bins[KPT / 4];   // the bins, four per register, for the range pass below
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) {
+        const uint32_t u = key[r];
+        // branch-free: a key past the article (0) decodes to NaN, converts to bin 0 and adds 0
+        const int bin = value_bin(key_value(u), vmin, inv);
+        atomicAdd(&hist[0][wave][bin], u != 0u ? 1 : 0);
+        if (r % 4 == 0) bins[r / 4] = 0u;
+        bins[r / 4] |= (uint32_t)bin << (8 * (r % 4));
+      }
+      __syncthreads();
+      if (wave == 0) select_bin(hist[0], lane, sel, 0u, 0);
+      __syncthreads();
+      // key range of the chosen bin
+      const uint32_t d = sel[3];
+      uint32_t bmin = 0xffffffffu, bmax = 0u;
+#pragma unroll
+      for (int r = 0; r < KPT; ++r) {
+        const uint32_t u = key[r];
+        const bool in = u != 0u && ((bins[r / 4] >> (8 * (r % 4))) & 0xffu) == d;
+        bmin = in ? min(bmin, u) : bmin;
+        bmax = in ? max(bmax, u) : bmax;
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        bmin = min(bmin, (uint32_t)__shfl_xor((int)bmin, o));
+        bmax = max(bmax, (uint32_t)__shfl_xor((int)bmax, o));
+      }
+      if (lane == 0) { wmin[wave] = bmin; wmax[wave] = bmax; }
+      __syncthreads();
+      if (tid == 0) {
+        uint32_t a = 0xffffffffu, z = 0u;
+        for (int w = 0; w < kTWaves; ++w) { a = min(a, wmin[w]); z = max(z, wmax[w]); }
+        sel[0] = a; sel[1] = z;
+      }
+      __syncthreads();
+      pb = 1;
+    }
+  }
+  // Radix select of the kc-th largest key over the occupied key range [lo, hi]: each pass splits
+  // the current range into at most 256 power-of-two-wide bins.  Windowing each pass to the
+  // range still in play keeps the passes few.
   while (true) {
     const uint32_t lo = sel[0], hi = sel[1];
     if (lo == hi) break;                             // block-uniform
@@ -291,39 +391,7 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
       if (u != 0u && u >= lo && u <= hi) atomicAdd(&hist[pb][wave][(u - lo) >> shift], 1);
     }
     __syncthreads();
-    if (wave == 0) {
-      // lane l owns bins 255-4l .. 252-4l (descending); totals over the 16 wave histograms
-      int c[4], lt = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        int t = 0;
-#pragma unroll
-        for (int w = 0; w < kTWaves; ++w) t += hist[pb][w][255 - 4 * lane - j];
-        c[j] = t;
-        lt += t;
-      }
-      int incl = lt;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o);
-        if (lane >= o) incl += y;
-      }
-      const int before = incl - lt;
-      const int krem = (int)sel[2];
-      if (before < krem && krem <= incl) {
-        int acc = before, d = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; break; }
-          acc += c[j];
-        }
-        const uint32_t nlo = lo + ((uint32_t)d << shift);
-        const uint32_t nhi_raw = nlo + ((1u << shift) - 1u);
-        sel[0] = nlo;
-        sel[1] = (nhi_raw < nlo || nhi_raw > hi) ? hi : nhi_raw;
-        sel[2] = (uint32_t)(krem - acc);
-      }
-    }
+    if (wave == 0) select_bin(hist[pb], lane, sel, lo, shift);
     __syncthreads();
     pb ^= 1;
   }
