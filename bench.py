@@ -326,8 +326,8 @@ def main():
                     help="also run three plain 1 GiB device copies (counter calibration for HBM bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: every GPU box here has one, and this path is timed on one "
-              "GPU's share (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: the path is timed on one GPU's share of the work, with no "
+              "collectives (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -149,7 +149,7 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
                  hipStream_t stream);
 
 /* ---- decoder ops of the gated prefill (Qwen3 layer, transformers 5.x modeling_qwen3.py) ------
- * Called by this build's prefill around the attention; the reference runs them as eager torch
+ * Called by this library's prefill around the attention; the reference runs them as eager torch
  * modules inside each decoder layer (qwen3_flex_attention.py:533-544 for q/k norm + RoPE). */
 
 /* Residual add + RMSNorm over rows of `dim` bf16 elements (Qwen3RMSNorm, Qwen3DecoderLayer's

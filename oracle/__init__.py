@@ -1,7 +1,8 @@
 """CPU oracle of the TokenGate prefill hot path — TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import anything from
-here, and only as the checker (or the timed CPU baseline), never as the product path.  The
+here, and only as the reference that results are compared against (or the timed CPU baseline),
+never as the product path.  The
 product (tokengate_amd) never imports this package and fails loudly when its HIP library is
 missing.
 
@@ -21,7 +22,7 @@ Pinning (what checks each function, see tests/test_oracle_*.py):
   pack               — per-row brute-force gather; padded-vs-varlen equivalence.
   scoring head       — torch.nn.functional linear/silu on the same weights.
   ssmax ratio        — closed form at hand-computed points.
-Tie order of torch.topk is implementation-defined; the lower-index rule is this build's stated
+Tie order of torch.topk is implementation-defined; the lower-index rule is this library's stated
 rule and is pinned by brute force, not by the reference (parity of ties with the reference's
 torch.topk is unpinned).
 """

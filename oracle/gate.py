@@ -3,7 +3,7 @@
 Restates tokengate/e2e_gate/gate_module/gate_forward.py:
   * K_clamped = max(1, min(K, n_art))                          (:1409-1410)
   * topk over the article scores                               (_select_topk_or_random :84-99;
-    torch.topk's tie order is implementation-defined — this build's rule, applied here, is that
+    torch.topk's tie order is implementation-defined — this library's rule, applied here, is that
     among equal scores the lower position wins; -0.0 equals +0.0; NaN ranks above +inf)
   * keep = cat(arange(s), s + sort(topk), arange(e, seq_len)) (:1417-1421 == _keep_indices :77-81)
   * gathers of hidden / K / V rows at the kept positions       (:1454-1522)

@@ -539,7 +539,7 @@ bool span_ok(int64_t rows, int64_t row_stride) { return (rows + 1) * row_stride 
 int check_bwd(const void *dout, const void *q, const void *k, const void *v, const void *out, const float *lse,
               const void *dq, const void *dk, const void *dv, const float *softmax_d, int32_t num_heads,
               int32_t num_heads_k, int32_t head_dim, float softmax_scale) {
-  TG_CHECK(head_dim == kD, "this build supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
+  TG_CHECK(head_dim == kD, "this library supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
   TG_CHECK(dout && q && k && v && out && lse && dq && dk && dv && softmax_d, "null tensor pointer");
   TG_CHECK(aligned16(dout) && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(dq) &&
                aligned16(dk) && aligned16(dv),

@@ -428,7 +428,7 @@ void pick_tiling(int hp, int rows, int64_t units, int &nw, int &n_qtiles) {
 
 int check_common(const void *q, const void *k, const void *v, const void *out, const float *lse,
                  int32_t num_heads, int32_t num_heads_k, int32_t head_dim) {
-  TG_CHECK(head_dim == kD, "this build supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
+  TG_CHECK(head_dim == kD, "this library supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
   TG_CHECK(q && k && v && out && lse, "null tensor pointer");
   TG_CHECK(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out),
            "q, k, v and out must be 16-byte aligned");

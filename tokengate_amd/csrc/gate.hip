@@ -8,7 +8,7 @@
 //     positions (index_select, :1497-1520), kept positions recorded for RoPE (:1457), the gate
 //     bias of kept article rows (build_gate_bias_vectorized :968-1036; RMS-normalised over the
 //     article as in E2EGate.forward, e2e_gate_module.py:348-385), zero on prefix/suffix rows.
-// This build packs the kept rows of all sequences back to back (varlen / cu_seqlens layout)
+// This library packs the kept rows of all sequences back to back (varlen / cu_seqlens layout)
 // instead of padding to the longest, and breaks score ties by the lower index.
 //
 // Kernels:

@@ -32,15 +32,15 @@ def _check_qkv(q, k, v):
     _check(q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1,
            "Input tensor must have contiguous last dimension")
     _check(q.dtype == torch.bfloat16 and q.shape[-1] == 128,
-           "this build supports bf16 with head_dim 128 only")
+           "this library supports bf16 with head_dim 128 only")
 
 
 def _check_unsupported(p_dropout, window_size_left, window_size_right, softcap, return_softmax):
     # The reference build compiles these features out (kernels/fa2bias/build.py:137-138).
-    _check(p_dropout == 0.0, "this build does not support dropout")
-    _check(window_size_left < 0 and window_size_right < 0, "this build does not support local attention")
-    _check(softcap == 0.0, "this build does not support softcap")
-    _check(not return_softmax, "this build does not return the softmax")
+    _check(p_dropout == 0.0, "this library does not support dropout")
+    _check(window_size_left < 0 and window_size_right < 0, "this library does not support local attention")
+    _check(softcap == 0.0, "this library does not support softcap")
+    _check(not return_softmax, "this library does not return the softmax")
 
 
 def _check_bias(bias, batch, heads, seqlen_k, what="key bias"):
@@ -91,7 +91,7 @@ class KeyBiasExt:
         _check(seqused_k is None and leftpad_k is None and block_table_ is None,
                "seqused_k, leftpad_k and block_table are not supported")
         _check(cu_seqlens_q.data_ptr() == cu_seqlens_k.data_ptr() and max_seqlen_q == max_seqlen_k,
-               "this build runs self-attention over one cu_seqlens (q and k must share it)")
+               "this library runs self-attention over one cu_seqlens (q and k must share it)")
         _check(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_cuda and cu_seqlens_q.is_contiguous(),
                "cu_seqlens_q must have dtype int32, live on the device and be contiguous")
         _check(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "varlen q, k, v must be (total, heads, head_dim)")
@@ -162,7 +162,7 @@ class KeyBiasExt:
         _check_qkv(q, k, v)
         _check_unsupported(p_dropout, window_size_left, window_size_right, softcap, False)
         _check(cu_seqlens_q.data_ptr() == cu_seqlens_k.data_ptr() and max_seqlen_q == max_seqlen_k,
-               "this build runs self-attention over one cu_seqlens (q and k must share it)")
+               "this library runs self-attention over one cu_seqlens (q and k must share it)")
         _check(cu_seqlens_q.dtype == torch.int32 and cu_seqlens_q.is_cuda and cu_seqlens_q.is_contiguous(),
                "cu_seqlens_q must have dtype int32, live on the device and be contiguous")
         _check(dout.stride(-1) == 1 and out.stride(-1) == 1, "dout and out must have contiguous last dimension")

@@ -304,7 +304,7 @@ def load_model(checkpoint: str = "random", base_model: Optional[str] = None, gat
     kernels; the reference's "flex" / "sdpa" paths do not exist here); dtype: bfloat16 only.
     Nothing is downloaded."""
     if dtype is not None and dtype != torch.bfloat16:
-        raise ValueError("this build runs the decoder in torch.bfloat16 only")
+        raise ValueError("this library runs the decoder in torch.bfloat16 only")
     if gate_attn != "fa2":
         raise ValueError(f"gate_attn={gate_attn!r}: only 'fa2' (the key-bias HIP kernels) is available")
     if not checkpoint.startswith("random") and _is_gate_checkpoint(checkpoint):
