@@ -38,7 +38,12 @@ def _check_select(scores_np, seqs, dev):
         art = scores_np[r0 + s:r0 + e].astype(np.float64)
         art = art[np.isfinite(art)] if not np.isfinite(scores_np).all() else art
         if len(art) and np.isfinite(scores_np[r0 + s:r0 + e]).all():
-            np.testing.assert_allclose(sumsq[b], np.sum(art * art), rtol=1e-4)
+            want = np.sum(art * art)
+            if want > np.finfo(np.float32).max:     # the float32 sum overflows, as the reference's does
+                assert np.isinf(sumsq[b])
+            else:
+                # squares below float32's range flush to zero, as in the reference's float32 mean
+                np.testing.assert_allclose(sumsq[b], want, rtol=1e-4, atol=1e-37)
     return keep, p
 
 
@@ -56,8 +61,12 @@ def test_random_ragged_batch(cuda):
     _check_select(scores_bf, seqs, cuda)
 
 
-@pytest.mark.parametrize("kind", ["all_equal", "few_values", "nan_and_zeros", "steps"])
+@pytest.mark.parametrize("kind", ["all_equal", "few_values", "nan_and_zeros", "steps", "infinities", "huge_range",
+                                  "two_clusters", "tiny_range", "denormals", "negative_only"])
 def test_heavy_ties(cuda, kind):
+    """Tie patterns plus the ranges that steer the value-space first pass: infinities and spans
+    that overflow float (pass skipped), two far clusters (everything in the end bins), ranges of a
+    few ulps and of denormals, negative-only scores."""
     rng = np.random.default_rng(1)
     n = 10_000
     if kind == "all_equal":
@@ -66,6 +75,21 @@ def test_heavy_ties(cuda, kind):
         s = rng.integers(0, 4, n).astype(np.float32)
     elif kind == "nan_and_zeros":
         s = rng.choice(np.array([0.0, -0.0, 1.0, -1.0, np.nan], np.float32), n)
+    elif kind == "infinities":
+        s = rng.standard_normal(n).astype(np.float32)
+        s[rng.choice(n, 50, replace=False)] = np.inf
+        s[rng.choice(n, 50, replace=False)] = -np.inf
+    elif kind == "huge_range":
+        s = (rng.standard_normal(n) * 10.0 ** rng.uniform(-38, 38, n)).astype(np.float32)
+        s[:2] = [np.finfo(np.float32).max, -np.finfo(np.float32).max]
+    elif kind == "two_clusters":
+        s = np.where(rng.random(n) < 0.5, 1e6, -1e6).astype(np.float32) + rng.standard_normal(n).astype(np.float32)
+    elif kind == "tiny_range":
+        s = (np.float32(1.0) + rng.integers(0, 8, n).astype(np.float32) * np.finfo(np.float32).eps).astype(np.float32)
+    elif kind == "denormals":
+        s = (rng.integers(-50, 50, n) * np.float32(1e-44)).astype(np.float32)
+    elif kind == "negative_only":
+        s = (-np.abs(rng.standard_normal(n)) - 3.0).astype(np.float32)
     else:
         s = np.repeat(np.arange(100, dtype=np.float32), 100)[rng.permutation(n)]
     seqs = [(0, n, 7, n - 3, K) for K in (1,)]
