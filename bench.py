@@ -250,6 +250,18 @@ def bench_ttft(dev, reps=5):
     return out
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (from /proc/cpuinfo), or 'unknown'."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_prune_baseline(seconds=3.0):
     """The oracle's top-K + keep + gathers (numpy, host cores) at the 32k gate workload, K=2000:
     topk order, sort, keep list, hidden + 2 layers' K/V row gathers."""
@@ -268,7 +280,7 @@ def cpu_prune_baseline(seconds=3.0):
             _ = t[kp]
         n += 1
     dt = (time.perf_counter() - t0) / n
-    return {"ms": round(dt * 1e3, 3), "cores": 1, "kind": "port",
+    return {"ms": round(dt * 1e3, 3), "cores": 1, "kind": "port", "cpu_model": cpu_model(),
             "sample": "oracle numpy top-K + keep + gathers of hidden and 2 layers of K/V, 32k / K=2000"}
 
 
@@ -298,6 +310,7 @@ def cpu_baseline(q, k, v, bias_raw, scale, seconds):
         done_rows += len(rows)
     dt = time.perf_counter() - t0
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"oracle float32 numpy fwd, last {done_rows} query rows x {H} heads of the 32k causal "
                       f"workload (full key range each), {flops:.3e} FLOP in {dt:.1f} s"}
 
