@@ -640,7 +640,6 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const fl
 // row_start[b] + keep[j] of every stream and writes destination row j.
 // ---------------------------------------------------------------------------------------------
 constexpr int kPThreads = 256;
-constexpr int kPRows = 4;     // kept rows per workgroup
 constexpr int kMaxStreams = 16;
 
 struct PackArgs {
@@ -657,14 +656,19 @@ struct PackArgs {
   float *bias_out;        // optional: gate bias of kept rows (0 on prefix / suffix rows)
 };
 
+// ROWS kept rows per workgroup: 4 for large packs, 1 when there are too few rows to give every CU
+// several workgroups (small K: the copy is latency-bound and wants as many rows in flight as possible)
+template <int ROWS>
 __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
+  constexpr int kPRows = ROWS;
   __shared__ int64_t src_row[kPRows];
+  __shared__ int64_t s_pos[kPRows];
   __shared__ int s_seq[kPRows];
   const int tid = threadIdx.x;
   const int64_t j0 = (int64_t)blockIdx.x * kPRows;
   if (tid < kPRows) {
     const int64_t j = j0 + tid;
-    int64_t srow = -1;
+    int64_t srow = -1, pos = 0;
     int sb = 0;
     if (j < a.total_kept) {
       int lo = 0, hi = a.nseq - 1;   // last sequence with kept_start <= j
@@ -673,20 +677,11 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
         if ((int64_t)a.geom[6 * mid + 5] <= j) lo = mid; else hi = mid - 1;
       }
       sb = lo;
-      const int64_t pos = a.keep[j];
+      pos = a.keep[j];
       srow = (int64_t)a.geom[6 * lo] + pos;
-      if (a.pos_out) a.pos_out[j] = pos;
-      if (a.bias_out) {
-        const int s = a.geom[6 * lo + 2], e = a.geom[6 * lo + 3];
-        float bv = 0.f;
-        if (pos >= s && pos < e && a.bias_src) {
-          bv = a.bias_src[srow];
-          if (a.sumsq) bv *= rsqrtf(a.sumsq[lo] / (float)(e - s) + a.eps);
-        }
-        a.bias_out[j] = bv;
-      }
     }
     src_row[tid] = srow;
+    s_pos[tid] = pos;
     s_seq[tid] = sb;
   }
   __syncthreads();
@@ -719,6 +714,24 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
         if (dst[k]) *reinterpret_cast<u32x4 *>(dst[k]) = v[k];
+    }
+  }
+  // positions and gate bias of the rows (after this thread's share of the copy is issued)
+  if (tid >= kPThreads - kPRows) {
+    const int r = tid - (kPThreads - kPRows);
+    const int64_t j = j0 + r, srow = src_row[r], pos = s_pos[r];
+    if (srow >= 0) {
+      if (a.pos_out) a.pos_out[j] = pos;
+      if (a.bias_out) {
+        const int lo = s_seq[r];
+        const int s = a.geom[6 * lo + 2], e = a.geom[6 * lo + 3];
+        float bv = 0.f;
+        if (pos >= s && pos < e && a.bias_src) {
+          bv = a.bias_src[srow];
+          if (a.sumsq) bv *= rsqrtf(a.sumsq[lo] / (float)(e - s) + a.eps);
+        }
+        a.bias_out[j] = bv;
+      }
     }
   }
 }
@@ -800,9 +813,11 @@ extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, co
   a.sumsq = sumsq;
   a.eps = rms_eps;
   a.bias_out = bias_out;
-  const int64_t nb = (total_kept + kPRows - 1) / kPRows;
-  TG_CHECK(nb < (1ll << 31), "grid too large");
-  hipLaunchKernelGGL(gate_pack_kernel, dim3((unsigned)nb), dim3(kPThreads), 0, stream, a);
+  TG_CHECK(total_kept < (1ll << 31), "grid too large");
+  if (total_kept < 16 * 256)
+    hipLaunchKernelGGL(gate_pack_kernel<1>, dim3((unsigned)total_kept), dim3(kPThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL(gate_pack_kernel<4>, dim3((unsigned)((total_kept + 3) / 4)), dim3(kPThreads), 0, stream, a);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }
