@@ -221,8 +221,11 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 }
 
 // Wave 0: over the 16 per-wave 256-bin histograms, find the bin d holding the sel[2]-th largest
-// element (bins counted from the top); sel[3] = d, sel[2] = its rank within the bin; for key-space
-// bins (width 2^shift from lo) also sel[0..1] = the bin's key range (clipped to the current hi).
+// element (bins counted from the top); sel[3] = d, sel[4] = its element count, sel[2] = the rank
+// within the bin; for key-space bins (width 2^shift from lo) also sel[0..1] = the bin's key range
+// (clipped to the current hi).
+// NH = number of histograms to sum (16 per-wave ones, or 1 shared one).
+template <int NH = kTWaves>
 __device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *sel, uint32_t lo, int shift) {
   // lane l owns bins 255-4l .. 252-4l (descending)
   int c[4], lt = 0;
@@ -230,7 +233,7 @@ __device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *se
   for (int j = 0; j < 4; ++j) {
     int t = 0;
 #pragma unroll
-    for (int w = 0; w < kTWaves; ++w) t += h[w][255 - 4 * lane - j];
+    for (int w = 0; w < NH; ++w) t += h[w][255 - 4 * lane - j];
     c[j] = t;
     lt += t;
   }
@@ -243,10 +246,10 @@ __device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *se
   const int before = incl - lt;
   const int krem = (int)sel[2];
   if (before < krem && krem <= incl) {
-    int acc = before, d = 0;
+    int acc = before, d = 0, cd = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; break; }
+      if (acc + c[j] >= krem) { d = 255 - 4 * lane - j; cd = c[j]; break; }
       acc += c[j];
     }
     const uint32_t hi = sel[1];
@@ -256,6 +259,7 @@ __device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *se
     sel[1] = (nhi_raw < nlo || nhi_raw > hi) ? hi : nhi_raw;
     sel[2] = (uint32_t)(krem - acc);
     sel[3] = (uint32_t)d;
+    sel[4] = (uint32_t)cd;
   }
 }
 
@@ -268,9 +272,12 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
                                                                      int64_t *keep, float *sumsq) {
   static_assert(KPT % 4 == 0, "bins are cached four per register");
   constexpr int NB = KPT * kTWaves;    // 64-key blocks
+  constexpr int kCand = 4096;          // keys of the chosen value bin gathered into LDS
   __shared__ int hist[2][kTWaves][256];   // double-buffered: the next pass's copy is cleared early
   __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
-  __shared__ uint32_t sel[4];             // lo, hi, k_rem, chosen bin
+  __shared__ uint32_t cand[kCand];
+  __shared__ int wofs[kTWaves];
+  __shared__ uint32_t sel[5];             // lo, hi, k_rem, chosen bin, its count
   __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
   __shared__ float red[kTWaves];
 
@@ -350,29 +357,70 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
       __syncthreads();
       if (wave == 0) select_bin(hist[0], lane, sel, 0u, 0);
       __syncthreads();
-      // key range of the chosen bin
+      // the chosen bin: its key range, and (when it holds at most kCand keys) its keys gathered
+      // into LDS so that the key-space passes below read a few LDS words instead of every key
       const uint32_t d = sel[3];
+      const int nc = (int)sel[4];
+      const bool gather = nc <= kCand;     // block-uniform
+      auto in_bin = [&](int r) { return key[r] != 0u && ((bins[r / 4] >> (8 * (r % 4))) & 0xffu) == d; };
+      int wcnt = 0;
       uint32_t bmin = 0xffffffffu, bmax = 0u;
 #pragma unroll
       for (int r = 0; r < KPT; ++r) {
-        const uint32_t u = key[r];
-        const bool in = u != 0u && ((bins[r / 4] >> (8 * (r % 4))) & 0xffu) == d;
-        bmin = in ? min(bmin, u) : bmin;
-        bmax = in ? max(bmax, u) : bmax;
+        const bool in = in_bin(r);
+        bmin = in ? min(bmin, key[r]) : bmin;
+        bmax = in ? max(bmax, key[r]) : bmax;
+        if (gather) wcnt += __builtin_popcountll(__builtin_amdgcn_ballot_w64(in));
       }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) {
         bmin = min(bmin, (uint32_t)__shfl_xor((int)bmin, o));
         bmax = max(bmax, (uint32_t)__shfl_xor((int)bmax, o));
       }
-      if (lane == 0) { wmin[wave] = bmin; wmax[wave] = bmax; }
+      if (lane == 0) { wmin[wave] = bmin; wmax[wave] = bmax; wofs[wave] = wcnt; }
       __syncthreads();
       if (tid == 0) {
         uint32_t a = 0xffffffffu, z = 0u;
-        for (int w = 0; w < kTWaves; ++w) { a = min(a, wmin[w]); z = max(z, wmax[w]); }
+        int o = 0;
+        for (int w = 0; w < kTWaves; ++w) {
+          a = min(a, wmin[w]);
+          z = max(z, wmax[w]);
+          const int c = wofs[w];
+          wofs[w] = o;
+          o += c;
+        }
         sel[0] = a; sel[1] = z;
       }
       __syncthreads();
+      if (gather) {
+        int base = wofs[wave];
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+          const bool in = in_bin(r);
+          const uint64_t m = __builtin_amdgcn_ballot_w64(in);
+          if (in) cand[base + lanes_below(m)] = key[r];
+          base += __builtin_popcountll(m);
+        }
+        __syncthreads();
+        // key-space passes over the gathered keys only, into one shared histogram per pass (few
+        // keys: little contention; the bin search then reads 256 counters instead of 16 x 256)
+        int cb = 1;
+        while (true) {
+          const uint32_t lo = sel[0], hi = sel[1];
+          if (lo == hi) break;                             // block-uniform
+          const uint32_t span = hi - lo;
+          const int shift = span < 256u ? 0 : 32 - __builtin_clz(span >> 8);
+          if (tid < 256) hist[cb ^ 1][0][tid] = 0;
+          for (int i = tid; i < nc; i += kTThreads) {
+            const uint32_t u = cand[i];
+            if (u >= lo && u <= hi) atomicAdd(&hist[cb][0][(u - lo) >> shift], 1);
+          }
+          __syncthreads();
+          if (wave == 0) select_bin<1>(hist[cb], lane, sel, lo, shift);
+          __syncthreads();
+          cb ^= 1;
+        }
+      }
       pb = 1;
     }
   }
@@ -460,7 +508,7 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const fl
   constexpr int NB = kTChunk * kTWaves;   // 64-key blocks per chunk
   __shared__ int hist[2][kTWaves][256];
   __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
-  __shared__ uint32_t sel[4];             // lo, hi, k_rem
+  __shared__ uint32_t sel[5];             // lo, hi, k_rem (and the bin fields select_bin writes)
   __shared__ int carry[2];                // ties seen, rows kept: over the chunks before this one
   __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
   __shared__ float red[kTWaves];
