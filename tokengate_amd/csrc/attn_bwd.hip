@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char vs[2][kTileBytes];   // sigma rows, chunk ^ (row%16)
   __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
   const int hl = lq / QW, ql = lq % QW;
   const int hgroups = a.group / HP;
   const int per_q = a.hkv * hgroups;
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
   auto lslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return ls0; else return ls1; };
   auto dslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return dsh0; else return dsh1; };
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
   // heaviest first: under the causal mask the first key tiles see the most queries
   const int kh = blockIdx.x % a.hkv;
   const int rest = blockIdx.x / a.hkv;

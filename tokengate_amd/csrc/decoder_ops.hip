@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16_t *x, int64_t x
                                                       int64_t ro_rs, const bf16_t *__restrict__ w,
                                                       bf16_t *out, int64_t o_rs, int64_t rows, int d, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   if (row >= rows) return;
   const int nch = d >> 3;
   float v[CPL][8];
@@ -178,7 +178,7 @@ __global__ __launch_bounds__(256) void branch_readout_kernel(const bf16_t *__res
                                                              const bf16_t *__restrict__ w,
                                                              float *__restrict__ out) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave_id();
   if (row >= rows) return;
   const int nch = inter >> 3;
   const bf16_t *g = gu + row * gu_rs;

@@ -76,7 +76,7 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     if constexpr (B == 0) return ws0; else if constexpr (B == 1) return ws1; else if constexpr (B == 2) return ws2;
     else return ws3;
   };
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
   const int64_t r0 = (int64_t)blockIdx.x * kSRows;
 
   const int64_t rows_here = min((int64_t)kSRows, a.n_rows - r0);
@@ -281,7 +281,7 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
   __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
   __shared__ float red[kTWaves];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int32_t *gm = geom + 6 * blockIdx.x;
   const int64_t row_start = gm[0];
   const int seq_len = gm[1], s = gm[2], e = gm[3], kc = gm[4];
@@ -513,7 +513,7 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const fl
   __shared__ uint32_t wmin[kTWaves], wmax[kTWaves];
   __shared__ float red[kTWaves];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int32_t *gm = geom + 6 * blockIdx.x;
   const int64_t row_start = gm[0];
   const int seq_len = gm[1], s = gm[2], e = gm[3], kc = gm[4];

@@ -129,6 +129,12 @@ __device__ __forceinline__ void wait_vm_outstanding(int n) {
 #undef TG_VMCNT
 }
 
+// Index of this wave in its workgroup, held in a scalar register.  The compiler cannot prove that
+// threadIdx.x / 64 is the same in every lane of a wave, so without this every condition derived
+// from the wave index (tile skips, mask checks) is compiled as exec-masked per-lane code that
+// runs on every path instead of a scalar branch.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Two floats -> packed bf16 pair (round to nearest even, v_cvt_pk_bf16_f32).
