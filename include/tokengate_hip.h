@@ -42,7 +42,12 @@ const char *tg_last_error(void);
  * (kernels/fa2bias/keybias.py:40-44; patched mha_fwd, keybias.patch:7-28, 65-83, 279-332).
  * bias_raw may be NULL (plain causal/non-causal attention, the Phase-1 "flash" call).
  * Causal masking aligns the last query with the last key (key j visible to query i iff
- * j <= i + Sk - Sq).  Rows that see no key get out = 0 and lse = +inf. */
+ * j <= i + Sk - Sq).  Rows that see no key get out = 0 and lse = +inf.
+ * workspace: caller-allocated device memory of tg_keybias_fwd_workspace_size() bytes (16-byte
+ * aligned) for the key-range split of launches too small to fill the GPU, like the split-KV
+ * accumulators the reference's mha_fwd allocates for itself (softmax_lse_accum / out_accum in
+ * flash-attn's set_params_splitkv); NULL, or fewer bytes, runs without the split.  Contents need
+ * no initialisation; calls that share one workspace must be stream-ordered. */
 int tg_keybias_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
                    void *out, float *lse,
                    int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
@@ -52,12 +57,18 @@ int tg_keybias_fwd(const void *q, const void *k, const void *v, const float *bia
                    int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
                    int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
                    int64_t bias_batch_stride, int64_t bias_head_stride,
-                   float softmax_scale, int32_t causal, hipStream_t stream);
+                   float softmax_scale, int32_t causal,
+                   void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes tg_keybias_fwd uses for these sizes on the current device (0: no split). */
+int64_t tg_keybias_fwd_workspace_size(int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                                      int32_t num_heads, int32_t num_heads_k, int32_t causal);
 
 /* Variable-length key-bias attention forward (one causal attention per packed sequence).
  * Replaces ext().varlen_fwd(q, k, v, None, cu, cu, None, None, None, bias_raw, max, max, 0.0,
  * scale, False, causal, -1, -1, 0.0, False, None) (kernels/fa2bias/keybias.py:90-100; varlen
- * bias enabled by kernels/fa2bias/build.py:58-78).  cu_seqlens serves both q and k. */
+ * bias enabled by kernels/fa2bias/build.py:58-78).  cu_seqlens serves both q and k.
+ * workspace: as for tg_keybias_fwd, sized by tg_keybias_varlen_fwd_workspace_size(). */
 int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
                           void *out, float *lse, const int32_t *cu_seqlens,
                           int32_t num_seqs, int32_t max_seqlen, int32_t total,
@@ -67,7 +78,12 @@ int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const flo
                           int64_t v_row_stride, int64_t v_head_stride,
                           int64_t o_row_stride, int64_t o_head_stride,
                           int64_t bias_seq_stride, int64_t bias_head_stride,
-                          float softmax_scale, int32_t causal, hipStream_t stream);
+                          float softmax_scale, int32_t causal,
+                          void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes tg_keybias_varlen_fwd uses for these sizes on the current device (0: no split). */
+int64_t tg_keybias_varlen_fwd_workspace_size(int32_t num_seqs, int32_t max_seqlen,
+                                             int32_t num_heads, int32_t num_heads_k, int32_t causal);
 
 /* Dense key-bias attention backward.
  * Replaces ext().bwd(dout, q, k, v, out, lse, None, None, None, bias_raw, 0.0, scale, causal,

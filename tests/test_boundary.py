@@ -19,7 +19,7 @@ def _header_symbols():
     for name in os.listdir(os.path.join(ROOT, "include")):
         if name.endswith(".h"):
             text = open(os.path.join(ROOT, "include", name)).read()
-            syms += re.findall(r"^\s*(?:int|const\s+char\s*\*|void)\s*(tg_\w+)\s*\(", text, flags=re.M)
+            syms += re.findall(r"^\s*(?:int64_t|int|const\s+char\s*\*|void)\s*(tg_\w+)\s*\(", text, flags=re.M)
     return sorted(set(syms))
 
 
@@ -80,11 +80,31 @@ def test_c_abi_rejects_bad_head_dim_without_touching_the_gpu():
     from tokengate_amd import _lib
     lib = _lib.load()
     rc = lib.tg_keybias_fwd(16, 16, 16, None, 16, 16, 1, 8, 8, 2, 1, 64,
-                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None)
+                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None, 0, None)
     assert rc != 0 and b"head_dim" in lib.tg_last_error()
     rc = lib.tg_keybias_fwd(16, 16, 16, None, 16, 16, 1, 8, 8, 3, 2, 128,
-                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None)
+                            0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 1.0, 1, None, 0, None)
     assert rc != 0 and b"divide" in lib.tg_last_error()
+
+
+def test_fwd_workspace_size_queries():
+    """The split workspace is planned only for grids that leave the chip idle, and never for
+    invalid sizes; the size queries make no GPU call."""
+    from tokengate_amd import _lib
+    lib = _lib.load()
+    assert lib.tg_keybias_fwd_workspace_size(0, 4096, 4096, 16, 8, 1) == 0
+    assert lib.tg_keybias_fwd_workspace_size(1, 4096, 4096, 16, 7, 1) == 0
+    assert lib.tg_keybias_varlen_fwd_workspace_size(1, 0, 16, 8, 1) == 0
+    # 32k causal fills the chip with 8-wave workgroups: no split
+    assert lib.tg_keybias_fwd_workspace_size(1, 32768, 32768, 16, 8, 1) == 0
+    # a 4k causal prompt fills the resident slots (no split); Phase 2 at K=2000 (2320 rows) and one
+    # decode row over a long cache leave most of them empty and are split
+    assert lib.tg_keybias_fwd_workspace_size(1, 4096, 4096, 16, 8, 1) == 0
+    assert lib.tg_keybias_fwd_workspace_size(1, 2320, 2320, 16, 8, 1) > 0
+    assert lib.tg_keybias_varlen_fwd_workspace_size(1, 2320, 16, 8, 1) > 0
+    assert lib.tg_keybias_fwd_workspace_size(1, 1, 32768, 16, 8, 1) > 0
+    # too few key tiles to split
+    assert lib.tg_keybias_fwd_workspace_size(1, 1, 128, 16, 8, 1) == 0
 
 
 def test_python_checks_match_reference_messages():

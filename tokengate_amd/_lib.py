@@ -22,11 +22,13 @@ SIGNATURES = {
     "tg_keybias_fwd": [vp, vp, vp, vp, vp, vp,
                        i32, i32, i32, i32, i32, i32,
                        i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
-                       i64, i64, f32, i32, vp],
+                       i64, i64, f32, i32, vp, i64, vp],
+    "tg_keybias_fwd_workspace_size": [i32, i32, i32, i32, i32, i32],
     "tg_keybias_varlen_fwd": [vp, vp, vp, vp, vp, vp, vp,
                               i32, i32, i32, i32, i32, i32,
                               i64, i64, i64, i64, i64, i64, i64, i64,
-                              i64, i64, f32, i32, vp],
+                              i64, i64, f32, i32, vp, i64, vp],
+    "tg_keybias_varlen_fwd_workspace_size": [i32, i32, i32, i32, i32],
     "tg_keybias_bwd": [vp] * 12 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_keybias_varlen_bwd": [vp] * 13 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_gate_score_mlp": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
@@ -37,7 +39,8 @@ SIGNATURES = {
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
     "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
 }
-RESTYPES = {"tg_last_error": C.c_char_p}
+RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,
+            "tg_keybias_varlen_fwd_workspace_size": C.c_int64}
 
 
 def lib_path(site: str = None) -> str:
@@ -62,6 +65,17 @@ def load(site: str = None):
         if site is None:
             _lib = lib
         return lib
+
+
+def fwd_workspace(size_fn: str, device, *size_args):
+    """Device workspace for the forward's key-range split (tg_keybias_fwd / tg_keybias_varlen_fwd),
+    or None when the library plans no split for these sizes.  Returns (tensor, pointer, bytes)."""
+    n = int(getattr(load(), size_fn)(*size_args))
+    if n <= 0:
+        return None, None, 0
+    import torch
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    return ws, ws.data_ptr(), n
 
 
 def call(name: str, *args) -> None:

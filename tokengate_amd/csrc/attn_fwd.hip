@@ -27,6 +27,7 @@
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
+#include <algorithm>
 #include <type_traits>
 
 #include "tg_common.h"
@@ -63,6 +64,14 @@ struct FwdArgs {
   int h, hkv, group;
   int n_qtiles;
   float scale_log2;            // softmax_scale * log2(e)
+  // Key-range split of the heaviest query tiles (small grids): the n_heavy heaviest query tiles
+  // of every (sequence, head group) are each processed by ns workgroups over consecutive key
+  // ranges; each writes a partial result (O normalised by its own row sum, bf16, and the running
+  // max / row sum) and the combine kernel merges them.  ns = 1, n_heavy = 0: no split.
+  int ns, n_heavy;
+  int64_t heavy_blocks;        // n_heavy * ns * (head groups) * batch: the grid's leading part
+  bf16_t *ws_o;                // [heavy unit][chunk][wave][8][64 lanes] x 16 B
+  float *ws_ml;                // [heavy unit][chunk][wave][64 lanes] x (m, l)
 };
 
 // MFMA row m = 8a + 4g + b (a, b in 0..3) of a 32-key block carries key sigma(m) = 16g + 4a + b,
@@ -120,14 +129,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   const int per_q = a.hkv * hgroups;
   const int bid = blockIdx.x;
   const int x = bid % per_q;
-  const int rest = bid / per_q;
   const int kh = x % a.hkv;
   const int hg = x / a.hkv;
   // Dense: heaviest q tile of every batch row first.  Varlen: sequence-major (all tiles of
   // sequence b before sequence b+1, heaviest first within it), so the workgroups resident at one
   // time share one sequence's K/V in L2 / MALL instead of streaming every sequence's K/V at once.
-  const int b = VARLEN ? rest / a.n_qtiles : rest % a.batch;
-  const int qt = a.n_qtiles - 1 - (VARLEN ? rest % a.n_qtiles : rest / a.batch);
+  // A split launch lists the chunks of the n_heavy heaviest tiles first, then the other tiles.
+  int b, rank, chunk = -1;
+  int64_t hunit = 0;
+  if (bid < a.heavy_blocks) {
+    const int r = bid / per_q;
+    chunk = r % a.ns;
+    const int r2 = r / a.ns;
+    b = VARLEN ? r2 / a.n_heavy : r2 % a.batch;
+    rank = VARLEN ? r2 % a.n_heavy : r2 / a.batch;
+    hunit = (int64_t)r2 * per_q + x;
+  } else {
+    const int r2 = (int)((bid - a.heavy_blocks) / per_q);
+    const int n_light = a.n_qtiles - a.n_heavy;
+    b = VARLEN ? r2 / n_light : r2 % a.batch;
+    rank = a.n_heavy + (VARLEN ? r2 % n_light : r2 / a.batch);
+  }
+  const int qt = a.n_qtiles - 1 - rank;
 
   int sq = a.sq, sk = a.sk;
   int64_t row0 = 0;
@@ -171,6 +194,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   int kv_end = sk;
   if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
   const int n_tiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
+  // key tiles [t_lo, t_hi) of this workgroup (a split tile's chunk covers its share of them)
+  int t_lo = 0, t_hi = n_tiles;
+  if (chunk >= 0) {
+    t_lo = (int)((int64_t)n_tiles * chunk / a.ns);
+    t_hi = (int)((int64_t)n_tiles * (chunk + 1) / a.ns);
+  }
 
   // ---- per-lane DMA source offsets (bytes within a tile; + tile * 64 rows per tile) ----
   // A 16 KB tile is 16 wave-loads of 1 KB; wave w issues loads w, w + kWaves, ...
@@ -231,7 +260,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     const int n0 = t * kBN;
     wait_vm<0>();
     ring_barrier();
-    if (t + 1 < n_tiles) issue_tile(t + 1, std::integral_constant<int, 1 - BUF>());
+    if (t + 1 < t_hi) issue_tile(t + 1, std::integral_constant<int, 1 - BUF>());
     if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) return;
 
     // ---- S^T = K Q^T + bias: 2 key blocks x 8 d-steps.  The accumulators start from the bias of
@@ -340,17 +369,36 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
       }
     }
   };
-  if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>());
-  int t = 0;
-  for (; t + 1 < n_tiles; t += 2) {
+  if (t_lo < t_hi) issue_tile(t_lo, std::integral_constant<int, 0>());
+  int t = t_lo;
+  for (; t + 1 < t_hi; t += 2) {
     tile_step(t, std::integral_constant<int, 0>());
     tile_step(t + 1, std::integral_constant<int, 1>());
   }
-  if (t < n_tiles) tile_step(t, std::integral_constant<int, 0>());
+  if (t < t_hi) tile_step(t, std::integral_constant<int, 0>());
 
   // ---- epilogue: normalise, write O (bf16) and LSE (natural log) ----
   const float l = pair_sum(lrun);
   const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (chunk >= 0) {
+    // partial result of this key chunk: O / l as bf16 (eight 16-byte pieces per lane, each
+    // piece a coalesced 1 KB wave store) and (running max in log2 units, row sum l)
+    const int64_t pw = (hunit * a.ns + chunk) * kWaves + wave;
+    u32x4 *po = reinterpret_cast<u32x4 *>(a.ws_o) + pw * (8 * 64) + lane;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const f32x16 &acc = oacc[j >> 1];
+      const int v0 = 8 * (j & 1);
+      const u32x4 w = {pack_bf16x2(acc[v0] * inv, acc[v0 + 1] * inv), pack_bf16x2(acc[v0 + 2] * inv, acc[v0 + 3] * inv),
+                       pack_bf16x2(acc[v0 + 4] * inv, acc[v0 + 5] * inv), pack_bf16x2(acc[v0 + 6] * inv, acc[v0 + 7] * inv)};
+      po[j * 64] = w;
+    }
+    float2 ml;
+    ml.x = mrun;
+    ml.y = l;
+    reinterpret_cast<float2 *>(a.ws_ml)[pw * 64 + lane] = ml;
+    return;
+  }
   if (qvalid) {
     bf16_t *orow = obase + (int64_t)qrow * a.o_rs + (int64_t)hl * a.o_hs;
 #pragma unroll
@@ -374,10 +422,96 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   }
 }
 
+// Merge of the key chunks of every split query tile.  One thread per 16-byte piece of a partial
+// (8 O values of one (head, query) column), so that every piece of every chunk is read by its
+// own thread.  With chunk c's running max m_c (log2 units), row sum l_c and normalised partial
+// O_c: m = max m_c, w_c = l_c 2^(m_c - m), O = sum w_c O_c / sum w_c, lse = (m + log2 sum w_c) ln 2.
+// Chunks that saw no key (l_c = 0) weigh nothing.
+constexpr int kCombineThreads = 256;
+template <int NW, int HP, bool VARLEN>
+__global__ __launch_bounds__(kCombineThreads) void keybias_fwd_combine_kernel(FwdArgs a) {
+  constexpr int QW = qpw<HP>();
+  constexpr int BM = bm<NW, HP>();
+  const int64_t t = (int64_t)blockIdx.x * kCombineThreads + threadIdx.x;   // (unit, wave, piece, lane)
+  const int lane = (int)(t & 63), j = (int)((t >> 6) & 7), wave = (int)((t >> 9) % NW);
+  const int64_t hunit = (t >> 9) / NW;
+  if (hunit >= a.heavy_blocks / a.ns) return;
+  const int lq = lane & 31, g = lane >> 5, hl = lq / QW, ql = lq % QW;
+  const int per_q = a.hkv * (a.group / HP);
+  const int x = (int)(hunit % per_q), r2 = (int)(hunit / per_q);
+  const int kh = x % a.hkv, hg = x / a.hkv;
+  const int b = VARLEN ? r2 / a.n_heavy : r2 % a.batch;
+  const int rank = VARLEN ? r2 % a.n_heavy : r2 / a.batch;
+  const int qt = a.n_qtiles - 1 - rank;
+  int sq = a.sq;
+  int64_t row0 = 0;
+  if constexpr (VARLEN) {
+    const int s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
+    row0 = s0;
+    sq = min(s1 - s0, a.sq);
+  }
+  const int qrow = qt * BM + wave * QW + ql;
+  if (qrow >= sq) return;   // the forward computed nothing for rows past the sequence
+
+  const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml);
+  const u32x4 *po = reinterpret_cast<const u32x4 *>(a.ws_o);
+  const int64_t pw0 = hunit * a.ns * NW + wave;   // chunk c: pw0 + c * NW
+  // one pass, the weights kept relative to the largest m seen so far (rescaled when it grows)
+  float mmax = -INFINITY;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.f;
+#pragma unroll 8
+  for (int c = 0; c < a.ns; ++c) {
+    const int64_t pw = pw0 + (int64_t)c * NW;
+    const float2 mc = ml[pw * 64 + lane];
+    const u32x4 pv = po[pw * (8 * 64) + j * 64 + lane];
+    if (!(mc.y > 0.f)) continue;
+    if (mc.x > mmax) {
+      const float sc = fast_exp2(mmax - mc.x);   // 0 while nothing has been added yet
+      wsum *= sc;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= sc;
+      mmax = mc.x;
+    }
+    const float w = mc.y * fast_exp2(mc.x - mmax);
+    wsum += w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[2 * e] += w * __builtin_bit_cast(float, pv[e] << 16);
+      acc[2 * e + 1] += w * __builtin_bit_cast(float, pv[e] & 0xffff0000u);
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const int h0 = kh * a.group + hg * HP;
+  bf16_t *orow = a.o + (VARLEN ? row0 * a.o_rs : (int64_t)b * a.o_bs) + (int64_t)qrow * a.o_rs +
+                 (int64_t)(h0 + hl) * a.o_hs;
+  // piece j holds accumulator values 8(j%2) .. 8(j%2)+7 of d-block j/2: d = 32 (j/2) + 16 (j%2)
+  // + 4g + {0..3} and the same + 8
+  const int d0 = 32 * (j >> 1) + 16 * (j & 1) + 4 * g;
+  const u32x2 w0 = {pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+  const u32x2 w1 = {pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
+  *reinterpret_cast<u32x2 *>(orow + d0) = w0;
+  *reinterpret_cast<u32x2 *>(orow + d0 + 8) = w1;
+  if (j == 0 && g == 0) {
+    const float lse = wsum > 0.f ? (mmax + __log2f(wsum)) * kLn2 : INFINITY;
+    const int hh = h0 + hl;
+    if constexpr (VARLEN)
+      a.lse[(int64_t)hh * a.lse_total + row0 + qrow] = lse;
+    else
+      a.lse[((int64_t)b * a.h + hh) * sq + qrow] = lse;
+  }
+}
+
 template <int NW, int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 void launch_fwd(const FwdArgs &a, int nblocks, hipStream_t stream) {
   hipLaunchKernelGGL((keybias_fwd_kernel<NW, HP, CAUSAL, HAS_BIAS, VARLEN>), dim3(nblocks), dim3(64 * NW), 0,
                      stream, a);
+  if (a.heavy_blocks > 0) {
+    const int64_t threads = a.heavy_blocks / a.ns * NW * 8 * 64;
+    hipLaunchKernelGGL((keybias_fwd_combine_kernel<NW, HP, VARLEN>),
+                       dim3((unsigned)((threads + kCombineThreads - 1) / kCombineThreads)), dim3(kCombineThreads), 0,
+                       stream, a);
+  }
 }
 
 template <bool VARLEN>
@@ -426,6 +560,57 @@ void pick_tiling(int hp, int rows, int64_t units, int &nw, int &n_qtiles) {
   n_qtiles = nw == 8 ? (int)t8 : (rows + bm4 - 1) / bm4;
 }
 
+// Key-range split plan.  A grid that leaves at least a quarter of the resident-workgroup slots
+// empty from the start (Phase 2 at small K, a few rows over a long cache, single-row decode) is
+// bound by its longest tiles while the chip idles: the tiles whose key range exceeds 1/ns of the
+// longest are split into ns chunks of consecutive key tiles (ns from the free slots, at least 4
+// key tiles per chunk), merged by the combine kernel.  A grid that fills the slots (a 4k prompt)
+// is not split: measured, the split's partial traffic and second launch cost more there than the
+// causal tail it removes.  Returns ns = 1 when nothing is split.
+struct SplitPlan {
+  int ns = 1, n_heavy = 0;
+  int64_t heavy_units = 0, bytes = 0;
+};
+constexpr int64_t kPartialBytesPerLane = 8 * 16 + 8;   // O / l as 64 bf16, then (m, l)
+SplitPlan plan_split(int nw, int hp, int n_qtiles, int64_t units, int sq, int sk, bool causal) {
+  SplitPlan p;
+  const int bmq = nw == 8 ? (hp == 2 ? bm<8, 2>() : bm<8, 1>()) : (hp == 2 ? bm<4, 2>() : bm<4, 1>());
+  const int64_t slots = (int64_t)device_cus() * (8 / nw);
+  const int64_t nblocks = (int64_t)n_qtiles * units;
+  if (nblocks <= 0 || 4 * nblocks > 3 * slots || sk <= 0) return p;
+  const int off = sk - sq;
+  auto tiles = [&](int qt) -> int {
+    int kv_end = sk;
+    if (causal) kv_end = std::min<int64_t>(sk, (int64_t)(qt + 1) * bmq + off);
+    return kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
+  };
+  const int tmax = tiles(n_qtiles - 1);
+  int ns = (int)std::min<int64_t>(32, std::max<int64_t>(2, slots / nblocks));
+  ns = std::min(ns, tmax / 4);
+  if (ns < 2) return p;
+  int n_heavy = 0;
+  for (int qt = n_qtiles - 1; qt >= 0 && (int64_t)tiles(qt) * ns > tmax; --qt) ++n_heavy;
+  if (n_heavy == 0) return p;
+  p.ns = ns;
+  p.n_heavy = n_heavy;
+  p.heavy_units = (int64_t)n_heavy * units;
+  p.bytes = p.heavy_units * ns * nw * 64 * kPartialBytesPerLane;
+  return p;
+}
+
+// Apply a plan to the launch arguments (no split if the workspace is missing or too small).
+// Returns the grid size.
+int64_t apply_split(FwdArgs &a, SplitPlan p, int nw, int64_t units, void *workspace, int64_t workspace_bytes) {
+  if (p.ns < 2 || workspace == nullptr || workspace_bytes < p.bytes) p = SplitPlan{};
+  a.ns = p.ns;
+  a.n_heavy = p.n_heavy;
+  a.heavy_blocks = p.heavy_units * p.ns;
+  a.ws_o = static_cast<bf16_t *>(workspace);
+  a.ws_ml = workspace ? reinterpret_cast<float *>(static_cast<char *>(workspace) + p.heavy_units * p.ns * nw * 64 * 128)
+                      : nullptr;
+  return a.heavy_blocks + (int64_t)(a.n_qtiles - a.n_heavy) * units;
+}
+
 int check_common(const void *q, const void *k, const void *v, const void *out, const float *lse,
                  int32_t num_heads, int32_t num_heads_k, int32_t head_dim) {
   TG_CHECK(head_dim == kD, "this library supports bf16 with head_dim 128 only (got head_dim %d)", head_dim);
@@ -460,7 +645,7 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
                               int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
                               int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
                               int64_t bias_batch_stride, int64_t bias_head_stride, float softmax_scale,
-                              int32_t causal, hipStream_t stream) {
+                              int32_t causal, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
   if (int e = check_common(q, k, v, out, lse, num_heads, num_heads_k, head_dim)) return e;
   TG_CHECK(batch >= 0 && seqlen_q >= 0 && seqlen_k >= 0, "negative size");
@@ -490,8 +675,11 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
   int nw = 8;
-  pick_tiling(hp, seqlen_q, (int64_t)batch * (num_heads / hp), nw, a.n_qtiles);
-  const int64_t nblocks = (int64_t)a.n_qtiles * batch * (num_heads / hp);
+  const int64_t units = (int64_t)batch * (num_heads / hp);
+  pick_tiling(hp, seqlen_q, units, nw, a.n_qtiles);
+  TG_CHECK(workspace == nullptr || aligned16(workspace), "workspace must be 16-byte aligned");
+  const int64_t nblocks = apply_split(a, plan_split(nw, hp, a.n_qtiles, units, seqlen_q, seqlen_k, causal != 0), nw,
+                                      units, workspace, workspace_bytes);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
   dispatch_fwd<false>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
   TG_HIP_CHECK(hipPeekAtLastError());
@@ -506,7 +694,7 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
                                      int64_t v_row_stride, int64_t v_head_stride, int64_t o_row_stride,
                                      int64_t o_head_stride, int64_t bias_seq_stride,
                                      int64_t bias_head_stride, float softmax_scale, int32_t causal,
-                                     hipStream_t stream) {
+                                     void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
   if (int e = check_common(q, k, v, out, lse, num_heads, num_heads_k, head_dim)) return e;
   TG_CHECK(cu_seqlens != nullptr, "cu_seqlens is null");
@@ -538,10 +726,37 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
   a.scale_log2 = softmax_scale * kLog2e;
   const int hp = (a.group % 2 == 0) ? 2 : 1;
   int nw = 8;
-  pick_tiling(hp, max_seqlen, (int64_t)num_seqs * (num_heads / hp), nw, a.n_qtiles);
-  const int64_t nblocks = (int64_t)a.n_qtiles * num_seqs * (num_heads / hp);
+  const int64_t units = (int64_t)num_seqs * (num_heads / hp);
+  pick_tiling(hp, max_seqlen, units, nw, a.n_qtiles);
+  TG_CHECK(workspace == nullptr || aligned16(workspace), "workspace must be 16-byte aligned");
+  const int64_t nblocks = apply_split(a, plan_split(nw, hp, a.n_qtiles, units, max_seqlen, max_seqlen, causal != 0),
+                                      nw, units, workspace, workspace_bytes);
   TG_CHECK(nblocks < (1ll << 31), "grid too large");
   dispatch_fwd<true>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
+}
+
+namespace {
+int64_t fwd_workspace_size(int32_t units_batch, int32_t seqlen_q, int32_t seqlen_k, int32_t num_heads,
+                           int32_t num_heads_k, int32_t causal) {
+  if (units_batch <= 0 || seqlen_q <= 0 || seqlen_k <= 0 || num_heads <= 0 || num_heads_k <= 0 ||
+      num_heads % num_heads_k != 0)
+    return 0;
+  const int hp = ((num_heads / num_heads_k) % 2 == 0) ? 2 : 1;
+  const int64_t units = (int64_t)units_batch * (num_heads / hp);
+  int nw = 8, nq = 0;
+  pick_tiling(hp, seqlen_q, units, nw, nq);
+  return plan_split(nw, hp, nq, units, seqlen_q, seqlen_k, causal != 0).bytes;
+}
+}  // namespace
+
+extern "C" int64_t tg_keybias_fwd_workspace_size(int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                                                  int32_t num_heads, int32_t num_heads_k, int32_t causal) {
+  return fwd_workspace_size(batch, seqlen_q, seqlen_k, num_heads, num_heads_k, causal);
+}
+
+extern "C" int64_t tg_keybias_varlen_fwd_workspace_size(int32_t num_seqs, int32_t max_seqlen, int32_t num_heads,
+                                                         int32_t num_heads_k, int32_t causal) {
+  return fwd_workspace_size(num_seqs, max_seqlen, max_seqlen, num_heads, num_heads_k, causal);
 }

@@ -85,6 +85,9 @@ class DecodeState:
         stream = torch.cuda.current_stream(q.device).cuda_stream
         lse = torch.empty(self.B, s.n_heads, 1, dtype=torch.float32, device=q.device)
         scale = 1.0 / math.sqrt(s.head_dim)
+        # one workspace for every sequence's launch (stream-ordered), sized for the longest
+        ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_fwd_workspace_size", q.device, 1, 1, max(lc.n),
+                                                  s.n_heads, s.n_kv_heads, 1)
         for b in range(self.B):
             kb = lc.k[lc.seg[b]:]
             vb = lc.v[lc.seg[b]:]
@@ -95,7 +98,7 @@ class DecodeState:
                       0, s.n_heads * s.head_dim, s.head_dim, 0, kb.stride(0), kb.stride(1),
                       0, vb.stride(0), vb.stride(1), 0, s.n_heads * s.head_dim, s.head_dim,
                       bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
-                      scale, 1, stream)
+                      scale, 1, ws_ptr if ws_bytes else None, ws_bytes, stream)
 
     @torch.no_grad()
     def step(self, tokens: torch.Tensor) -> torch.Tensor:

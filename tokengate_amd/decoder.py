@@ -172,13 +172,15 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     nseq = cu_seqlens.numel() - 1
     if bias_raw is not None and (bias_raw.dtype != torch.float32 or bias_raw.stride(-1) != 1):
         raise RuntimeError("varlen_attention: bias must be fp32 with a contiguous key axis")
+    ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_varlen_fwd_workspace_size", q.device, nseq, int(max_seqlen),
+                                              H, Hkv, 1)
     _lib.call("tg_keybias_varlen_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
               bias_raw.data_ptr() if bias_raw is not None else None, out.data_ptr(), lse.data_ptr(),
               cu_seqlens.data_ptr(), nseq, int(max_seqlen), T, H, Hkv, D,
               q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
               out.stride(0), out.stride(1),
               bias_raw.stride(0) if bias_raw is not None else 0, bias_raw.stride(1) if bias_raw is not None else 0,
-              float(scale), 1, _stream(q))
+              float(scale), 1, ws_ptr, ws_bytes, _stream(q))
     return out
 
 

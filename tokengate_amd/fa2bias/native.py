@@ -74,13 +74,15 @@ class KeyBiasExt:
             out = torch.empty_like(q)
         lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
         if B and Sq:
+            ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_fwd_workspace_size", q.device, B, Sq, Sk, H, Hkv,
+                                                      int(bool(is_causal)))
             _lib.call("tg_keybias_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
                       bias.data_ptr() if bias is not None else None, out.data_ptr(), lse.data_ptr(),
                       B, Sq, Sk, H, Hkv, D,
                       q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
                       v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
                       bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
-                      float(softmax_scale), int(bool(is_causal)), _stream(q))
+                      float(softmax_scale), int(bool(is_causal)), ws_ptr, ws_bytes, _stream(q))
         return [out, lse, torch.empty(0, device=q.device), torch.empty(0, device=q.device)]
 
     def varlen_fwd(self, q, k, v, out_, cu_seqlens_q, cu_seqlens_k, seqused_k, leftpad_k, block_table_,
@@ -108,13 +110,15 @@ class KeyBiasExt:
             out.zero_()
         lse = torch.empty((H, total), dtype=torch.float32, device=q.device)
         if nseq > 0 and total > 0 and max_seqlen_q > 0:
+            ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_varlen_fwd_workspace_size", q.device, nseq,
+                                                      int(max_seqlen_q), H, Hkv, int(bool(is_causal)))
             _lib.call("tg_keybias_varlen_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
                       bias.data_ptr() if bias is not None else None, out.data_ptr(), lse.data_ptr(),
                       cu_seqlens_q.data_ptr(), nseq, int(max_seqlen_q), total, H, Hkv, D,
                       q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
                       out.stride(0), out.stride(1),
                       bias.stride(0) if bias is not None else 0, bias.stride(1) if bias is not None else 0,
-                      float(softmax_scale), int(bool(is_causal)), _stream(q))
+                      float(softmax_scale), int(bool(is_causal)), ws_ptr, ws_bytes, _stream(q))
         return [out, lse, torch.empty(0, device=q.device), torch.empty(0, device=q.device)]
 
     def bwd(self, dout, q, k, v, out, softmax_lse, dq_, dk_, dv_, alibi_slopes_, p_dropout, softmax_scale,
