@@ -198,7 +198,8 @@ def bench_ttft(dev, reps=5):
     prefill through the first token, sync; median of `reps` after one warmup.  The "_branch" line
     runs the finalized gate instead: the MLP scoring branch (a copy of the gate layer's SwiGLU, I
     6144, with an absorbed (1, I) readout row) on the gate layer's attention boundary, the gate
-    layer's MLP on the kept rows only, scaled softmax in Phase 2."""
+    layer's MLP on the kept rows only, scaled softmax in Phase 2.  decode_ms_per_token (32k, K=2000
+    and K=all): greedy decode steps after the prefill, median of 8 after 2 warmup steps."""
     import statistics
     import torch
     from tokengate_amd import decoder as dec
@@ -212,7 +213,24 @@ def bench_ttft(dev, reps=5):
 
     branch = G.random_branch_head(wts, 1, seed=5)
 
-    def run(name, lens, Ks, head=head):
+    def decode_ms(r, head, steps=8, warmup=2):
+        """Greedy decode after the prefill r (tokengate_amd.decode.DecodeState.step, all 28 layers,
+        attention over the pruned caches): median milliseconds per token over `steps` steps."""
+        from tokengate_amd.decode import DecodeState
+        st = DecodeState(wts, head, 1, r, steps + warmup + 1)
+        cur = r.first_tokens
+        ts = []
+        for i in range(steps + warmup):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            cur = st.step(cur)
+            torch.cuda.synchronize()
+            if i >= warmup:
+                ts.append((time.perf_counter() - t0) * 1e3)
+        del st
+        return round(statistics.median(ts), 3)
+
+    def run(name, lens, Ks, head=head, decode=False):
         ids = [torch.randint(0, shape.vocab, (n,), generator=g).to(dev) for n in lens]
         starts = [64] * len(lens)
         ends = [n - 256 for n in lens]
@@ -222,6 +240,8 @@ def bench_ttft(dev, reps=5):
         out[name] = {"ttft_ms": round(statistics.median(times), 3), "reps_ms": [round(t, 3) for t in times],
                      "prompt_tokens": sum(lens), "kept_tokens": r.cu_kept[-1],
                      "phase_ms": {k: round(v, 3) for k, v in r.phase_ms.items()}}
+        if decode:
+            out[name]["decode_ms_per_token"] = decode_ms(r, head)
         if r.cu_kept[-1] <= 32768:
             # Phase 2 replayed from a captured graph (captured during the warm-up call)
             graphs = P.Phase2Graphs()
@@ -238,8 +258,8 @@ def bench_ttft(dev, reps=5):
         torch.cuda.empty_cache()
 
     for K in (100, 2000):
-        run(f"32k_K{K}", [32768], [K])
-    run("32k_Kall", [32768], [10_000_000])
+        run(f"32k_K{K}", [32768], [K], decode=K == 2000)
+    run("32k_Kall", [32768], [10_000_000], decode=True)
     run("32k_K2000_branch", [32768], [2000], head=branch)
     rng = torch.Generator().manual_seed(17)
     lens = [int(x) for x in torch.randint(16384, 131073, (8,), generator=rng)]

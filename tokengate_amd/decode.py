@@ -78,6 +78,12 @@ class DecodeState:
         self.ssmax = pf.kept_ratio is not None
         self.n_kept_f = h2d(torch.tensor([float(x) for x in pf.n_kept], dtype=torch.float32), dev)
         self.steps = 0
+        # one key-range-split workspace for every attention launch of every step (stream-ordered),
+        # sized for the longest cache this state can reach (the planned size grows with the keys)
+        longest = max(max(lc.n) for lc in self.layers) + max_new_tokens
+        self._ws, ptr, self._ws_bytes = _lib.fwd_workspace("tg_keybias_fwd_workspace_size", dev, 1, 1, longest,
+                                                           shape.n_heads, shape.n_kv_heads, 1)
+        self._ws_ptr = ptr if self._ws_bytes else None
 
     def _attend(self, lc: _LayerCache, q: torch.Tensor, out: torch.Tensor) -> None:
         """q (B, H, D) -> out (B, H, D): sequence b attends over its segment's n[b] rows."""
@@ -85,9 +91,7 @@ class DecodeState:
         stream = torch.cuda.current_stream(q.device).cuda_stream
         lse = torch.empty(self.B, s.n_heads, 1, dtype=torch.float32, device=q.device)
         scale = 1.0 / math.sqrt(s.head_dim)
-        # one workspace for every sequence's launch (stream-ordered), sized for the longest
-        ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_fwd_workspace_size", q.device, 1, 1, max(lc.n),
-                                                  s.n_heads, s.n_kv_heads, 1)
+        ws_ptr, ws_bytes = self._ws_ptr, self._ws_bytes
         for b in range(self.B):
             kb = lc.k[lc.seg[b]:]
             vb = lc.v[lc.seg[b]:]
