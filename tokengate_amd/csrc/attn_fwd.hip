@@ -422,20 +422,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   }
 }
 
-// Merge of the key chunks of every split query tile.  One thread per 16-byte piece of a partial
-// (8 O values of one (head, query) column), so that every piece of every chunk is read by its
-// own thread.  With chunk c's running max m_c (log2 units), row sum l_c and normalised partial
-// O_c: m = max m_c, w_c = l_c 2^(m_c - m), O = sum w_c O_c / sum w_c, lse = (m + log2 sum w_c) ln 2.
+// Merge of the key chunks of every split query tile.  A 512-thread workgroup covers 8 / CG of the
+// eight 16-byte pieces (8 O values of each of the 64 columns of one forward wave) of one split
+// tile; per piece, thread (group cg, lane) folds chunks cg, cg + CG, ... of its column and group 0
+// merges the CG partial results through LDS, so that a long chunk list (a decode row over a long
+// cache) is walked CG ways in parallel.
+// With chunk c's running max m_c (log2 units), row sum l_c and normalised partial O_c:
+// m = max m_c, w_c = l_c 2^(m_c - m), O = sum w_c O_c / sum w_c, lse = (m + log2 sum w_c) ln 2.
 // Chunks that saw no key (l_c = 0) weigh nothing.
-constexpr int kCombineThreads = 256;
+constexpr int kCombineMaxGroups = 8;
 template <int NW, int HP, bool VARLEN>
-__global__ __launch_bounds__(kCombineThreads) void keybias_fwd_combine_kernel(FwdArgs a) {
+__global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int CG) {
   constexpr int QW = qpw<HP>();
   constexpr int BM = bm<NW, HP>();
-  const int64_t t = (int64_t)blockIdx.x * kCombineThreads + threadIdx.x;   // (unit, wave, piece, lane)
-  const int lane = (int)(t & 63), j = (int)((t >> 6) & 7), wave = (int)((t >> 9) % NW);
-  const int64_t hunit = (t >> 9) / NW;
-  if (hunit >= a.heavy_blocks / a.ns) return;
+  // (m, wsum, acc[8]) of groups 1..CG-1 of each piece: PP * (CG - 1) < 8 slots
+  __shared__ float part[kCombineMaxGroups - 1][10][64];
+  const int PP = 8 / CG;                                   // pieces per workgroup
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int cg = wv % CG, pj = wv / CG;
+  const int j = (int)(blockIdx.x % CG) * PP + pj;          // piece
+  const int wave = (int)((blockIdx.x / CG) % NW);          // forward wave whose columns these are
+  const int64_t hunit = (blockIdx.x / CG) / NW;
+  float (*mypart)[10][64] = part + pj * (CG - 1);
   const int lq = lane & 31, g = lane >> 5, hl = lq / QW, ql = lq % QW;
   const int per_q = a.hkv * (a.group / HP);
   const int x = (int)(hunit % per_q), r2 = (int)(hunit / per_q);
@@ -450,36 +458,57 @@ __global__ __launch_bounds__(kCombineThreads) void keybias_fwd_combine_kernel(Fw
     row0 = s0;
     sq = min(s1 - s0, a.sq);
   }
-  const int qrow = qt * BM + wave * QW + ql;
-  if (qrow >= sq) return;   // the forward computed nothing for rows past the sequence
+  const int qw0 = qt * BM + wave * QW;
+  if (qw0 >= sq) return;   // workgroup-uniform: the forward computed nothing for these rows
+  const int qrow = qw0 + ql;
+  const bool valid = qrow < sq;
 
   const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml);
   const u32x4 *po = reinterpret_cast<const u32x4 *>(a.ws_o);
   const int64_t pw0 = hunit * a.ns * NW + wave;   // chunk c: pw0 + c * NW
-  // one pass, the weights kept relative to the largest m seen so far (rescaled when it grows)
-  float mmax = -INFINITY;
+  // fold this group's chunks, the weights relative to the largest m seen so far
+  float mmax = -INFINITY, wsum = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float wsum = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < a.ns; ++c) {
-    const int64_t pw = pw0 + (int64_t)c * NW;
-    const float2 mc = ml[pw * 64 + lane];
-    const u32x4 pv = po[pw * (8 * 64) + j * 64 + lane];
-    if (!(mc.y > 0.f)) continue;
-    if (mc.x > mmax) {
-      const float sc = fast_exp2(mmax - mc.x);   // 0 while nothing has been added yet
-      wsum *= sc;
+  if (valid) {
+#pragma unroll 4
+    for (int c = cg; c < a.ns; c += CG) {
+      const int64_t pw = pw0 + (int64_t)c * NW;
+      const float2 mc = ml[pw * 64 + lane];
+      const u32x4 pv = po[pw * (8 * 64) + j * 64 + lane];
+      if (!(mc.y > 0.f)) continue;
+      if (mc.x > mmax) {
+        const float sc = fast_exp2(mmax - mc.x);   // 0 while nothing has been added yet
+        wsum *= sc;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] *= sc;
-      mmax = mc.x;
-    }
-    const float w = mc.y * fast_exp2(mc.x - mmax);
-    wsum += w;
+        for (int i = 0; i < 8; ++i) acc[i] *= sc;
+        mmax = mc.x;
+      }
+      const float w = mc.y * fast_exp2(mc.x - mmax);
+      wsum += w;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc[2 * e] += w * __builtin_bit_cast(float, pv[e] << 16);
-      acc[2 * e + 1] += w * __builtin_bit_cast(float, pv[e] & 0xffff0000u);
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] += w * __builtin_bit_cast(float, pv[e] << 16);
+        acc[2 * e + 1] += w * __builtin_bit_cast(float, pv[e] & 0xffff0000u);
+      }
     }
+  }
+  if (cg > 0) {
+    mypart[cg - 1][0][lane] = mmax;
+    mypart[cg - 1][1][lane] = wsum;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mypart[cg - 1][2 + i][lane] = acc[i];
+  }
+  __syncthreads();
+  if (cg > 0 || !valid) return;
+  for (int q = 0; q < CG - 1; ++q) {
+    const float m2 = mypart[q][0][lane], w2 = mypart[q][1][lane];
+    if (!(w2 > 0.f)) continue;
+    const float mn = fmaxf(mmax, m2);
+    const float s1 = fast_exp2(mmax - mn), s2 = fast_exp2(m2 - mn);   // s1 = 0 if mmax = -inf
+    wsum = wsum * s1 + w2 * s2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * s1 + mypart[q][2 + i][lane] * s2;
+    mmax = mn;
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
   const int h0 = kh * a.group + hg * HP;
@@ -507,10 +536,13 @@ void launch_fwd(const FwdArgs &a, int nblocks, hipStream_t stream) {
   hipLaunchKernelGGL((keybias_fwd_kernel<NW, HP, CAUSAL, HAS_BIAS, VARLEN>), dim3(nblocks), dim3(64 * NW), 0,
                      stream, a);
   if (a.heavy_blocks > 0) {
-    const int64_t threads = a.heavy_blocks / a.ns * NW * 8 * 64;
-    hipLaunchKernelGGL((keybias_fwd_combine_kernel<NW, HP, VARLEN>),
-                       dim3((unsigned)((threads + kCombineThreads - 1) / kCombineThreads)), dim3(kCombineThreads), 0,
-                       stream, a);
+    // chunk groups: up to 8, and at least two chunks per group; CG workgroups of 512 threads per
+    // (split tile, forward wave)
+    int cgroups = 1;
+    while (cgroups < kCombineMaxGroups && 2 * cgroups * 2 <= a.ns) cgroups *= 2;
+    const int64_t blocks = a.heavy_blocks / a.ns * NW * cgroups;
+    hipLaunchKernelGGL((keybias_fwd_combine_kernel<NW, HP, VARLEN>), dim3((unsigned)blocks), dim3(512), 0, stream, a,
+                       cgroups);
   }
 }
 
