@@ -10,13 +10,14 @@
 //   1. preprocess: D = rowsum(dO * O) (returned as softmax_d, like FA2);
 //   2. dQ kernel, query-parallel (same 8-wave / 32-column structure as the forward): per 64-key
 //      tile recompute S^T = K Q^T and dP^T = V dO^T, form dS^T, accumulate dQ^T += K^T dS^T;
-//   3. dK/dV/dBias kernel, key-parallel: each wave owns 32 keys (K^T and V^T resident in
+//   3. dK/dV/dBias kernel, key-parallel: each wave owns 16 keys (K^T and V^T resident in
 //      registers) of one KV head and loops over every query head of its GQA group and every
 //      32-query tile: S = Q K^T, dP = dO V^T, P, dS, dV^T += dO^T P, dK^T += Q^T dS, and the dBias
 //      column sums stay in registers (one scalar per lane per head).
-// Tiles that are read both row-major (MFMA A operand, sigma-permuted rows) and transposed
-// (ds_read_b64_tr_b16) are stored in natural row order with the swizzle dual_swz(), which is
-// bank-conflict free for both access patterns.
+// Tiles that are read both row-major (MFMA A operand, permuted rows) and transposed
+// (ds_read_b64_tr_b16) are stored in natural row order with a chunk swizzle (dual_swz() for the
+// dQ kernel's K tile, k16_swz() for the dK/dV kernel's Q / dO tiles) chosen so that both access
+// patterns are bank-conflict free.
 #include <type_traits>
 
 #include "tg_common.h"
@@ -300,15 +301,33 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
 }
 
 // ---- 3. dK / dV / dBias kernel -----------------------------------------------------------
-constexpr int kKWaves = 4;
-constexpr int kKThreads = 64 * kKWaves;
-constexpr int kKBlock = 32 * kKWaves;   // keys per workgroup
+constexpr int kKBlock = 128;            // keys per workgroup
 constexpr int kQT = 32;                 // queries per tile
 constexpr int kQTileBytes = kQT * kRow; // 8 KiB
 
+// Eight waves; each owns 16 keys of one KV head and loops over every query head of its GQA group
+// and every 32-query tile, on v_mfma_f32_16x16x32_bf16
+// (lane l: A row l%16 with k = 8(l/16)+j, B column l%16 with the same k, C rows 4(l/16)+i at
+// column l%16).  Per wave: K^T / V^T fragments 2 x 16 VGPRs, dK^T / dV^T accumulators 2 x 32,
+// S / dP 2 x 8, so that eight waves (two per SIMD) fit where the 32-key form holds one per SIMD.
+// Tile rows are read through the row map pi_rb(m) = 8(m/4) + 4rb + m%4, so that the S^T / dP^T
+// accumulators of lane group g hold queries 8g .. 8g+7 — the B operand layout of dV^T += dO^T P
+// and dK^T += Q^T dS — and the Q / dO tiles use the swizzle k16_swz, conflict-free for both the
+// row reads (16 rows x one 16-byte chunk per 16 lanes) and the transposing reads (8 rows x 32 B
+// per 32 lanes).
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ uint32_t k16_swz(int row) {
+  const int a = row >> 3, b = row & 3;
+  return (uint32_t)(8 * (a & 1) + 2 * b + (a >> 1));
+}
+constexpr int kK16Waves = 8;
+constexpr int kK16Threads = 64 * kK16Waves;
+static_assert(16 * kK16Waves == kKBlock, "eight waves of 16 keys");
+
 template <bool CAUSAL, bool HAS_BIAS, bool VARLEN>
-__global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
-  // one __shared__ object per ring slot: Q / dO natural rows with dual_swz, lse (natural log), D
+__global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char qs0[kQTileBytes], qs1[kQTileBytes];
   __shared__ __attribute__((aligned(1024))) char dos0[kQTileBytes], dos1[kQTileBytes];
   __shared__ __attribute__((aligned(128))) float ls0[kQT], ls1[kQT];
@@ -318,11 +337,10 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
   auto lslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return ls0; else return ls1; };
   auto dslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return dsh0; else return dsh1; };
 
-  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
-  // heaviest first: under the causal mask the first key tiles see the most queries
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int kh = blockIdx.x % a.hkv;
   const int rest = blockIdx.x / a.hkv;
-  const int b = VARLEN ? rest / a.n_tiles : rest % a.batch;   // varlen: sequence-major
+  const int b = VARLEN ? rest / a.n_tiles : rest % a.batch;
   const int kt = VARLEN ? rest % a.n_tiles : rest / a.batch;
   const Seq sq_ = seq_of<VARLEN>(a, b);
   const int sq = sq_.sq, sk = sq_.sk;
@@ -330,45 +348,44 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
   const int n0 = kt * kKBlock;
   if (n0 >= sk) return;
   const int off = sk - sq;
-  const int kw0 = n0 + 32 * wave;
-  const int key = kw0 + lq;              // this lane's key (MFMA column)
+  const int kw0 = n0 + 16 * wave;
+  const int key = kw0 + l16;             // this lane's key (MFMA column)
   const bool kvalid = key < sk;
   const bool wave_has_keys = kw0 < sk;
 
   const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
   const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
-  bf16x8 kf[8], vf[8];
+  bf16x8 kf[4], vf[4];   // B operands: K^T / V^T rows d = 32ks + 8g .. +7 of this lane's key
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    kf[s] = __builtin_bit_cast(bf16x8, gload16(kbase + (int64_t)key * a.k_rs + 16 * s + 8 * g, kvalid));
-    vf[s] = __builtin_bit_cast(bf16x8, gload16(vbase + (int64_t)key * a.v_rs + 16 * s + 8 * g, kvalid));
+  for (int ks = 0; ks < 4; ++ks) {
+    kf[ks] = __builtin_bit_cast(bf16x8, gload16(kbase + (int64_t)key * a.k_rs + 32 * ks + 8 * g, kvalid));
+    vf[ks] = __builtin_bit_cast(bf16x8, gload16(vbase + (int64_t)key * a.v_rs + 32 * ks + 8 * g, kvalid));
   }
 
-  // first query tile that sees any of this workgroup's keys
   int m_start = 0;
   if constexpr (CAUSAL) m_start = max(0, n0 - off) / kQT * kQT;
   const int n_qt = sq > m_start ? (sq - m_start + kQT - 1) / kQT : 0;
 
-  const int qrow_l = (wave * 2) * 4 + (lane >> 4);   // rows written by this lane's two DMA slots:
-  uint32_t qoff[2], dooff[2];                          // wave w covers rows 8w .. 8w+7
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int row = qrow_l + 4 * it;
-    const uint32_t c16 = ((uint32_t)(lane & 15) ^ dual_swz(row)) << 4;
-    qoff[it] = (uint32_t)(row * a.q_rs * 2) + c16;
-    dooff[it] = (uint32_t)(row * a.do_rs * 2) + c16;
-  }
+  // LDS DMA: wave w fills rows 4w .. 4w+3 of the Q and dO tiles (one 1 KB load each)
+  const int drow = 4 * wave + (lane >> 4);
+  const uint32_t dchunk = ((uint32_t)(lane & 15) ^ k16_swz(drow)) << 4;
+  const uint32_t qoff = (uint32_t)(drow * a.q_rs * 2) + dchunk;
+  const uint32_t dooff = (uint32_t)(drow * a.do_rs * 2) + dchunk;
 
-  const int r16 = lane & 15;
-  const int tr_row = r16 >> 2;
-  const int tr_c = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
-  const uint32_t tr_half = (uint32_t)((r16 & 1) * 8);
+  // row-read addresses (A operands of S and dP): row pi_rb(l16), logical chunk 4ks + g
+  uint32_t ra[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) ra[rb] = (uint32_t)(8 * (l16 >> 2) + 4 * rb + (l16 & 3));
+  // transposing-read addresses (A operands of dV^T / dK^T): lane 4k+m of group g supplies row
+  // 8g + k (+4 for the second read), bytes 32 dblk + 8m
+  const int tk = l16 >> 2, tm = l16 & 3;
+  const int trow0 = 8 * g + tk, trow1 = trow0 + 4;
 
-  f32x16 dkacc[4], dvacc[4];
+  f32x4 dkacc[8], dvacc[8];
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
+  for (int d = 0; d < 8; ++d)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) { dkacc[d][v] = 0.f; dvacc[d][v] = 0.f; }
+    for (int v = 0; v < 4; ++v) { dkacc[d][v] = 0.f; dvacc[d][v] = 0.f; }
 
   for (int hi = 0; hi < a.group; ++hi) {
     const int hh = kh * a.group + hi;
@@ -385,16 +402,12 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
     float dbacc = 0.f;
 
     auto issue_tile = [&](int m0, auto buf_c) {
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        dma16(qrs, qslot(buf_c) + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff[it]);
-        dma16(dors, doslot(buf_c) + (wave * 2 + it) * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff[it]);
-      }
+      dma16(qrs, qslot(buf_c) + wave * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff);
+      dma16(dors, doslot(buf_c) + wave * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff);
       if (wave == 0 && lane < kQT) dma4(lrs, lslot(buf_c), (uint32_t)(m0 + lane) * 4);
       if (wave == 1 && lane < kQT) dma4(drs, dslot(buf_c), (uint32_t)(m0 + lane) * 4);
     };
 
-    // two-slot ring unrolled by two (compile-time slots), as in the dQ kernel
     auto tile_step = [&](int t, auto buf_c) {
       constexpr int BUF = decltype(buf_c)::value;
       const int m0 = m_start + t * kQT;
@@ -403,68 +416,85 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (t + 1 < n_qt) issue_tile(m0 + kQT, std::integral_constant<int, 1 - BUF>());
       if (!wave_has_keys || (CAUSAL && m0 + kQT - 1 + off < kw0)) return;
 
-      // S = Q K^T and dP = dO V^T: A operands are sigma rows of the Q / dO tiles
-      f32x16 sacc, pacc;
+      // S = Q K^T and dP = dO V^T for queries m0 + pi_rb(row), this lane's key
+      f32x4 sacc[2], pacc[2];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) { sacc[v] = 0.f; pacc[v] = 0.f; }
-      const int srow = sigma(lq);
+      for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const uint32_t o16 = srow * kRow + (((uint32_t)(2 * s + g) ^ dual_swz(srow)) << 4);
-        sacc = mfma32(lds_load16(qslot(buf_c), o16), kf[s], sacc);
-        pacc = mfma32(lds_load16(doslot(buf_c), o16), vf[s], pacc);
+        for (int v = 0; v < 4; ++v) { sacc[rb][v] = 0.f; pacc[rb][v] = 0.f; }
+#pragma unroll
+      for (int k2 = 0; k2 < 4; k2 += 2) {
+        bf16x8 qa[2][2], da[2][2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            const uint32_t o16 = ra[rb] * kRow + (((uint32_t)(4 * (k2 + e) + g) ^ k16_swz((int)ra[rb])) << 4);
+            qa[e][rb] = lds_load16(qslot(buf_c), o16);
+            da[e][rb] = lds_load16(doslot(buf_c), o16);
+          }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            sacc[rb] = mfma16(qa[e][rb], kf[k2 + e], sacc[rb]);
+            pacc[rb] = mfma16(da[e][rb], vf[k2 + e], pacc[rb]);
+          }
       }
-      // rows of the accumulators: queries m0 + 16g + v
-      const f32x4 *lp = reinterpret_cast<const f32x4 *>(lslot(buf_c) + 16 * g);
-      const f32x4 *dp = reinterpret_cast<const f32x4 *>(dslot(buf_c) + 16 * g);
-      const bool need_mask = (m0 + kQT > sq) || (kw0 + 32 > sk) || (CAUSAL && kw0 + 31 > m0 + off);
-      uint32_t pk[8], dk8[8];
+      // accumulator value i of row block rb is query m0 + 8g + 4rb + i
+      const bool need_mask = (m0 + kQT > sq) || (kw0 + 16 > sk) || (CAUSAL && kw0 + 15 > m0 + off);
+      uint32_t pk[4], dk4[4];
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const f32x4 l4 = lp[i4], d4 = dp[i4];
+      for (int rb = 0; rb < 2; ++rb) {
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lslot(buf_c) + 8 * g + 4 * rb);
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dslot(buf_c) + 8 * g + 4 * rb);
         float p[4], ds[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int v = 4 * i4 + e;
-          float z = sacc[v];
+        for (int i = 0; i < 4; ++i) {
+          float z = sacc[rb][i];
           if constexpr (HAS_BIAS) z += bk;
-          p[e] = fast_exp2(fmaf(z, a.scale_log2, -l4[e] * kLog2e));
+          p[i] = fast_exp2(fmaf(z, a.scale_log2, -l4[i] * kLog2e));
           if (need_mask) {
-            const int qi = m0 + 16 * g + v;
+            const int qi = m0 + 8 * g + 4 * rb + i;
             bool masked = qi >= sq || !kvalid;
             if constexpr (CAUSAL) masked = masked || (key > qi + off);
-            p[e] = masked ? 0.f : p[e];
+            p[i] = masked ? 0.f : p[i];
           }
-          ds[e] = p[e] * (pacc[v] - d4[e]);
-          dbacc += ds[e];
+          ds[i] = p[i] * (pacc[rb][i] - d4[i]);
+          dbacc += ds[i];
         }
-        pk[2 * i4] = pack_bf16x2(p[0], p[1]);
-        pk[2 * i4 + 1] = pack_bf16x2(p[2], p[3]);
-        dk8[2 * i4] = pack_bf16x2(ds[0], ds[1]);
-        dk8[2 * i4 + 1] = pack_bf16x2(ds[2], ds[3]);
+        pk[2 * rb] = pack_bf16x2(p[0], p[1]);
+        pk[2 * rb + 1] = pack_bf16x2(p[2], p[3]);
+        dk4[2 * rb] = pack_bf16x2(ds[0], ds[1]);
+        dk4[2 * rb + 1] = pack_bf16x2(ds[2], ds[3]);
       }
-      // dV^T += dO^T P and dK^T += Q^T dS (A operands: transposed reads of the dO / Q tiles)
+      const bf16x8 pop = __builtin_bit_cast(bf16x8, u32x4{pk[0], pk[1], pk[2], pk[3]});
+      const bf16x8 dop = __builtin_bit_cast(bf16x8, u32x4{dk4[0], dk4[1], dk4[2], dk4[3]});
+      // dV^T += dO^T P and dK^T += Q^T dS: A rows d = 16 dblk + l16, k = queries 8g .. 8g+7;
+      // the transposed reads of four d-blocks are issued ahead of their eight MFMAs
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 wp = {pk[4 * s], pk[4 * s + 1], pk[4 * s + 2], pk[4 * s + 3]};
-        const u32x4 wd = {dk8[4 * s], dk8[4 * s + 1], dk8[4 * s + 2], dk8[4 * s + 3]};
-        const bf16x8 pop = __builtin_bit_cast(bf16x8, wp);
-        const bf16x8 dop = __builtin_bit_cast(bf16x8, wd);
-        const int q0r = 16 * g + 8 * s;
+      for (int d4 = 0; d4 < 8; d4 += 4) {
+        bf16x8 dot_[4], qt_[4];
 #pragma unroll
-        for (int dblk = 0; dblk < 4; ++dblk) {
-          const int c = 4 * dblk + tr_c;
-          const int r0 = q0r + tr_row, r1 = q0r + 4 + tr_row;
-          const uint32_t o0 = r0 * kRow + (((uint32_t)c ^ dual_swz(r0)) << 4) + tr_half;
-          const uint32_t o1 = r1 * kRow + (((uint32_t)c ^ dual_swz(r1)) << 4) + tr_half;
-          const bf16x8 dot_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(doslot(buf_c) + o0),
-                                                                                 lds_read_tr16(doslot(buf_c) + o1),
-                                                                                 0, 1, 2, 3, 4, 5, 6, 7));
-          dvacc[dblk] = mfma32(dot_, pop, dvacc[dblk]);
-          const bf16x8 qt_ = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qslot(buf_c) + o0),
-                                                                                lds_read_tr16(qslot(buf_c) + o1),
-                                                                                0, 1, 2, 3, 4, 5, 6, 7));
-          dkacc[dblk] = mfma32(qt_, dop, dkacc[dblk]);
+        for (int e = 0; e < 4; ++e) {
+          const int dblk = d4 + e;
+          const int c = 2 * dblk + (tm >> 1);
+          const uint32_t hb = (uint32_t)((tm & 1) * 8);
+          const uint32_t o0 = trow0 * kRow + (((uint32_t)c ^ k16_swz(trow0)) << 4) + hb;
+          const uint32_t o1 = trow1 * kRow + (((uint32_t)c ^ k16_swz(trow1)) << 4) + hb;
+          dot_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(doslot(buf_c) + o0),
+                                                                       lds_read_tr16(doslot(buf_c) + o1),
+                                                                       0, 1, 2, 3, 4, 5, 6, 7));
+          qt_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qslot(buf_c) + o0),
+                                                                      lds_read_tr16(qslot(buf_c) + o1),
+                                                                      0, 1, 2, 3, 4, 5, 6, 7));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dvacc[d4 + e] = mfma16(dot_[e], pop, dvacc[d4 + e]);
+          dkacc[d4 + e] = mfma16(qt_[e], dop, dkacc[d4 + e]);
         }
       }
     };
@@ -479,7 +509,8 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
       if (t < n_qt) tile_step(t, std::integral_constant<int, 0>());
     }
     if constexpr (HAS_BIAS) {
-      const float tot = pair_sum(dbacc);
+      float tot = dbacc + __shfl_xor(dbacc, 16);
+      tot += __shfl_xor(tot, 32);
       if (g == 0 && kvalid)
         a.dbias[(int64_t)b * a.dbias_bs + (int64_t)hh * a.dbias_hs + key] = tot * a.scale;
     }
@@ -488,17 +519,14 @@ __global__ __launch_bounds__(kKThreads, 1) void bwd_dkdv_kernel(BwdArgs a) {
     bf16_t *krow = a.dk + (VARLEN ? row0 * a.dk_rs : (int64_t)b * a.dk_bs) + (int64_t)key * a.dk_rs + (int64_t)kh * a.dk_hs;
     bf16_t *vrow = a.dv + (VARLEN ? row0 * a.dv_rs : (int64_t)b * a.dv_bs) + (int64_t)key * a.dv_rs + (int64_t)kh * a.dv_hs;
 #pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d = 32 * dblk + 8 * a4 + 4 * g;
-        const u32x2 wk = {pack_bf16x2(dkacc[dblk][4 * a4] * a.scale, dkacc[dblk][4 * a4 + 1] * a.scale),
-                          pack_bf16x2(dkacc[dblk][4 * a4 + 2] * a.scale, dkacc[dblk][4 * a4 + 3] * a.scale)};
-        const u32x2 wv = {pack_bf16x2(dvacc[dblk][4 * a4], dvacc[dblk][4 * a4 + 1]),
-                          pack_bf16x2(dvacc[dblk][4 * a4 + 2], dvacc[dblk][4 * a4 + 3])};
-        *reinterpret_cast<u32x2 *>(krow + d) = wk;
-        *reinterpret_cast<u32x2 *>(vrow + d) = wv;
-      }
+    for (int dblk = 0; dblk < 8; ++dblk) {
+      const int d = 16 * dblk + 4 * g;   // accumulator value i is d + i
+      const u32x2 wk = {pack_bf16x2(dkacc[dblk][0] * a.scale, dkacc[dblk][1] * a.scale),
+                        pack_bf16x2(dkacc[dblk][2] * a.scale, dkacc[dblk][3] * a.scale)};
+      const u32x2 wv = {pack_bf16x2(dvacc[dblk][0], dvacc[dblk][1]), pack_bf16x2(dvacc[dblk][2], dvacc[dblk][3])};
+      *reinterpret_cast<u32x2 *>(krow + d) = wk;
+      *reinterpret_cast<u32x2 *>(vrow + d) = wv;
+    }
   }
 }
 
@@ -523,7 +551,7 @@ void launch_bwd(const BwdArgs &a0, bool causal, bool has_bias, int64_t nrows, hi
   const unsigned nk = (unsigned)((int64_t)nkt * a.batch * a.hkv);
 #define TG_DKV(C, B)                                                                                   \
   if (causal == C && has_bias == B)                                                                    \
-    hipLaunchKernelGGL((bwd_dkdv_kernel<C, B, VARLEN>), dim3(nk), dim3(kKThreads), 0, st, a);
+    hipLaunchKernelGGL((bwd_dkdv16_kernel<C, B, VARLEN>), dim3(nk), dim3(kK16Threads), 0, st, a);
   TG_DKV(true, true) TG_DKV(true, false) TG_DKV(false, true) TG_DKV(false, false)
 #undef TG_DKV
 }
