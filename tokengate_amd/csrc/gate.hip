@@ -732,37 +732,53 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
     s_pos[tid] = pos;
     s_seq[tid] = sb;
   }
+  // stream descriptors in LDS (indexed per lane below) and each stream's first 16-byte unit
+  // within a row's units, all streams back to back
+  __shared__ tg_pack_stream sst[kMaxStreams];
+  __shared__ int upre[kMaxStreams + 1];
+  if (tid < a.n_streams) sst[tid] = a.st[tid];
+  if (tid == 0) {
+    int acc = 0;
+    for (int si = 0; si < a.n_streams; ++si) {
+      upre[si] = acc;
+      acc += (a.st[si].chunk_bytes >> 4) * a.st[si].n_chunks;
+    }
+    upre[a.n_streams] = acc;
+  }
   __syncthreads();
-  for (int si = 0; si < a.n_streams; ++si) {
-    const tg_pack_stream st = a.st[si];
-    const int units_per_chunk = st.chunk_bytes >> 4;
-    const int units = units_per_chunk * st.n_chunks;
-    const int total = units * kPRows;
-    // four independent 16-byte loads in flight per thread before their stores
-    for (int w0 = tid; w0 < total; w0 += 4 * kPThreads) {
-      u32x4 v[4];
-      char *dst[4];
+  // every 16-byte unit of every stream of the workgroup's rows, flattened; each thread issues the
+  // loads of up to kPBatch units before their stores, so that a row's streams are in flight
+  // together instead of one stream's latency after another
+  constexpr int kPBatch = 8;
+  const int U = upre[a.n_streams];
+  const int total = U * kPRows;
+  for (int w0 = tid; w0 < total; w0 += kPBatch * kPThreads) {
+    u32x4 v[kPBatch];
+    char *dst[kPBatch];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int w = w0 + k * kPThreads;
-        dst[k] = nullptr;
-        if (w < total) {
-          const int rr = w / units, u = w % units;
-          const int64_t srow = src_row[rr];
-          if (srow >= 0) {
-            const int ch = u / units_per_chunk, cu = u % units_per_chunk;
-            const char *src = static_cast<const char *>(st.src) + srow * st.src_row_stride +
-                              (int64_t)ch * st.src_chunk_stride + 16 * cu;
-            v[k] = *reinterpret_cast<const u32x4 *>(src);
-            dst[k] = static_cast<char *>(st.dst) + (j0 + rr) * st.dst_row_stride + (int64_t)ch * st.chunk_bytes +
-                     16 * cu;
-          }
+    for (int k = 0; k < kPBatch; ++k) {
+      const int w = w0 + k * kPThreads;
+      dst[k] = nullptr;
+      if (w < total) {
+        const int rr = w / U, uu = w % U;
+        const int64_t srow = src_row[rr];
+        if (srow >= 0) {
+          int si = 0;
+          while (uu >= upre[si + 1]) ++si;
+          const tg_pack_stream &st = sst[si];
+          const int upc = st.chunk_bytes >> 4;
+          const int u = uu - upre[si];
+          const int ch = u / upc, cu = u % upc;
+          const char *src = static_cast<const char *>(st.src) + srow * st.src_row_stride +
+                            (int64_t)ch * st.src_chunk_stride + 16 * cu;
+          v[k] = *reinterpret_cast<const u32x4 *>(src);
+          dst[k] = static_cast<char *>(st.dst) + (j0 + rr) * st.dst_row_stride + (int64_t)ch * st.chunk_bytes + 16 * cu;
         }
       }
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (dst[k]) *reinterpret_cast<u32x4 *>(dst[k]) = v[k];
     }
+#pragma unroll
+    for (int k = 0; k < kPBatch; ++k)
+      if (dst[k]) *reinterpret_cast<u32x4 *>(dst[k]) = v[k];
   }
   // positions and gate bias of the rows (after this thread's share of the copy is issued)
   if (tid >= kPThreads - kPRows) {
