@@ -92,24 +92,27 @@ def test_short_workspace_runs_unsplit(cuda):
     assert torch.equal(out_short, out_none) and torch.equal(lse_short, lse_none)
 
 
-@pytest.mark.parametrize("lens", [[2320], [1000, 0, 600]], ids=["phase2_K2000", "ragged3"])
-def test_varlen_split(cuda, lens):
+@pytest.mark.parametrize("lens,causal,has_bias", [([2320], True, True), ([1000, 0, 600], True, True),
+                                                  ([1000, 0, 600], False, True), ([700, 1500], True, False)],
+                         ids=["phase2_K2000", "ragged3", "ragged3_noncausal", "two_nobias"])
+def test_varlen_split(cuda, lens, causal, has_bias):
     """Varlen launches as Phase 2 makes them at small K: split through the fa2bias shim."""
     g = torch.Generator(device=cuda).manual_seed(sum(lens))
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     total, H, Hkv, D = int(cu[-1]), 16, 8, 128
     maxlen = max(lens)
-    assert _lib.load().tg_keybias_varlen_fwd_workspace_size(len(lens), maxlen, H, Hkv, 1) > 0
+    assert _lib.load().tg_keybias_varlen_fwd_workspace_size(len(lens), maxlen, H, Hkv, int(causal)) > 0
     q = torch.randn(total, H, D, device=cuda, generator=g).to(torch.bfloat16)
     k = torch.randn(total, Hkv, D, device=cuda, generator=g).to(torch.bfloat16)
     v = torch.randn(total, Hkv, D, device=cuda, generator=g).to(torch.bfloat16)
     scale = D ** -0.5
-    bias_raw = (torch.randn(len(lens), H, maxlen, device=cuda, generator=g) / scale).contiguous()
+    bias_raw = (torch.randn(len(lens), H, maxlen, device=cuda, generator=g) / scale).contiguous() if has_bias else None
     from tokengate_amd.fa2bias.keybias import ext
     cu_t = torch.tensor(cu, device=cuda)
     out, lse, _, _ = ext().varlen_fwd(q, k, v, None, cu_t, cu_t, None, None, None, bias_raw, maxlen, maxlen,
-                                      0.0, scale, False, True, -1, -1, 0.0, False, None)
+                                      0.0, scale, False, causal, -1, -1, 0.0, False, None)
     torch.cuda.synchronize()
-    ro, rl = ora.keybias_varlen_fwd(to_np(q), to_np(k), to_np(v), to_np(bias_raw), cu, scale, True)
+    ro, rl = ora.keybias_varlen_fwd(to_np(q), to_np(k), to_np(v), None if bias_raw is None else to_np(bias_raw), cu,
+                                    scale, causal)
     assert_close("varlen split out", to_np(out), ro)
     assert_close("varlen split lse", to_np(lse), rl)
