@@ -215,12 +215,26 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     if (t + 1 < n_tiles) issue_tile(t + 1, buf ^ 1);
     if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
 
-    // S^T = K Q^T and dP^T = V dO^T (A operands: sigma rows of K and V)
+    // S^T = K Q^T and dP^T = V dO^T (A operands: sigma rows of K and V); the S^T accumulators
+    // start from their keys' bias (raw-score units), as in the forward
     f32x16 sacc[2], pacc[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb) {
+      if constexpr (HAS_BIAS) {
+        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
 #pragma unroll
-      for (int v = 0; v < 16; ++v) { sacc[kb][v] = 0.f; pacc[kb][v] = 0.f; }
+        for (int i = 0; i < 4; ++i) {
+          const f32x4 t4 = bp[i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sacc[kb][4 * i + e] = t4[e];
+        }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
+      }
+#pragma unroll
+      for (int v = 0; v < 16; ++v) pacc[kb][v] = 0.f;
+    }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
 #pragma unroll
@@ -237,23 +251,12 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     uint32_t dsk[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      float bb[16];
-      if constexpr (HAS_BIAS) {
-        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x4 t4 = bp[i];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bb[4 * i + e] = t4[e];
-        }
-      }
 #pragma unroll
       for (int v = 0; v < 16; v += 2) {
         float ds2[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          float z = sacc[kb][v + e];
-          if constexpr (HAS_BIAS) z += bb[v + e];
+          const float z = sacc[kb][v + e];
           float p = fast_exp2(fmaf(z, a.scale_log2, -lse2));
           if (need_mask) {
             const int key = n0 + 32 * kb + 16 * g + v + e;
