@@ -33,8 +33,9 @@ namespace {
 
 // ---------------------------------------------------------------------------------------------
 // Scoring head: s = w2 . silu(W1 x + b1) + b2, x in R^2048 (bf16), W1 (256 x 2048) bf16.
-// Workgroup: 4 waves, 128 rows; wave w owns rows 32w..32w+31 and all 256 hidden units
-// (8 column blocks of 32).  K loop over the 2048 inputs in steps of 32 through a 4-deep LDS ring
+// Workgroup: 8 waves, 128 rows; wave w owns rows 32(w%4)..+31 and hidden units 128(w/4)..+127
+// (4 column blocks of 32): two waves per SIMD, the partial w2 dot products of a row's two halves
+// added through LDS at the end.  K loop over the 2048 inputs in steps of 32 through a 4-deep LDS ring
 // (X tile 128 x 32 = 8 KiB, W1 tile 256 x 32 = 16 KiB per stage), unrolled so that every ring slot
 // index is a compile-time constant.  Accumulators are C^T blocks
 // (hidden unit = MFMA row, token = column) so each lane ends with one token's 16 hidden units
@@ -44,7 +45,7 @@ constexpr int kDin = 2048;
 constexpr int kDh = 256;
 constexpr int kSRows = 128;
 constexpr int kSK = 32;
-constexpr int kSThreads = 256;
+constexpr int kSThreads = 512;
 constexpr int kSStages = 4;
 
 struct ScoreArgs {
@@ -77,48 +78,45 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     else return ws3;
   };
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
+  const int rg = wave & 3, hh = wave >> 2;   // row group, hidden half
   const int64_t r0 = (int64_t)blockIdx.x * kSRows;
 
   const int64_t rows_here = min((int64_t)kSRows, a.n_rows - r0);
   const brsrc_t xrs = make_rsrc(a.x + r0 * a.x_rs, (uint32_t)(((rows_here - 1) * a.x_rs + kDin) * 2));
   const brsrc_t wrs = make_rsrc(a.w1, (uint32_t)(kDh * kDin * 2));
-  // DMA slots: X tile = 512 chunks (2 per thread... 256 threads x 16 B = 4 KiB per issue): 2 issues;
-  // W tile = 1024 chunks: 4 issues.  LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).
-  // per-lane source offsets (bytes) within a k step; the step's byte offset is added per issue
-  uint32_t xoff[2], woff[4];
-#pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int slot = (wave * 2 + it) * 64 + lane;        // 0..511
+  // DMA slots: X tile = 512 chunks (one 1 KiB issue per wave), W tile = 1024 chunks (two);
+  // LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).  Per-lane source offsets
+  // (bytes) within a k step; the step's byte offset is added per issue.
+  uint32_t xoff, woff[2];
+  {
+    const int slot = wave * 64 + lane;                   // 0..511
     const int r = slot >> 2, p = slot & 3;
     const int c = p ^ ((r >> 1) & 3);
-    xoff[it] = (uint32_t)((r * a.x_rs + 8 * c) * 2);
+    xoff = (uint32_t)((r * a.x_rs + 8 * c) * 2);
   }
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int slot = (wave * 4 + it) * 64 + lane;        // 0..1023
+  for (int it = 0; it < 2; ++it) {
+    const int slot = (wave * 2 + it) * 64 + lane;        // 0..1023
     const int r = slot >> 2, p = slot & 3;
     const int c = p ^ ((r >> 1) & 3);
     woff[it] = (uint32_t)((r * kDin + 8 * c) * 2);
   }
-  // DMA slots: X tile = 512 chunks (two 1 KiB issues per wave), W tile = 1024 chunks (four);
-  // LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).
   auto issue = [&](int kstep, auto buf_c) {
     const uint32_t k0b = (uint32_t)(kstep * kSK * 2);
     char *xd = xsl(buf_c), *wd = wsl(buf_c);
+    dma16(xrs, xd + wave * 1024, xoff + k0b);
 #pragma unroll
-    for (int it = 0; it < 2; ++it) dma16(xrs, xd + (wave * 2 + it) * 1024, xoff[it] + k0b);
-#pragma unroll
-    for (int it = 0; it < 4; ++it) dma16(wrs, wd + (wave * 4 + it) * 1024, woff[it] + k0b);
+    for (int it = 0; it < 2; ++it) dma16(wrs, wd + (wave * 2 + it) * 1024, woff[it] + k0b);
   };
 
-  f32x16 acc[8];
+  f32x16 acc[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
 
   constexpr int nk = kDin / kSK;
-  constexpr int kOps = 6;   // DMA ops per thread per step (2 X + 4 W)
+  constexpr int kOps = 3;   // DMA ops per thread per step (1 X + 2 W)
   static_assert(nk % kSStages == 0, "the k loop is unrolled by the ring depth");
   // One k step with a compile-time ring slot: reads of slot BUF and the DMA into slot
   // (BUF + kSStages - 1) % kSStages are then provably disjoint, so the compiler does not make the
@@ -130,25 +128,25 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     wait_vm<decltype(waitn_c)::value>();   // step ks resident for this wave
     ring_barrier();                        // ... for every wave; the slot of step ks-1 is free
     if (ks + kSStages - 1 < nk) issue(ks + kSStages - 1, std::integral_constant<int, NXT>());
-    // B operand: X^T column (token) = lane's row 32*wave + lq; k = 16*s + 8g + j
+    // B operand: X^T column (token) = lane's row 32*rg + lq; k = 16*s + 8g + j
     const char *xb_lds = xsl(buf_c), *wb_lds = wsl(buf_c);
-    const int xr = 32 * wave + lq;
-    bf16x8 xb[2], wa[2][8];
+    const int xr = 32 * rg + lq;
+    bf16x8 xb[2], wa[2][4];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int c = 2 * s + g;
       xb[s] = lds_load16(xb_lds, xr * 64 + (((uint32_t)c ^ ((xr >> 1) & 3)) << 4));
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int wr = 32 * j + lq;   // A operand: W1 row (hidden unit)
+      for (int j = 0; j < 4; ++j) {
+        const int wr = 32 * (4 * hh + j) + lq;   // A operand: W1 row (hidden unit)
         wa[s][j] = lds_load16(wb_lds, wr * 64 + (((uint32_t)c ^ ((wr >> 1) & 3)) << 4));
       }
     }
-    __builtin_amdgcn_sched_barrier(0);   // all 18 reads in flight before the first MFMA
+    __builtin_amdgcn_sched_barrier(0);   // all 10 reads in flight before the first MFMA
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = mfma32(wa[s][j], xb[s], acc[j]);
+      for (int j = 0; j < 4; ++j) acc[j] = mfma32(wa[s][j], xb[s], acc[j]);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -170,20 +168,23 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
   step(ks + 1, I1(), W2());
   step(ks + 2, I2(), W1());
   step(ks + 3, I3(), I0());
-  // epilogue: lane holds token (32*wave + lq), hidden units 32j + 8(v/4) + 4g + v%4
+  // epilogue: lane holds token (32*rg + lq), hidden units 32(4hh + j) + 8(v/4) + 4g + v%4
   float part = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int u = 32 * j + 8 * (v >> 2) + 4 * g + (v & 3);
+      const int u = 32 * (4 * hh + j) + 8 * (v >> 2) + 4 * g + (v & 3);
       const float h = acc[j][v] + a.b1[u];
       const float sl = h / (1.f + __expf(-h));
       part = fmaf(sl, a.w2[u], part);
     }
   const float tot = pair_sum(part);
-  const int64_t row = r0 + 32 * wave + lq;
-  if (g == 0 && row < a.n_rows) a.out[row] = tot + a.b2;
+  __shared__ float upper[kSRows];   // the second hidden half's sums, per row
+  if (hh == 1 && g == 0) upper[32 * rg + lq] = tot;
+  __syncthreads();
+  const int64_t row = r0 + 32 * rg + lq;
+  if (hh == 0 && g == 0 && row < a.n_rows) a.out[row] = (tot + upper[32 * rg + lq]) + a.b2;
 }
 
 // ---------------------------------------------------------------------------------------------
