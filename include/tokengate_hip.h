@@ -204,6 +204,14 @@ int tg_silu_mul(const void *gate_up, int64_t gate_up_row_stride, int64_t n_rows,
 int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_stride, int64_t n_rows, int32_t inter,
                            const void *w_row, float *scores, hipStream_t stream);
 
+/* LM head on the rows that produce the next token (1 to 8 rows): out[b, v] = bf16(sum_d x[b, d] *
+ * weight[v, d]) as fp32, accumulated in fp32 — F.linear(x, lm_head).float() on bf16 tensors, as
+ * the reference's first-token / decode step computes the logits (gate_forward.py:1559-1562,
+ * gate_decode.py:227).
+ * weight: (vocab, dim) bf16 row-major (the embedding when tied); dim a multiple of 512. */
+int tg_lm_head(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t vocab,
+               int32_t dim, float *out, int64_t out_row_stride, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

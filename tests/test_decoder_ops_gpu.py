@@ -121,6 +121,28 @@ def test_branch_readout(cuda, rows, inter):
     #                                                       product moves ~1/4 of the rows by an ulp
 
 
+@pytest.mark.parametrize("rows,vocab,dim", [(1, 151936, 2048), (3, 1000, 2048), (8, 4099, 512), (2, 777, 2560)])
+def test_lm_head(cuda, rows, vocab, dim):
+    """The LM head GEMV against the float64 product of the same bf16 inputs rounded to bf16 (what
+    F.linear on bf16 tensors returns): within one bf16 ulp (summation order), bf16 values, and
+    the argmax of each row equal to torch's bf16 F.linear wherever torch's top two differ."""
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows * 7 + vocab)
+    x = _bf(torch.randn(rows, dim + 64, generator=g, device=cuda))[:, :dim]     # padded rows
+    w = _bf(torch.randn(vocab, dim, generator=g, device=cuda) * dim ** -0.5)
+    got = dec.lm_head(x, w)
+    torch.cuda.synchronize()
+    assert got.shape == (rows, vocab) and got.dtype == torch.float32
+    ref = (x.double() @ w.double().t()).to(torch.bfloat16).float()
+    assert torch.equal(got, got.to(torch.bfloat16).float())
+    ulp = torch.finfo(torch.bfloat16).eps * ref.abs().clamp(min=1e-30)
+    assert bool(((got - ref).abs() <= ulp + 1e-6).all())
+    tl = torch.nn.functional.linear(x, w).float()
+    top2 = tl.topk(2, dim=-1).values
+    clear = top2[:, 0] > top2[:, 1]
+    assert torch.equal(got.argmax(-1)[clear], tl.argmax(-1)[clear])
+
+
 def test_decoder_op_errors(cuda):
     from tokengate_amd import decoder as dec
     x = torch.zeros(4, 2050, dtype=torch.bfloat16, device=cuda)

@@ -38,6 +38,7 @@ SIGNATURES = {
     "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp],
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
     "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
+    "tg_lm_head": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,
             "tg_keybias_varlen_fwd_workspace_size": C.c_int64}

@@ -200,6 +200,57 @@ __global__ __launch_bounds__(256) void branch_readout_kernel(const bf16_t *__res
   if (lane == 0) out[row] = (float)(__bf16)acc;
 }
 
+// ---- LM head on a few rows: logits[b, v] = bf16(sum_d x[b, d] * w[v, d]) as fp32 -----------------
+// The vocab projection of the rows that produce the next token (F.linear on bf16 tensors, then
+// .float()).  HBM-bound on the (vocab, dim) weight: each wave owns 4 consecutive vocab rows and
+// issues all their 16-byte loads of a 512-element column chunk before the bf16 pair dot products;
+// the NR input rows are read from L2 alongside.
+constexpr int kLmMaxRows = 8;
+template <int NR>
+__global__ __launch_bounds__(256) void lm_head_kernel(const bf16_t *__restrict__ x, int64_t x_rs,
+                                                      const bf16_t *__restrict__ w, int64_t vocab, int dim,
+                                                      float *__restrict__ out, int64_t out_rs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
+  if (v0 >= vocab) return;
+  float acc[4][NR];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int b = 0; b < NR; ++b) acc[r][b] = 0.f;
+  for (int c = 0; c < dim; c += 512) {
+    u32x4 wv[4], xv[NR];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      wv[r] = u32x4{0u, 0u, 0u, 0u};
+      if (v0 + r < vocab) wv[r] = *reinterpret_cast<const u32x4 *>(w + (v0 + r) * dim + c + 8 * lane);
+    }
+#pragma unroll
+    for (int b = 0; b < NR; ++b) xv[b] = *reinterpret_cast<const u32x4 *>(x + b * x_rs + c + 8 * lane);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int b = 0; b < NR; ++b)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t wd = wv[r][e], xd = xv[b][e];
+          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wd), __builtin_bit_cast(bf16x2, xd),
+                                                      acc[r][b], false);
+        }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int b = 0; b < NR; ++b) acc[r][b] = wave_sum(acc[r][b]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (v0 + r < vocab)
+#pragma unroll
+        for (int b = 0; b < NR; ++b) out[b * out_rs + v0 + r] = (float)(__bf16)acc[r][b];
+  }
+}
+
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
@@ -319,6 +370,29 @@ extern "C" int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_s
   hipLaunchKernelGGL(branch_readout_kernel, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const bf16_t *>(gate_up), gate_up_row_stride, n_rows, inter,
                      static_cast<const bf16_t *>(w_row), scores);
+  TG_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+
+extern "C" int tg_lm_head(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t vocab,
+                          int32_t dim, float *out, int64_t out_row_stride, hipStream_t stream) {
+  clear_error();
+  TG_CHECK(x && weight && out, "lm_head: null pointer");
+  TG_CHECK(n_rows >= 1 && n_rows <= kLmMaxRows, "lm_head: 1 to %d rows (got %d)", kLmMaxRows, n_rows);
+  TG_CHECK(dim > 0 && dim % 512 == 0, "lm_head: dim must be a positive multiple of 512 (got %d)", dim);
+  TG_CHECK(vocab > 0 && x_row_stride % 8 == 0 && x_row_stride >= dim && out_row_stride >= vocab,
+           "lm_head: bad vocab or row strides");
+  TG_CHECK(aligned16(x) && aligned16(weight), "lm_head: x and weight must be 16-byte aligned");
+  const int64_t blocks = (vocab + 15) / 16;
+  TG_CHECK(blocks < (1ll << 31), "lm_head: vocab too large");
+  const bf16_t *xp = static_cast<const bf16_t *>(x);
+  const bf16_t *wp = static_cast<const bf16_t *>(weight);
+#define TG_LM(NR)                                                                                          \
+  if (n_rows == NR)                                                                                        \
+    hipLaunchKernelGGL(lm_head_kernel<NR>, dim3((unsigned)blocks), dim3(256), 0, stream, xp, x_row_stride, wp, \
+                       vocab, dim, out, out_row_stride);
+  TG_LM(1) TG_LM(2) TG_LM(3) TG_LM(4) TG_LM(5) TG_LM(6) TG_LM(7) TG_LM(8)
+#undef TG_LM
   TG_HIP_CHECK(hipGetLastError());
   return 0;
 }

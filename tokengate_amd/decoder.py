@@ -317,8 +317,21 @@ def alloc_kv(shape: DecoderShape, rows: int, device) -> LayerKV:
                    torch.empty(rows, shape.n_kv_heads, shape.head_dim, dtype=torch.bfloat16, device=device))
 
 
+def lm_head(normed: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """F.linear(normed, weight).float() on bf16 tensors: tg_lm_head (HBM-bound GEMV) for up to 8
+    rows, torch's GEMM for larger batches."""
+    n, d = normed.shape
+    if n > 8 or d % 512 != 0 or normed.stride(1) != 1 or weight.stride(1) != 1 or weight.stride(0) != d:
+        return F.linear(normed, weight).float()
+    V = weight.shape[0]
+    out = torch.empty(n, V, dtype=torch.float32, device=normed.device)
+    _lib.call("tg_lm_head", normed.data_ptr(), normed.stride(0), n, weight.data_ptr(), V, d, out.data_ptr(),
+              out.stride(0), _stream(normed))
+    return out
+
+
 def logits_last(wts: DecoderWeights, h: torch.Tensor, last_rows: torch.Tensor) -> torch.Tensor:
     """Final norm + LM head on the given rows only (the rows that produce the next token)."""
     rows = h.index_select(0, last_rows)
     normed = rmsnorm(rows, wts.final_norm, wts.shape.rms_eps)
-    return F.linear(normed, wts.lm_head).float()
+    return lm_head(normed, wts.lm_head)
