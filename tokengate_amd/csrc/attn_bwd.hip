@@ -318,9 +318,6 @@ constexpr int kQTileBytes = kQT * kRow; // 8 KiB
 // and dK^T += Q^T dS — and the Q / dO tiles use the swizzle k16_swz, conflict-free for both the
 // row reads (16 rows x one 16-byte chunk per 16 lanes) and the transposing reads (8 rows x 32 B
 // per 32 lanes).
-__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ uint32_t k16_swz(int row) {
   const int a = row >> 3, b = row & 3;
   return (uint32_t)(8 * (a & 1) + 2 * b + (a >> 1));

@@ -10,18 +10,20 @@
 //   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
 //     size is even) over NW * 32/HP consecutive query positions; every K/V tile it streams
 //     through LDS serves all HP heads;
-//   * each wave owns 32 MFMA columns = HP heads x 32/HP query positions; the KV sequence is
-//     streamed in 64-key tiles by LDS DMA (buffer_load ... lds: no staging registers, zero fill
-//     past Sk), double-buffered, one barrier per tile, the next tile in flight during compute;
-//   * scores are computed transposed, S^T = K Q^T, on v_mfma_f32_32x32x16_bf16: the accumulator
-//     then holds one (head, query) column per lane and 16 keys per lane, so the online-softmax
-//     max and sum are in-lane plus one cross-half exchange;
-//   * K rows are stored in LDS in a permuted order (sigma) chosen so that lane group g of the
-//     S^T accumulator holds 16 CONSECUTIVE keys; the accumulator, rounded to bf16, is then directly
-//     the B operand of O^T = V^T P^T, whose A operand (8 consecutive keys at one d per lane) comes
-//     from row-major V through the transposing LDS read ds_read_b64_tr_b16;
-//   * O^T accumulates per lane for one column, so the per-query rescale is a scalar per lane, and
-//     it is applied lazily (only when the running max grows by more than 2^8);
+//   * each wave owns 32 MFMA columns in two blocks of 16 (the HP = 2 heads, or two halves of 32
+//     query positions); the KV sequence is streamed in 64-key tiles by LDS DMA (buffer_load ...
+//     lds: no staging registers, zero fill past Sk), double-buffered, one barrier per tile, the
+//     next tile in flight during compute;
+//   * scores are computed transposed, S^T = K Q^T, on v_mfma_f32_16x16x32_bf16 (on gfx950 it
+//     sustains ~2.4 PFLOP/s against ~2.0 for the 32x32x16 form): the accumulators then hold
+//     one column per lane and block and 16 of its keys, the other 48 in the lanes l^16, l^32,
+//     l^48, so the online-softmax max is in-lane plus two permlane swaps;
+//   * K rows are stored in LDS in a permuted order (kperm) chosen so that lane group G of a
+//     32-key step's S^T accumulators holds keys 8G .. 8G+7; the accumulators, rounded to bf16, are
+//     then directly the B operand of O^T = V^T P^T, whose A operand (8 consecutive keys at one d
+//     per lane) comes from row-major V through the transposing LDS read ds_read_b64_tr_b16;
+//   * O^T accumulates per lane for one column per block, so the per-query rescale is a scalar per
+//     lane, and it is applied lazily (only when the running max grows by more than 2^8);
 //   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work;
 //     all NW waves share every K/V tile and each issues 1/NW of its LDS DMA.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
@@ -74,9 +76,14 @@ struct FwdArgs {
   float *ws_ml;                // [heavy unit][chunk][wave][64 lanes] x (m, l)
 };
 
-// MFMA row m = 8a + 4g + b (a, b in 0..3) of a 32-key block carries key sigma(m) = 16g + 4a + b,
-// so that lane group g of the S^T accumulator holds keys 16g .. 16g+15 in register order.
-__device__ __forceinline__ int sigma(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
+// LDS row lr of a 64-key tile holds key kperm(lr): within each 32-key step, S^T block kb' (rows
+// 16kb' .. 16kb'+15) row m carries key 8(m/4) + 4kb' + m%4, so that lane group G of the two S^T
+// accumulators of a step holds keys 8G .. 8G+7 of the step — exactly the k range of the B operand
+// (P^T) of O^T += V^T P^T for that step.
+__device__ __forceinline__ int kperm(int lr) {
+  const int m = lr & 15;
+  return 32 * (lr >> 5) + 8 * (m >> 2) + 4 * ((lr >> 4) & 1) + (m & 3);
+}
 
 // Lazy rescaling threshold (log2 units): the running max used for exp2 is raised only when a tile
 // exceeds it by more than this, so P <= 2^8 (exact in bf16's exponent range) and the O rescale
@@ -84,12 +91,15 @@ __device__ __forceinline__ int sigma(int m) { return 16 * ((m >> 2) & 1) + 4 * (
 constexpr float kRescaleTau = 8.0f;
 
 // LDS tile layouts (64 keys x 128 d, 256 B per row, 16-byte chunks):
-//   K: row lr holds key 32*(lr/32) + sigma(lr%32); logical chunk c at physical chunk c ^ (lr%16)
-//      -> the S^T A-operand read (32 consecutive rows, one chunk) is bank-conflict free.
-//   V: row = key (natural order); logical chunk c at physical chunk c ^ 4*(key%4)
-//      -> the transposing reads (4 keys x 64 B per 16-lane group) spread over all banks.
+//   K: row lr holds key kperm(lr); logical chunk c at physical chunk c ^ (lr%16)
+//      -> the S^T A-operand read (16 consecutive rows, one chunk per 16 lanes) is conflict free.
+//   V: row = key (natural order); logical chunk c at physical chunk c ^ vswz(key), vswz moving
+//      32-byte pairs of chunks by (key%4) + 4((key/8)%2), so that the transposing reads of half a
+//      wave (8 keys x the same 32 bytes) fall on 8 different 32-byte bank groups.
 // Both are filled by LDS DMA straight from global memory (no staging registers); keys past Sk
 // read as zero through the buffer descriptor's range check.
+__device__ __forceinline__ int vswz(int key) { return 2 * ((key & 3) | (((key >> 3) & 1) << 2)); }
+
 // v_max3_f32 without the canonicalising v_max the compiler adds in IEEE mode (the inputs are
 // MFMA results or -inf, never signalling NaNs).
 __device__ __forceinline__ float vmax3(float a, float b, float c) {
@@ -97,6 +107,11 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
   return d;
 }
+
+// Column blocks of a wave: block cb (0, 1) is head cb of the workgroup's pair (HP = 2) or query
+// half cb (HP = 1); lane l holds column l%16 of each block.
+template <int HP> __device__ __forceinline__ int col_head(int cb) { return HP == 2 ? cb : 0; }
+template <int HP> __device__ __forceinline__ int col_query(int cb, int c16) { return HP == 2 ? c16 : 16 * cb + c16; }
 
 template <int NW, int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a) {
@@ -119,10 +134,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int lq = lane & 31;      // MFMA column: head lq / QW, query lq % QW
-  const int g = lane >> 5;
-  const int hl = lq / QW;        // this lane's head within the workgroup's HP heads
-  const int ql = lq % QW;
+  const int c16 = lane & 15;     // MFMA column within each 16-column block
+  const int G = lane >> 4;       // lane group: rows 4G .. 4G+3 of every 16x16 accumulator
 
   // ---- which (query tile, sequence, kv head, head pair) this workgroup owns ----
   const int hgroups = a.group / HP;
@@ -179,17 +192,25 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   const brsrc_t brs =
       make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
 
-  // ---- this wave's queries and its Q fragments (B operand of S^T = K Q^T) ----
+  // ---- this wave's queries and its Q fragments (B operand of S^T = K Q^T, 32 d per k-step) ----
   const int qw0 = q0 + wave * QW;
-  const int qrow = qw0 + ql;
-  const bool qvalid = qrow < sq;
+  int qrow[2];
+  bool qvalid[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    qrow[cb] = qw0 + col_query<HP>(cb, c16);
+    qvalid[cb] = qrow[cb] < sq;
+  }
   const bool wave_has_rows = qw0 < sq;
   const int qw_hi = min(qw0 + QW, sq) - 1;
-  bf16x8 qf[8];
+  bf16x8 qf[2][4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
-    qf[s] = __builtin_bit_cast(
-        bf16x8, gload16(qbase + (int64_t)qrow * a.q_rs + (int64_t)hl * a.q_hs + 16 * s + 8 * g, qvalid));
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      qf[cb][ks] = __builtin_bit_cast(
+          bf16x8, gload16(qbase + (int64_t)qrow[cb] * a.q_rs + (int64_t)col_head<HP>(cb) * a.q_hs + 32 * ks + 8 * G,
+                          qvalid[cb]));
 
   int kv_end = sk;
   if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
@@ -210,10 +231,9 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     const int slot = wave + it * kWaves;                  // 1 KB slot = 4 rows
     const int lr = slot * 4 + (lane >> 4);                // K LDS row written by this lane
     const int kc = (lane & 15) ^ (lr & 15);               // logical chunk stored there
-    const int kkey = 32 * (lr >> 5) + sigma(lr & 31);
-    koff[it] = (uint32_t)(kkey * a.k_rs * 2 + kc * 16);
+    koff[it] = (uint32_t)(kperm(lr) * a.k_rs * 2 + kc * 16);
     const int vkey = slot * 4 + (lane >> 4);              // V LDS row (= key) written by this lane
-    const int vc = (lane & 15) ^ (4 * (vkey & 3));
+    const int vc = (lane & 15) ^ vswz(vkey);
     voff[it] = (uint32_t)(vkey * a.v_rs * 2 + vc * 16);
   }
   auto issue_tile = [&](int tile, auto buf_c) {
@@ -231,25 +251,24 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     }
   };
 
-  // V transposed-read addressing: lane l of 16-lane group G reads key K0 + (l%16)/4, 4 d-values
-  // starting at 32*dblk + 16*(G%2) + 4*(l%4).
-  const int r16 = lane & 15;
-  const uint32_t v_rowpart = (uint32_t)((r16 >> 2) * kKRowBytes + (r16 & 1) * 8);
-  const int v_cpart = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
-  const int v_swz = r16 >> 2;
-  // lane part of each d-block's read address (< 1 KB: the mask only tells the compiler so, which
-  // lets it see that these reads stay inside their ring slot and need not wait for DMA elsewhere)
-  uint32_t vch[4];
+  // V transposed reads (A operand of O^T += V^T P^T: d = 16 dblk + l%16, keys 8G .. 8G+7 of a
+  // 32-key step): lane r of group G addresses key 8G + r/4 (+4 for the upper four keys) and the
+  // 8 bytes of d = 16 dblk + 4(r%4) .. +3; the transposing read hands lane r the four keys at
+  // d = 16 dblk + r.  The swizzle vswz(key) depends only on r/4 and G%2 here.  The lane part of
+  // each address is masked to the 8 KB it can reach, which tells the compiler these reads stay
+  // inside their ring slot (and need not wait for DMA into the other one).
+  const int vsw = 2 * ((c16 >> 2) | ((G & 1) << 2));
+  const uint32_t v_lane = (uint32_t)((8 * G + (c16 >> 2)) * kKRowBytes + 16 * ((c16 & 3) >> 1) + 8 * (c16 & 1));
+  uint32_t vch[8];
 #pragma unroll
-  for (int dblk = 0; dblk < 4; ++dblk)
-    vch[dblk] = (v_rowpart + (uint32_t)((4 * (dblk ^ v_swz) + v_cpart) << 4)) & 0x3F8u;
+  for (int dblk = 0; dblk < 8; ++dblk) vch[dblk] = (v_lane + (uint32_t)(((2 * dblk) ^ vsw) << 4)) & 0x1FF8u;
 
-  f32x16 oacc[4];
-  float mrun = -INFINITY, lrun = 0.f;
+  f32x4 oacc[2][8];
+  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.f, 0.f};
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
+  for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) oacc[d][v] = 0.f;
+    for (int d = 0; d < 8; ++d) oacc[cb][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Two-slot ring, unrolled by two so that every slot index is a compile-time constant: tile t
   // lives in slot t % 2; at the top of tile t this wave's DMA for t is complete (nothing later
@@ -263,109 +282,124 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     if (t + 1 < t_hi) issue_tile(t + 1, std::integral_constant<int, 1 - BUF>());
     if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) return;
 
-    // ---- S^T = K Q^T + bias: 2 key blocks x 8 d-steps.  The accumulators start from the bias of
-    // their keys (raw-score units), so the bias add costs no VALU work. ----
-    f32x16 sacc[2];
+    // ---- S^T = K Q^T + bias: 2 column blocks x 4 key blocks x 4 d-steps.  The accumulators start
+    // from the bias of their keys (raw-score units), so the bias add costs no VALU work. ----
+    f32x4 sacc[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      if constexpr (HAS_BIAS) {
-        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bslot(buf_c)[hl][32 * kb + 16 * g]);
+    for (int cb = 0; cb < 2; ++cb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const f32x4 bb = bp[i];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[kb][4 * i + e] = bb[e];
+      for (int kb = 0; kb < 4; ++kb) {
+        if constexpr (HAS_BIAS) {
+          sacc[cb][kb] = *reinterpret_cast<const f32x4 *>(
+              &bslot(buf_c)[col_head<HP>(cb)][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
+        } else {
+          sacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
       }
     }
     // all 16 K fragments of the tile are read before the first MFMA, so LDS latency is paid once
-    bf16x8 kfr[8][2];
+    bf16x8 kfr[4][4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int lr = 32 * kb + lq;
-        kfr[s][kb] = lds_load16(kslot(buf_c), lr * kKRowBytes + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
+      for (int kb = 0; kb < 4; ++kb) {
+        const int lr = 16 * kb + c16;
+        kfr[kb][ks] = lds_load16(kslot(buf_c), lr * kKRowBytes + ((uint32_t)((4 * ks + G) ^ c16) << 4));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) sacc[kb] = mfma32(kfr[s][kb], qf[s], sacc[kb]);
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) sacc[cb][kb] = mfma16(kfr[kb][ks], qf[cb][ks], sacc[cb][kb]);
+      }
     }
 
-    // ---- online softmax: one (head, query) column per lane, 32 keys per lane ----
+    // ---- online softmax: lane holds 16 keys of one column per block; the other 48 keys of that
+    // column sit in lanes l^16, l^32, l^48 ----
     const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
-    f32x16 (&tv)[2] = sacc;
+    if (need_mask) {
+      // key > lim -> -inf by adding 0 or -inf, selected by the sign of lim - key (an arithmetic
+      // shift the compiler cannot turn back into per-element compares, whose 64-bit results would
+      // crowd the scalar registers)
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      if (need_mask) {
-        const int kidx = n0 + 32 * kb + 16 * g;
+      for (int cb = 0; cb < 2; ++cb) {
+        int lim = sk - 1;
+        if constexpr (CAUSAL) lim = min(lim, qrow[cb] + off);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = kidx + v;
-          bool masked = key >= sk;
-          if constexpr (CAUSAL) masked = masked || (key > qrow + off);
-          tv[kb][v] = masked ? -INFINITY : tv[kb][v];
+        for (int kb = 0; kb < 4; ++kb) {
+          const int rel = lim - (n0 + 32 * (kb >> 1) + 8 * G + 4 * (kb & 1));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            int sgn;
+            asm("v_ashrrev_i32 %0, 31, %1" : "=v"(sgn) : "v"(rel - i));   // -1 where key > lim
+            const float pen = __builtin_bit_cast(float, (uint32_t)sgn & 0xFF800000u);
+            sacc[cb][kb][i] += pen;
+          }
         }
       }
     }
-    // tile max as a tree of v_max3 (short dependency chain, no canonicalising maxes)
-    float m11[11];
+    float mx[2];
 #pragma unroll
-    for (int i = 0; i < 10; ++i) {
-      const int e0 = 3 * i, e1 = 3 * i + 1, e2 = 3 * i + 2;
-      m11[i] = vmax3(tv[e0 >> 4][e0 & 15], tv[e1 >> 4][e1 & 15], tv[e2 >> 4][e2 & 15]);
+    for (int cb = 0; cb < 2; ++cb) {
+      const f32x4 *s = sacc[cb];
+      const float m0 = vmax3(s[0][0], s[0][1], s[0][2]), m1 = vmax3(s[0][3], s[1][0], s[1][1]);
+      const float m2 = vmax3(s[1][2], s[1][3], s[2][0]), m3 = vmax3(s[2][1], s[2][2], s[2][3]);
+      const float m4 = vmax3(s[3][0], s[3][1], s[3][2]);
+      const float m = vmax3(vmax3(m0, m1, m2), vmax3(m3, m4, s[3][3]), m0);
+      mx[cb] = quad_swap_max(m) * a.scale_log2;   // tile max in log2 units (-inf if fully masked)
     }
-    m11[10] = vmax3(tv[1][14], tv[1][15], tv[1][15]);
-    float mx = vmax3(vmax3(m11[0], m11[1], m11[2]), vmax3(m11[3], m11[4], m11[5]),
-                     vmax3(vmax3(m11[6], m11[7], m11[8]), m11[9], m11[10]));
-    mx = half_swap_max(mx) * a.scale_log2;   // tile max in log2 units (-inf if fully masked)
-    if (__builtin_amdgcn_ballot_w64(mx > mrun + kRescaleTau) != 0) {
-      const float m_new = fmaxf(mrun, mx);
-      // 0 on the first visible tile; rows that have seen no key yet (m_new = -inf) keep 1.
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(mrun - m_new);
-      mrun = m_new;
-      lrun *= alpha;
+    if (__builtin_amdgcn_ballot_w64(mx[0] > mrun[0] + kRescaleTau || mx[1] > mrun[1] + kRescaleTau) != 0) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d) oacc[d] *= alpha;
+      for (int cb = 0; cb < 2; ++cb) {
+        const float m_new = fmaxf(mrun[cb], mx[cb]);
+        // 0 on the first visible tile; columns that have seen no key yet (m_new = -inf) keep 1.
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(mrun[cb] - m_new);
+        mrun[cb] = m_new;
+        lrun[cb] *= alpha;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) oacc[cb][d] *= alpha;
+      }
     }
-    const float mneg = mrun == -INFINITY ? 0.f : -mrun;
     // P rounded to bf16 pairs; the row sum adds those same bf16 values (v_dot2 with 1.0, one
     // instruction per pair), i.e. exactly the weights the P V product uses.
-    uint32_t pk[2][8];
-    float ps[4] = {0.f, 0.f, 0.f, 0.f};    // four independent partial sums
+    uint32_t pk[2][4][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int cb = 0; cb < 2; ++cb) {
+      const float mneg = mrun[cb] == -INFINITY ? 0.f : -mrun[cb];
+      float ps[2] = {0.f, 0.f};
 #pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        const float p0 = fast_exp2(fmaf(tv[kb][v], a.scale_log2, mneg));
-        const float p1 = fast_exp2(fmaf(tv[kb][v + 1], a.scale_log2, mneg));
-        pk[kb][v >> 1] = pack_bf16x2(p0, p1);
-        ps[(v >> 1) & 3] = sum_bf16x2(pk[kb][v >> 1], ps[(v >> 1) & 3]);
-      }
-    }
-    lrun += (ps[0] + ps[1]) + (ps[2] + ps[3]);
-
-    // ---- O^T += V^T P^T ----
+      for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 w = {pk[kb][4 * s], pk[kb][4 * s + 1], pk[kb][4 * s + 2], pk[kb][4 * s + 3]};
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, w);
-        const uint32_t krow = (uint32_t)((32 * kb + 16 * g + 8 * s) * kKRowBytes);
-#pragma unroll
-        for (int dblk = 0; dblk < 4; ++dblk) {
-          const s16x4 lo = lds_read_tr16(vslot(buf_c) + krow + vch[dblk]);
-          const s16x4 hi = lds_read_tr16(vslot(buf_c) + krow + 4 * kKRowBytes + vch[dblk]);
-          const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          oacc[dblk] = mfma32(vf, pb, oacc[dblk]);
+        for (int i = 0; i < 4; i += 2) {
+          const float p0 = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, mneg));
+          const float p1 = fast_exp2(fmaf(sacc[cb][kb][i + 1], a.scale_log2, mneg));
+          pk[cb][kb][i >> 1] = pack_bf16x2(p0, p1);
+          ps[kb & 1] = sum_bf16x2(pk[cb][kb][i >> 1], ps[kb & 1]);
         }
+      }
+      lrun[cb] += ps[0] + ps[1];
+    }
+
+    // ---- O^T += V^T P^T: 2 key steps x 8 d-blocks x 2 column blocks ----
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      bf16x8 pb[2];
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const u32x4 w = {pk[cb][2 * st][0], pk[cb][2 * st][1], pk[cb][2 * st + 1][0], pk[cb][2 * st + 1][1]};
+        pb[cb] = __builtin_bit_cast(bf16x8, w);
+      }
+      const uint32_t krow = (uint32_t)(32 * st * kKRowBytes);
+#pragma unroll
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        const s16x4 lo = lds_read_tr16(vslot(buf_c) + krow + vch[dblk]);
+        const s16x4 hi = lds_read_tr16(vslot(buf_c) + krow + 4 * kKRowBytes + vch[dblk]);
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) oacc[cb][dblk] = mfma16(vf, pb[cb], oacc[cb][dblk]);
       }
     }
   };
@@ -378,52 +412,62 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   if (t < t_hi) tile_step(t, std::integral_constant<int, 0>());
 
   // ---- epilogue: normalise, write O (bf16) and LSE (natural log) ----
-  const float l = pair_sum(lrun);
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  float l[2], inv[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    l[cb] = quad_sum(lrun[cb]);
+    inv[cb] = l[cb] > 0.f ? 1.f / l[cb] : 0.f;
+  }
   if (chunk >= 0) {
-    // partial result of this key chunk: O / l as bf16 (eight 16-byte pieces per lane, each
-    // piece a coalesced 1 KB wave store) and (running max in log2 units, row sum l)
+    // partial result of this key chunk: O / l as bf16 (piece j = 4 cb + p holds d-blocks 2p and
+    // 2p+1 of column block cb; each piece a coalesced 1 KB wave store) and, per column block,
+    // (running max in log2 units, row sum l)
     const int64_t pw = (hunit * a.ns + chunk) * kWaves + wave;
     u32x4 *po = reinterpret_cast<u32x4 *>(a.ws_o) + pw * (8 * 64) + lane;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const f32x16 &acc = oacc[j >> 1];
-      const int v0 = 8 * (j & 1);
-      const u32x4 w = {pack_bf16x2(acc[v0] * inv, acc[v0 + 1] * inv), pack_bf16x2(acc[v0 + 2] * inv, acc[v0 + 3] * inv),
-                       pack_bf16x2(acc[v0 + 4] * inv, acc[v0 + 5] * inv), pack_bf16x2(acc[v0 + 6] * inv, acc[v0 + 7] * inv)};
+      const int cb = j >> 2, p = j & 3;
+      const f32x4 &o0 = oacc[cb][2 * p], &o1 = oacc[cb][2 * p + 1];
+      const float s = inv[cb];
+      const u32x4 w = {pack_bf16x2(o0[0] * s, o0[1] * s), pack_bf16x2(o0[2] * s, o0[3] * s),
+                       pack_bf16x2(o1[0] * s, o1[1] * s), pack_bf16x2(o1[2] * s, o1[3] * s)};
       po[j * 64] = w;
     }
-    float2 ml;
-    ml.x = mrun;
-    ml.y = l;
-    reinterpret_cast<float2 *>(a.ws_ml)[pw * 64 + lane] = ml;
+    float2 *pml = reinterpret_cast<float2 *>(a.ws_ml) + pw * 128 + lane;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      float2 ml;
+      ml.x = mrun[cb];
+      ml.y = l[cb];
+      pml[cb * 64] = ml;
+    }
     return;
   }
-  if (qvalid) {
-    bf16_t *orow = obase + (int64_t)qrow * a.o_rs + (int64_t)hl * a.o_hs;
 #pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk) {
+  for (int cb = 0; cb < 2; ++cb) {
+    if (!qvalid[cb]) continue;
+    const int hl = col_head<HP>(cb);
+    bf16_t *orow = obase + (int64_t)qrow[cb] * a.o_rs + (int64_t)hl * a.o_hs;
+    const float s = inv[cb];
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d = 32 * dblk + 8 * a4 + 4 * g;
-        const u32x2 w = {pack_bf16x2(oacc[dblk][4 * a4] * inv, oacc[dblk][4 * a4 + 1] * inv),
-                         pack_bf16x2(oacc[dblk][4 * a4 + 2] * inv, oacc[dblk][4 * a4 + 3] * inv)};
-        *reinterpret_cast<u32x2 *>(orow + d) = w;
-      }
+    for (int dblk = 0; dblk < 8; ++dblk) {
+      const f32x4 &o = oacc[cb][dblk];
+      const u32x2 w = {pack_bf16x2(o[0] * s, o[1] * s), pack_bf16x2(o[2] * s, o[3] * s)};
+      *reinterpret_cast<u32x2 *>(orow + 16 * dblk + 4 * G) = w;
     }
-    if (g == 0) {
-      const float lse = l > 0.f ? (mrun + __log2f(l)) * kLn2 : INFINITY;
+    if (G == 0) {
+      const float lse = l[cb] > 0.f ? (mrun[cb] + __log2f(l[cb])) * kLn2 : INFINITY;
       const int hh = h0 + hl;
       if constexpr (VARLEN)
-        a.lse[(int64_t)hh * a.lse_total + row0 + qrow] = lse;
+        a.lse[(int64_t)hh * a.lse_total + row0 + qrow[cb]] = lse;
       else
-        a.lse[((int64_t)b * a.h + hh) * sq + qrow] = lse;
+        a.lse[((int64_t)b * a.h + hh) * sq + qrow[cb]] = lse;
     }
   }
 }
 
 // Merge of the key chunks of every split query tile.  A 512-thread workgroup covers 8 / CG of the
-// eight 16-byte pieces (8 O values of each of the 64 columns of one forward wave) of one split
+// eight 16-byte pieces (8 O values of each of the 64 lanes of one forward wave) of one split
 // tile; per piece, thread (group cg, lane) folds chunks cg, cg + CG, ... of its column and group 0
 // merges the CG partial results through LDS, so that a long chunk list (a decode row over a long
 // cache) is walked CG ways in parallel.
@@ -444,7 +488,9 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
   const int wave = (int)((blockIdx.x / CG) % NW);          // forward wave whose columns these are
   const int64_t hunit = (blockIdx.x / CG) / NW;
   float (*mypart)[10][64] = part + pj * (CG - 1);
-  const int lq = lane & 31, g = lane >> 5, hl = lq / QW, ql = lq % QW;
+  const int c16 = lane & 15, G = lane >> 4;
+  const int cb = j >> 2, p = j & 3;                        // column block, d-block pair of the piece
+  const int hl = col_head<HP>(cb);
   const int per_q = a.hkv * (a.group / HP);
   const int x = (int)(hunit % per_q), r2 = (int)(hunit / per_q);
   const int kh = x % a.hkv, hg = x / a.hkv;
@@ -460,7 +506,7 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
   }
   const int qw0 = qt * BM + wave * QW;
   if (qw0 >= sq) return;   // workgroup-uniform: the forward computed nothing for these rows
-  const int qrow = qw0 + ql;
+  const int qrow = qw0 + col_query<HP>(cb, c16);
   const bool valid = qrow < sq;
 
   const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml);
@@ -473,7 +519,7 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
 #pragma unroll 4
     for (int c = cg; c < a.ns; c += CG) {
       const int64_t pw = pw0 + (int64_t)c * NW;
-      const float2 mc = ml[pw * 64 + lane];
+      const float2 mc = ml[pw * 128 + cb * 64 + lane];
       const u32x4 pv = po[pw * (8 * 64) + j * 64 + lane];
       if (!(mc.y > 0.f)) continue;
       if (mc.x > mmax) {
@@ -514,14 +560,13 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
   const int h0 = kh * a.group + hg * HP;
   bf16_t *orow = a.o + (VARLEN ? row0 * a.o_rs : (int64_t)b * a.o_bs) + (int64_t)qrow * a.o_rs +
                  (int64_t)(h0 + hl) * a.o_hs;
-  // piece j holds accumulator values 8(j%2) .. 8(j%2)+7 of d-block j/2: d = 32 (j/2) + 16 (j%2)
-  // + 4g + {0..3} and the same + 8
-  const int d0 = 32 * (j >> 1) + 16 * (j & 1) + 4 * g;
+  // piece j holds d-blocks 2p and 2p+1 of column block cb: d = 32p + 4G + {0..3} and the same + 16
+  const int d0 = 32 * p + 4 * G;
   const u32x2 w0 = {pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv)};
   const u32x2 w1 = {pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv)};
   *reinterpret_cast<u32x2 *>(orow + d0) = w0;
-  *reinterpret_cast<u32x2 *>(orow + d0 + 8) = w1;
-  if (j == 0 && g == 0) {
+  *reinterpret_cast<u32x2 *>(orow + d0 + 16) = w1;
+  if (p == 0 && G == 0) {
     const float lse = wsum > 0.f ? (mmax + __log2f(wsum)) * kLn2 : INFINITY;
     const int hh = h0 + hl;
     if constexpr (VARLEN)
@@ -603,7 +648,7 @@ struct SplitPlan {
   int ns = 1, n_heavy = 0;
   int64_t heavy_units = 0, bytes = 0;
 };
-constexpr int64_t kPartialBytesPerLane = 8 * 16 + 8;   // O / l as 64 bf16, then (m, l)
+constexpr int64_t kPartialBytesPerLane = 8 * 16 + 2 * 8;   // O / l as 64 bf16, then (m, l) per column block
 SplitPlan plan_split(int nw, int hp, int n_qtiles, int64_t units, int sq, int sk, bool causal) {
   SplitPlan p;
   const int bmq = nw == 8 ? (hp == 2 ? bm<8, 2>() : bm<8, 1>()) : (hp == 2 ? bm<4, 2>() : bm<4, 1>());

@@ -71,6 +71,23 @@ __device__ __forceinline__ float half_swap_max(float x) {
   return fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1]));
 }
 __device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
+// Max over the four 16-lane groups (lanes l, l^16, l^32, l^48): v_permlane16_swap(x, x) returns
+// (rows 0 and 2 in both rows of each pair, rows 1 and 3 likewise), whose max is max(x[l], x[l^16]);
+// then the same across the two halves.
+__device__ __forceinline__ float quad_swap_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
+                                                   false, false);
+  return half_swap_max(fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1])));
+}
+__device__ __forceinline__ float quad_sum(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+// C = A(16x32) * B(32x16) + C on the bf16 matrix cores.  Lane l holds A[l%16][8*(l/16)+j] and
+// B[8*(l/16)+j][l%16] for j=0..7; C value i sits at row 4*(l/16)+i, column l%16.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
 
 // ---- buffer resources and LDS DMA (gfx950) --------------------------------------------------
 typedef __amdgpu_buffer_rsrc_t brsrc_t;
