@@ -73,7 +73,7 @@ struct FwdArgs {
   int ns, n_heavy;
   int64_t heavy_blocks;        // n_heavy * ns * (head groups) * batch: the grid's leading part
   bf16_t *ws_o;                // [heavy unit][chunk][wave][8][64 lanes] x 16 B
-  float *ws_ml;                // [heavy unit][chunk][wave][64 lanes] x (m, l)
+  float *ws_ml;                // [heavy unit][chunk][wave][column block][64 lanes] x (m, l)
 };
 
 // LDS row lr of a 64-key tile holds key kperm(lr): within each 32-key step, S^T block kb' (rows
