@@ -87,6 +87,22 @@ def test_c_abi_rejects_bad_head_dim_without_touching_the_gpu():
     assert rc != 0 and b"divide" in lib.tg_last_error()
 
 
+def test_lm_head_rejects_bad_arguments_without_touching_the_gpu():
+    from tokengate_amd import _lib
+    lib = _lib.load()
+    # (x, x_row_stride, n_rows, weight, vocab, dim, out, out_row_stride, stream); pointers are
+    # never dereferenced: every check fails before a launch
+    cases = [((16, 2048, 0, 16, 1000, 2048, 16, 1000, None), b"rows"),
+             ((16, 2048, 9, 16, 1000, 2048, 16, 1000, None), b"rows"),
+             ((16, 2048, 1, 16, 1000, 2000, 16, 1000, None), b"multiple of 512"),
+             ((16, 1024, 1, 16, 1000, 2048, 16, 1000, None), b"strides"),
+             ((None, 2048, 1, 16, 1000, 2048, 16, 1000, None), b"null"),
+             ((8, 2048, 1, 16, 1000, 2048, 16, 1000, None), b"aligned")]
+    for args, msg in cases:
+        rc = lib.tg_lm_head(*args)
+        assert rc != 0 and msg in lib.tg_last_error(), (args, lib.tg_last_error())
+
+
 def test_fwd_workspace_size_queries():
     """The split workspace is planned only for grids that leave the chip idle, and never for
     invalid sizes; the size queries make no GPU call."""
