@@ -14,10 +14,10 @@
 //      registers) of one KV head and loops over every query head of its GQA group and every
 //      32-query tile: S = Q K^T, dP = dO V^T, P, dS, dV^T += dO^T P, dK^T += Q^T dS, and the dBias
 //      column sums stay in registers (one scalar per lane per head).
-// Tiles that are read both row-major (MFMA A operand, permuted rows) and transposed
-// (ds_read_b64_tr_b16) are stored in natural row order with a chunk swizzle (dual_swz() for the
-// dQ kernel's K tile, k16_swz() for the dK/dV kernel's Q / dO tiles) chosen so that both access
-// patterns are bank-conflict free.
+// Both kernels run on v_mfma_f32_16x16x32_bf16.  Tiles that are read both row-major (MFMA A
+// operand) and transposed (ds_read_b64_tr_b16) use a chunk swizzle chosen so that both access
+// patterns are bank-conflict free (dq_kswz() for the dQ kernel's K tile, k16_swz() for the dK/dV
+// kernel's Q / dO tiles).
 #include <type_traits>
 
 #include "tg_common.h"
@@ -46,11 +46,6 @@ struct BwdArgs {
   float scale, scale_log2;
 };
 
-__device__ __forceinline__ int sigma(int m) { return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3); }
-// Chunk swizzle of a natural-order tile read both row-major (sigma rows) and transposed.
-__device__ __forceinline__ uint32_t dual_swz(int row) {
-  return (uint32_t)(4 * (row & 3) + (((row >> 2) ^ ((row >> 4) << 1)) & 3));
-}
 
 // Sequence geometry shared by the kernels.
 struct Seq {
@@ -115,16 +110,30 @@ constexpr int kBN = 64;                 // keys per tile
 constexpr int kTileBytes = kBN * kRow;  // 16 KiB
 template <int HP> constexpr int dq_bm() { return kQWaves * (32 / HP); }
 
+// dQ kernel tile layouts (16x16x32 MFMAs).  LDS row lr of a 64-key tile holds key dq_perm(lr):
+// within each 32-key step, S^T block kb' row m carries key 8(m/4) + 4kb' + m%4, so that lane group
+// G of a step's S^T / dP^T accumulators holds keys 8G .. 8G+7 — the k range of the B operand
+// (dS^T) of dQ^T += K^T dS^T.  K's chunk swizzle dq_kswz is a bijection of the row's low four bits
+// (conflict-free row reads: 16 rows, one chunk each) that also puts the 8 rows of half a wave's
+// transposing read (rows 4G + r/4) on 8 different 32-byte bank groups.
+__device__ __forceinline__ int dq_perm(int lr) {
+  const int m = lr & 15;
+  return 32 * (lr >> 5) + 8 * (m >> 2) + 4 * ((lr >> 4) & 1) + (m & 3);
+}
+__device__ __forceinline__ uint32_t dq_kswz(int row) { return (uint32_t)(2 * (row & 7) + ((row >> 3) & 1)); }
+
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   constexpr int QW = 32 / HP;
   constexpr int BM = dq_bm<HP>();
-  __shared__ __attribute__((aligned(1024))) char ks[2][kTileBytes];   // natural rows, dual_swz
-  __shared__ __attribute__((aligned(1024))) char vs[2][kTileBytes];   // sigma rows, chunk ^ (row%16)
-  __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN];
+  // K: rows in dq_perm order, chunk ^ dq_kswz(row) (read row-major and transposed);
+  // V: rows in dq_perm order, chunk ^ (row % 16) (read row-major only)
+  __shared__ __attribute__((aligned(1024))) char ks[2][kTileBytes];
+  __shared__ __attribute__((aligned(1024))) char vs[2][kTileBytes];
+  __shared__ __attribute__((aligned(256))) float bs[2][HP][kBN + 4];
 
-  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
-  const int hl = lq / QW, ql = lq % QW;
+  const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
+  const int c16 = lane & 15, G = lane >> 4;
   const int hgroups = a.group / HP;
   const int per_q = a.hkv * hgroups;
   const int x = blockIdx.x % per_q, rest = blockIdx.x / per_q;
@@ -139,7 +148,6 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   if (q0 >= sq) return;
   const int off = sk - sq;
   const int h0 = kh * a.group + hg * HP;
-  const int hh = h0 + hl;
 
   const int64_t qb = VARLEN ? row0 * a.q_rs : (int64_t)b * a.q_bs;
   const int64_t dob = VARLEN ? row0 * a.do_rs : (int64_t)b * a.do_bs;
@@ -151,22 +159,39 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   const brsrc_t brs =
       make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
 
+  // this wave's 32 columns: block cb (0, 1) = head cb (HP = 2) or query half cb (HP = 1), lane l
+  // holding column l % 16 of each block
   const int qw0 = q0 + wave * QW;
-  const int qrow = qw0 + ql;
-  const bool qvalid = qrow < sq;
+  int qrow[2], hh[2];
+  bool qvalid[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    qrow[cb] = qw0 + (HP == 2 ? c16 : 16 * cb + c16);
+    hh[cb] = h0 + (HP == 2 ? cb : 0);
+    qvalid[cb] = qrow[cb] < sq;
+  }
   const bool wave_has_rows = qw0 < sq;
   const int qw_hi = min(qw0 + QW, sq) - 1;
-  bf16x8 qf[8], df[8];
+  // Q and dO fragments (B operands of S^T = K Q^T and dP^T = V dO^T, 32 d per k-step)
+  bf16x8 qf[2][4], df[2][4];
+  float lse2[2], dsum[2];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    qf[s] = __builtin_bit_cast(bf16x8, gload16(a.q + qb + (int64_t)qrow * a.q_rs + (int64_t)hh * a.q_hs + 16 * s + 8 * g, qvalid));
-    df[s] = __builtin_bit_cast(bf16x8, gload16(a.dout + dob + (int64_t)qrow * a.do_rs + (int64_t)hh * a.do_hs + 16 * s + 8 * g, qvalid));
-  }
-  float lse2 = INFINITY, dsum = 0.f;
-  if (qvalid) {
-    const int64_t li = VARLEN ? (int64_t)hh * a.lse_total + row0 + qrow : ((int64_t)b * a.h + hh) * sq + qrow;
-    lse2 = a.lse[li] * kLog2e;
-    dsum = a.softmax_d[li];
+  for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      qf[cb][ks4] = __builtin_bit_cast(bf16x8, gload16(a.q + qb + (int64_t)qrow[cb] * a.q_rs + (int64_t)hh[cb] * a.q_hs +
+                                                           32 * ks4 + 8 * G, qvalid[cb]));
+      df[cb][ks4] = __builtin_bit_cast(bf16x8, gload16(a.dout + dob + (int64_t)qrow[cb] * a.do_rs +
+                                                           (int64_t)hh[cb] * a.do_hs + 32 * ks4 + 8 * G, qvalid[cb]));
+    }
+    lse2[cb] = INFINITY;
+    dsum[cb] = 0.f;
+    if (qvalid[cb]) {
+      const int64_t li = VARLEN ? (int64_t)hh[cb] * a.lse_total + row0 + qrow[cb]
+                                : ((int64_t)b * a.h + hh[cb]) * sq + qrow[cb];
+      lse2[cb] = a.lse[li] * kLog2e;
+      dsum[cb] = a.softmax_d[li];
+    }
   }
 
   int kv_end = sk;
@@ -176,10 +201,10 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   uint32_t koff[2], voff[2];
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
-    const int row = (wave * 2 + it) * 4 + (lane >> 4);
-    koff[it] = (uint32_t)(row * a.k_rs * 2 + (((lane & 15) ^ dual_swz(row)) << 4));
-    const int vkey = 32 * (row >> 5) + sigma(row & 31);
-    voff[it] = (uint32_t)(vkey * a.v_rs * 2 + (((lane & 15) ^ (row & 15)) << 4));
+    const int lr = (wave * 2 + it) * 4 + (lane >> 4);          // LDS row written by this lane
+    const int key = dq_perm(lr);
+    koff[it] = (uint32_t)(key * a.k_rs * 2 + (((lane & 15) ^ dq_kswz(lr)) << 4));
+    voff[it] = (uint32_t)(key * a.v_rs * 2 + (((lane & 15) ^ (lr & 15)) << 4));
   }
   auto issue_tile = [&](int tile, int buf) {
     const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
@@ -194,17 +219,23 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     }
   };
 
-  // transposed K reads (A operand of dQ^T = K^T dS^T)
-  const int r16 = lane & 15;
-  const int tr_row = r16 >> 2;
-  const int tr_c = 2 * ((lane >> 4) & 1) + ((r16 & 3) >> 1);
-  const uint32_t tr_half = (uint32_t)((r16 & 1) * 8);
+  // K^T fragments (A operand of dQ^T += K^T dS^T: d = 16 dblk + l%16, keys 8G .. 8G+7 of a 32-key
+  // step) by transposing reads: lane r of group G addresses the key 8G + r/4 (+4 for the upper
+  // four), i.e. LDS row 32 st + 16 hi + 4G + r/4, and the 8 bytes of d = 16 dblk + 4(r%4) .. +3.
+  // The swizzle dq_kswz depends only on the row's low four bits, so the lane part of every
+  // address is one of eight per-lane values.
+  const int trow = 4 * G + (c16 >> 2);
+  uint32_t ktr[8];
+#pragma unroll
+  for (int dblk = 0; dblk < 8; ++dblk)
+    ktr[dblk] = (uint32_t)(trow * kRow + ((((uint32_t)(2 * dblk + ((c16 & 3) >> 1))) ^ dq_kswz(trow)) << 4) +
+                           8 * (c16 & 1));
 
-  f32x16 dqacc[4];
+  f32x4 dqacc[2][8];
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
+  for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) dqacc[d][v] = 0.f;
+    for (int d = 0; d < 8; ++d) dqacc[cb][d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (n_tiles > 0) issue_tile(0, 0);
   for (int t = 0; t < n_tiles; ++t) {
@@ -215,91 +246,96 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     if (t + 1 < n_tiles) issue_tile(t + 1, buf ^ 1);
     if (!wave_has_rows || (CAUSAL && n0 > qw_hi + off)) continue;
 
-    // S^T = K Q^T and dP^T = V dO^T (A operands: sigma rows of K and V); the S^T accumulators
-    // start from their keys' bias (raw-score units), as in the forward
-    f32x16 sacc[2], pacc[2];
+    // S^T = K Q^T (+ bias, as the accumulators' start) and dP^T = V dO^T: 2 column blocks x 4 key
+    // blocks x 4 d-steps each
+    f32x4 sacc[2][4], pacc[2][4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      if constexpr (HAS_BIAS) {
-        const f32x4 *bp = reinterpret_cast<const f32x4 *>(&bs[buf][hl][32 * kb + 16 * g]);
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        if constexpr (HAS_BIAS)
+          sacc[cb][kb] = *reinterpret_cast<const f32x4 *>(
+              &bs[buf][HP == 2 ? cb : 0][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
+        else
+          sacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        pacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int ks4 = 0; ks4 < 4; ++ks4) {
+      bf16x8 kf[4], vf[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const int lr = 16 * kb + c16;
+        kf[kb] = lds_load16(ks[buf], lr * kRow + ((((uint32_t)(4 * ks4 + G)) ^ dq_kswz(lr)) << 4));
+        vf[kb] = lds_load16(vs[buf], lr * kRow + ((uint32_t)((4 * ks4 + G) ^ c16) << 4));
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          sacc[cb][kb] = mfma16(kf[kb], qf[cb][ks4], sacc[cb][kb]);
+          pacc[cb][kb] = mfma16(vf[kb], df[cb][ks4], pacc[cb][kb]);
+        }
+      }
+    }
+    // dS = P (dP - D), P = exp2(S scale log2e - lse log2e); keys past the end or in the causal
+    // future get P = 0 (a sign mask from lim - key, no per-element compare results in SGPRs)
+    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
+    uint32_t dsk[2][4][2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      int lim = sk - 1;
+      if constexpr (CAUSAL) lim = min(lim, qrow[cb] + off);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const int rel = lim - (n0 + 32 * (kb >> 1) + 8 * G + 4 * (kb & 1));
+        float ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const f32x4 t4 = bp[i];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sacc[kb][4 * i + e] = t4[e];
-        }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sacc[kb][v] = 0.f;
-      }
-#pragma unroll
-      for (int v = 0; v < 16; ++v) pacc[kb][v] = 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const int krow = 32 * kb + sigma(lq);
-        const bf16x8 kf = lds_load16(ks[buf], krow * kRow + (((uint32_t)(2 * s + g) ^ dual_swz(krow)) << 4));
-        sacc[kb] = mfma32(kf, qf[s], sacc[kb]);
-        const int vrow = 32 * kb + lq;
-        const bf16x8 vf = lds_load16(vs[buf], vrow * kRow + ((uint32_t)((2 * s + g) ^ (lq & 15)) << 4));
-        pacc[kb] = mfma32(vf, df[s], pacc[kb]);
-      }
-    }
-    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
-    uint32_t dsk[2][8];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int v = 0; v < 16; v += 2) {
-        float ds2[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-          const float z = sacc[kb][v + e];
-          float p = fast_exp2(fmaf(z, a.scale_log2, -lse2));
+          float p = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, -lse2[cb]));
           if (need_mask) {
-            const int key = n0 + 32 * kb + 16 * g + v + e;
-            bool masked = key >= sk;
-            if constexpr (CAUSAL) masked = masked || (key > qrow + off);
-            p = masked ? 0.f : p;
+            int sgn;
+            asm("v_ashrrev_i32 %0, 31, %1" : "=v"(sgn) : "v"(rel - i));   // -1 where key > lim
+            const uint32_t pbits = __builtin_bit_cast(uint32_t, p) & ~(uint32_t)sgn;
+            p = __builtin_bit_cast(float, pbits);
           }
-          ds2[e] = p * (pacc[kb][v + e] - dsum);
+          ds[i] = p * (pacc[cb][kb][i] - dsum[cb]);
         }
-        dsk[kb][v >> 1] = pack_bf16x2(ds2[0], ds2[1]);
+        dsk[cb][kb][0] = pack_bf16x2(ds[0], ds[1]);
+        dsk[cb][kb][1] = pack_bf16x2(ds[2], ds[3]);
       }
     }
-    // dQ^T += K^T dS^T
+    // dQ^T += K^T dS^T: 2 key steps x 8 d-blocks x 2 column blocks
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int st = 0; st < 2; ++st) {
+      bf16x8 bop[2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 w = {dsk[kb][4 * s], dsk[kb][4 * s + 1], dsk[kb][4 * s + 2], dsk[kb][4 * s + 3]};
-        const bf16x8 bop = __builtin_bit_cast(bf16x8, w);
-        const int k0 = 32 * kb + 16 * g + 8 * s;
+      for (int cb = 0; cb < 2; ++cb) {
+        const u32x4 w = {dsk[cb][2 * st][0], dsk[cb][2 * st][1], dsk[cb][2 * st + 1][0], dsk[cb][2 * st + 1][1]};
+        bop[cb] = __builtin_bit_cast(bf16x8, w);
+      }
 #pragma unroll
-        for (int dblk = 0; dblk < 4; ++dblk) {
-          const int c = 4 * dblk + tr_c;
-          const int r0 = k0 + tr_row, r1 = k0 + 4 + tr_row;
-          const s16x4 lo = lds_read_tr16(ks[buf] + r0 * kRow + (((uint32_t)c ^ dual_swz(r0)) << 4) + tr_half);
-          const s16x4 hi = lds_read_tr16(ks[buf] + r1 * kRow + (((uint32_t)c ^ dual_swz(r1)) << 4) + tr_half);
-          const bf16x8 aop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-          dqacc[dblk] = mfma32(aop, bop, dqacc[dblk]);
-        }
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        const s16x4 lo = lds_read_tr16(ks[buf] + 32 * st * kRow + ktr[dblk]);
+        const s16x4 hi = lds_read_tr16(ks[buf] + (32 * st + 16) * kRow + ktr[dblk]);
+        const bf16x8 aop = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) dqacc[cb][dblk] = mfma16(aop, bop[cb], dqacc[cb][dblk]);
       }
     }
   }
-  if (qvalid) {
-    bf16_t *row = a.dq + (VARLEN ? row0 * a.dq_rs : (int64_t)b * a.dq_bs) + (int64_t)qrow * a.dq_rs + (int64_t)hh * a.dq_hs;
 #pragma unroll
-    for (int dblk = 0; dblk < 4; ++dblk)
+  for (int cb = 0; cb < 2; ++cb) {
+    if (!qvalid[cb]) continue;
+    bf16_t *row = a.dq + (VARLEN ? row0 * a.dq_rs : (int64_t)b * a.dq_bs) + (int64_t)qrow[cb] * a.dq_rs +
+                  (int64_t)hh[cb] * a.dq_hs;
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d = 32 * dblk + 8 * a4 + 4 * g;
-        const u32x2 w = {pack_bf16x2(dqacc[dblk][4 * a4] * a.scale, dqacc[dblk][4 * a4 + 1] * a.scale),
-                         pack_bf16x2(dqacc[dblk][4 * a4 + 2] * a.scale, dqacc[dblk][4 * a4 + 3] * a.scale)};
-        *reinterpret_cast<u32x2 *>(row + d) = w;
-      }
+    for (int dblk = 0; dblk < 8; ++dblk) {
+      const f32x4 &o = dqacc[cb][dblk];
+      const u32x2 w = {pack_bf16x2(o[0] * a.scale, o[1] * a.scale), pack_bf16x2(o[2] * a.scale, o[3] * a.scale)};
+      *reinterpret_cast<u32x2 *>(row + 16 * dblk + 4 * G) = w;
+    }
   }
 }
 
