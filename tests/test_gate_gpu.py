@@ -61,6 +61,29 @@ def test_random_ragged_batch(cuda):
     _check_select(scores_bf, seqs, cuda)
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_selection_sweep(cuda, seed):
+    """Seeded random batches: 1-8 sequences, lengths up to 70k (past the register-resident limit,
+    so the streaming top-K runs too), random state spans (empty ones included) and K (0, 1,
+    keep-all, around the article length), scores normal, bf16-rounded (many ties) or few-valued."""
+    rng = np.random.default_rng(500 + seed)
+    seqs, r0 = [], 0
+    for _ in range(int(rng.integers(1, 9))):
+        L = int(rng.integers(1, 70000)) if rng.random() < 0.2 else int(rng.integers(1, 9000))
+        s = int(rng.integers(0, min(L, 300) + 1))
+        e = int(rng.integers(s, L + 1))
+        K = int(rng.choice([0, 1, 5, 100, 500, 2000, 10_000_000, int(rng.integers(0, e - s + 2))]))
+        seqs.append((r0, L, s, e, K))
+        r0 += L
+    scores = rng.standard_normal(r0).astype(np.float32)
+    kind = int(rng.integers(3))
+    if kind == 1:
+        scores = torch.from_numpy(scores).to(torch.bfloat16).float().numpy()
+    elif kind == 2:
+        scores = np.round(scores * 4).astype(np.float32)
+    _check_select(scores, seqs, cuda)
+
+
 @pytest.mark.parametrize("kind", ["all_equal", "few_values", "nan_and_zeros", "steps", "infinities", "huge_range",
                                   "two_clusters", "tiny_range", "denormals", "negative_only"])
 def test_heavy_ties(cuda, kind):
