@@ -277,6 +277,24 @@ def bench_ttft(dev, reps=5):
     return out
 
 
+def prefill_trace_run(dev, runs=8):
+    """The 32k / K=2000 gated prefill of bench_ttft (same decoder, head and prompt generator), run
+    `runs` times back to back with no other work, for a per-kernel trace of one prefill."""
+    import torch
+    from tokengate_amd import decoder as dec
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    shape = dec.QWEN3_1P7B
+    wts = dec.random_decoder(shape, seed=0, device=dev)
+    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=5, device=dev)
+    g = torch.Generator().manual_seed(7)
+    ids = [torch.randint(0, shape.vocab, (32768,), generator=g).to(dev)]
+    for i in range(runs):
+        P.prefill_batch(wts, head, ids, [64], [32768 - 256], 1, [2000])
+        torch.cuda.synchronize()
+        print(f"prefill {i + 1}/{runs} done", flush=True)
+
+
 def cpu_model() -> str:
     """The host CPU's model name (from /proc/cpuinfo), or 'unknown'."""
     try:
@@ -364,6 +382,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run three plain 1 GiB device copies (counter calibration for HBM bytes)")
+    ap.add_argument("--ttft-only", action="store_true",
+                    help="only run 8 back-to-back gated prefills at 32k / K=2000 (for a kernel trace)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the path is timed on one GPU's share of the work, with no "
@@ -376,6 +396,9 @@ def main():
         sys.exit(1)
     from tokengate_amd.fa2bias import keybias  # noqa: F401  (registers the custom ops)
     dev = torch.device("cuda:0")
+    if args.ttft_only:
+        prefill_trace_run(dev)
+        return
 
     S, H, Hkv = 32768, 16, 8
     q, k, v, bias_raw, scale = make_inputs(S, H, Hkv, 3.0, 2, dev, qkv_scale=1.0 / math.sqrt(128))
