@@ -182,8 +182,9 @@ int tg_rmsnorm(const void *x, int64_t x_row_stride, const void *residual, int64_
  * folded in: per head (attn_scale) and per row (the scaled-softmax ratio r_q, :417-431).
  * qkv rows hold [q heads | k heads | v heads] x head_dim (=128) bf16.  For token t at position
  * positions[t] (int64): angle_i = float(positions[t]) * inv_freq[i] (fp32, i < 64); q head h ->
- * q_out row t (may alias qkv), times q_head_scale[h] and q_row_scale[t] where those are non-NULL;
- * k head g -> k_out row t (the layer's KV cache, (rows, num_heads_k, 128)); v head g copied to
+ * q_out row t (may alias qkv); where q_head_scale / q_row_scale are non-NULL the rotated query,
+ * rounded to bf16, is multiplied by s = bf16(q_head_scale[h] * q_row_scale[t]) (a missing factor
+ * is 1) and rounded again — the reference's bf16 q * s_eff; k head g -> k_out row t (the layer's KV cache, (rows, num_heads_k, 128)); v head g copied to
  * v_out row t. */
 int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const int64_t *positions, int64_t n_tokens,
                     int32_t num_heads, int32_t num_heads_k, int32_t head_dim, const void *q_norm_weight,

@@ -67,13 +67,26 @@ def keybias_fwd(q, k, v, bias_raw, scale, causal=True, rows=None, dtype=np.float
     return out, lse
 
 
-def keybias_bwd(dout, q, k, v, bias_raw, scale, causal=True):
+def keybias_bwd(dout, q, k, v, bias_raw, scale, causal=True, out=None, bf16_operands=False, lse=None):
     """Backward of keybias_fwd.  Returns dq, dk, dv (input shapes), dbias_raw (B,H,Sk) — the
-    gradient with respect to bias_raw, i.e. scale * sum_i dS — and softmax_d (B,H,Sq)."""
+    gradient with respect to bias_raw, i.e. scale * sum_i dS — and softmax_d (B,H,Sq).
+
+    out: the forward output handed to the backward (B,Sq,H,D), as the reference's op receives
+    it (keybias.py:52-63, 66-82: the saved bf16 `out`); D = rowsum(dO * out) then uses it, as
+    FA2's backward does.  Default: the oracle's own float64 forward output.
+    lse: the forward's log-sum-exp handed to the backward (B,H,Sq), likewise an input of the
+    reference's op; P = exp(z - lse) then uses it.  Default: the oracle's own.
+    bf16_operands: round P and dS to bf16 before the products that consume them (dV = P^T dO;
+    dK, dQ from dS), the FlashAttention-2 backward's operand precision (flash-attn 2.8.3
+    flash_bwd_kernel.h, not vendored: the patch context keybias.patch:243-248 forms dS in fp32
+    just before that conversion); dBias and D stay in full precision (keybias.patch:246)."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     G = H // Hkv
-    out, lse = keybias_fwd(q, k, v, bias_raw, scale, causal)
+    o_fwd, lse_fwd = keybias_fwd(q, k, v, bias_raw, scale, causal)
+    o_d = o_fwd if out is None else np.asarray(out, dtype=np.float64)
+    lse = lse_fwd if lse is None else np.asarray(lse, dtype=np.float64)
+    rnd = (lambda x: bf16_round(x).astype(np.float64)) if bf16_operands else (lambda x: x)
     dq = np.zeros(q.shape)
     dk = np.zeros(k.shape)
     dv = np.zeros(v.shape)
@@ -92,13 +105,13 @@ def keybias_bwd(dout, q, k, v, bias_raw, scale, causal=True):
             fin = np.isfinite(lse[b, h])
             p = np.exp(z - np.where(fin, lse[b, h], 0.0)[:, None])
             p[~fin] = 0.0
-            Dv = (do * out[b, :, h]).sum(axis=1)
+            Dv = (do * o_d[b, :, h]).sum(axis=1)
             sd[b, h] = Dv
             dp = do @ vg.T
             ds = p * (dp - Dv[:, None])
-            dq[b, :, h] = scale * ds @ kg
-            dk[b, :, g] += scale * ds.T @ qb
-            dv[b, :, g] += p.T @ do
+            dq[b, :, h] = scale * rnd(ds) @ kg
+            dk[b, :, g] += scale * rnd(ds).T @ qb
+            dv[b, :, g] += rnd(p).T @ do
             dbias[b, h] = scale * ds.sum(axis=0)
     return dq, dk, dv, dbias, sd
 

@@ -50,12 +50,18 @@ def fwd(q, k, v, bias_raw, scale, causal=True, chunk=1024):
     return out, lse
 
 
-def bwd(dout, q, k, v, bias_raw, scale, causal=True, chunk=1024):
-    """Returns dq, dk, dv (float32, input shapes), dbias_raw (B,H,Sk) or None, softmax_d (B,H,Sq)."""
+def bwd(dout, q, k, v, bias_raw, scale, causal=True, chunk=1024, out=None, bf16_operands=False, lse=None):
+    """Returns dq, dk, dv (float32, input shapes), dbias_raw (B,H,Sk) or None, softmax_d (B,H,Sq).
+    out / lse / bf16_operands as in oracle.attention.keybias_bwd: D and P from the forward output
+    and log-sum-exp handed to the backward, P and dS rounded to bf16 before the products that
+    consume them."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     G = H // Hkv
-    out, lse = fwd(q, k, v, bias_raw, scale, causal, chunk)
+    o_fwd, lse_fwd = fwd(q, k, v, bias_raw, scale, causal, chunk)
+    out = o_fwd if out is None else out.float()
+    lse = lse_fwd if lse is None else lse.float()
+    rnd = (lambda x: x.to(torch.bfloat16).float()) if bf16_operands else (lambda x: x)
     dq = torch.zeros(B, Sq, H, D, dtype=torch.float32, device=q.device)
     dk = torch.zeros(B, Sk, Hkv, D, dtype=torch.float32, device=q.device)
     dv = torch.zeros(B, Sk, Hkv, D, dtype=torch.float32, device=q.device)
@@ -78,9 +84,10 @@ def bwd(dout, q, k, v, bias_raw, scale, causal=True, chunk=1024):
                 p = torch.where(fin[:, None], p, torch.zeros_like(p))
                 dp = do[i0:i1] @ vg.t()
                 ds = p * (dp - sd[b, h, i0:i1][:, None])
-                dq[b, i0:i1, h] = scale * (ds @ kg)
-                dk[b, :, g] += scale * (ds.t().contiguous() @ qh[i0:i1])
-                dv[b, :, g] += p.t().contiguous() @ do[i0:i1]
+                dsr = rnd(ds)
+                dq[b, i0:i1, h] = scale * (dsr @ kg)
+                dk[b, :, g] += scale * (dsr.t().contiguous() @ qh[i0:i1])
+                dv[b, :, g] += rnd(p).t().contiguous() @ do[i0:i1]
                 if dbias is not None:
                     dbias[b, h] += scale * ds.sum(0)
     return dq, dk, dv, dbias, sd

@@ -71,14 +71,15 @@ class Weights:
 
 
 def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
-          q_temp: Optional[torch.Tensor] = None, q_row: Optional[torch.Tensor] = None, boundary: Optional[list] = None):
+          q_temp: Optional[torch.Tensor] = None, q_scale: Optional[torch.Tensor] = None,
+          boundary: Optional[list] = None):
     """One decoder layer on a batch x (B, n, d) float32 at positions pos (B, n); bias_logit
-    (B, H, n) per-key logit bias or None; q_temp (H,) per-head temperature or None.  Without
-    q_row the temperature multiplies the query and the bias per head (_phase2_q_bias, attn_scale
-    branch); with q_row (B, n) — the scaled-softmax mode — the query is scaled by
-    q_temp[h] * q_row[b, i] and bias_logit is used as given (the caller folds in
-    mean_h(temperature) * r_k).  Returns (x_out, k, v) with k/v (B, n, Hkv, D) after norm and RoPE;
-    boundary (a list), if given, receives the attention residual a = x + o_proj(attn)."""
+    (B, H, n) per-key logit bias or None.  q_temp (H,): a per-head temperature multiplying the
+    query and the bias (the fp32 form of the per-head branch of _phase2_q_bias); q_scale
+    (B, H, n): a per-(head, row) query multiplier, the bias used as given (the caller passes the
+    reference's bf16 Phase-2 values, phase2_tables).  Returns (x_out, k, v) with k/v
+    (B, n, Hkv, D) after norm and RoPE; boundary (a list), if given, receives the attention
+    residual a = x + o_proj(attn)."""
     s = W.shape
     L = W.layers[i]
     B, n, _ = x.shape
@@ -96,19 +97,39 @@ def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Op
     scale = 1.0 / math.sqrt(D)
     braw = None
     if bias_logit is not None:
-        bl = bias_logit
-        if q_temp is not None and q_row is None:
-            bl = bl * q_temp[None, :, None]
+        bl = bias_logit * q_temp[None, :, None] if q_temp is not None else bias_logit
         braw = bl / scale
     if q_temp is not None:
         q = q * q_temp[None, None, :, None]
-    if q_row is not None:
-        q = q * q_row[:, :, None, None]
+    if q_scale is not None:
+        q = q * q_scale.permute(0, 2, 1)[..., None]
     attn, _ = oat.fwd(q, k, v, braw, scale, causal=True)
     x = x + attn.reshape(B, n, H * D) @ L["wo"].t()
     if boundary is not None:
         boundary.append(x)
     return mlp_half(W, i, x), k, v
+
+
+def phase2_tables(head, scores_art: np.ndarray, keep: np.ndarray, art_start: int, art_end: int):
+    """The reference's Phase-2 constants of one sample (oracle.gate's bf16 chain): per Phase-2
+    layer j, the key bias bias'[j] (H, n_kept) in logit units and the query multiplier
+    s[j] (H, n_kept), both bf16 values as float32 tensors; s is None without a temperature."""
+    gs = head.gate_scale.float().cpu().numpy()
+    b = og.gate_bias_layers(scores_art, gs, gain=float(getattr(head, "bias_gain", 1.0)))
+    gb = og.kept_bias_layers(b, keep, art_start, art_end)                   # (n, L2, H)
+    temp = og.softplus32(head.attn_scale.float().cpu().numpy()) if head.attn_scale is not None else None
+    ssmax = bool(getattr(head, "scaled_softmax", False)) and temp is not None
+    r = og.ssmax_ratio(keep).astype(np.float32) if ssmax else None
+    biases, scales = [], []
+    for j in range(gb.shape[1]):
+        tj = temp[j] if temp is not None else None
+        biases.append(torch.from_numpy(og.phase2_bias(gb[:, j, :], tj, r).T.copy()))
+        if tj is None:
+            scales.append(None)
+        else:
+            sq = og.phase2_query_scale(tj, r)
+            scales.append(torch.from_numpy(np.broadcast_to(sq, (sq.shape[0], len(keep))).copy()))
+    return biases, scales
 
 
 def mlp_half(W: Weights, i: int, a: torch.Tensor) -> torch.Tensor:
@@ -124,12 +145,18 @@ def head_scores(head, h: torch.Tensor) -> np.ndarray:
                         head.w2.cpu().numpy(), head.b2)
 
 
-def branch_scores(head, a: torch.Tensor, ln2: torch.Tensor, eps: float) -> torch.Tensor:
+def branch_scores_f32(head, a: torch.Tensor, ln2: torch.Tensor, eps: float) -> torch.Tensor:
     """The finalized gate's scoring branch on boundary rows a (n, d), float32:
     w_row . (silu(W_gate z) * (W_up z)), z = rms(a) * ln2 (gate_branch_hs, absorbed readout)."""
     wg, wu = head.w_gu.float().cpu().chunk(2, 0)
     z = rms(a.float(), ln2.float(), eps)
     return (F.silu(z @ wg.t()) * (z @ wu.t())) @ head.w_row.float().cpu()
+
+
+def branch_scores(head, a: torch.Tensor, ln2: torch.Tensor, eps: float) -> torch.Tensor:
+    """branch_scores_f32 rounded to bf16: the branch's output is the model dtype's
+    (gate_forward.py:519-521), and the raw score the gate normalises is that bf16 value."""
+    return branch_scores_f32(head, a, ln2, eps).to(torch.bfloat16).float()
 
 
 def _is_branch(head) -> bool:
@@ -164,7 +191,7 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
         x, _, _ = layer(W, i, x, pos, boundary=bnd)
     a = bnd[-1]
     Ks = K if isinstance(K, (list, tuple)) else [K] * B
-    keeps, biases, h_gate = [], [], []
+    keeps, biases, h_gate, scs = [], [], [], []
     for b in range(B):
         st, en = art_starts[b], art_ends[b]
         h_gate.append(x[b, :lens[b]].clone())
@@ -172,30 +199,32 @@ def prefill(W: Weights, head, ids_list: Sequence[Sequence[int]], art_starts, art
               else gate_scores(W, head, gate_layer, a[b, st:en], x[b, st:en]))
         kp = keep_override[b] if keep_override is not None else og.keep_indices(sc, Ks[b], st, en, lens[b])
         keeps.append(np.asarray(kp, dtype=np.int64))
-        biases.append(og.gate_bias(sc, keeps[-1], st, en))
+        scs.append(np.asarray(sc, dtype=np.float32))
+        biases.append(og.gate_bias(scs[-1], keeps[-1], st, en, gain=float(getattr(head, "bias_gain", 1.0))))
     n_alloc = max(len(k) for k in keeps)
     hp = torch.zeros(B, n_alloc, s.d_model)
     kpos = torch.zeros(B, n_alloc, dtype=torch.long)
-    gb = torch.full((B, n_alloc), -1e9, dtype=torch.float64)
-    for b in range(B):
-        kt = torch.as_tensor(keeps[b])
-        hp[b, :len(kt)] = x[b, kt]
-        kpos[b, :len(kt)] = kt
-        gb[b, :len(kt)] = torch.as_tensor(biases[b])
     if tuple(head.gate_scale.shape) != (s.n_layers - gate_layer - 1, s.n_heads):
         raise ValueError("gate_scale must be (layers above the gate, heads)")
-    gs = F.softplus(head.gate_scale.float().cpu()) * float(getattr(head, "bias_gain", 1.0))   # (L2, H)
-    at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
-    ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
-    r = torch.as_tensor(og.ssmax_ratio(kpos.numpy()), dtype=torch.float32) if ssmax else None   # (B, n_alloc)
+    L2 = s.n_layers - gate_layer - 1
+    # pad slots carry -1e9 (gate_forward.py:1467-1469); their query multiplier is irrelevant
+    bl = torch.full((L2, B, s.n_heads, n_alloc), -1e9)
+    qs = torch.ones(L2, B, s.n_heads, n_alloc)
+    any_scale = False
+    for b in range(B):
+        kt = torch.as_tensor(keeps[b])
+        n = len(kt)
+        hp[b, :n] = x[b, kt]
+        kpos[b, :n] = kt
+        bj, sj = phase2_tables(head, scs[b], keeps[b], art_starts[b], art_ends[b])
+        for j in range(L2):
+            bl[j, b, :, :n] = bj[j]
+            if sj[j] is not None:
+                qs[j, b, :, :n] = sj[j]
+                any_scale = True
     xx = hp
     for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
-        if ssmax:
-            bl = gb.float()[:, None, :] * gs[j][None, :, None] * at[j].mean() * r[:, None, :]
-        else:
-            bl = gb.float()[:, None, :] * gs[j][None, :, None]
-        bl = torch.where(gb[:, None, :] <= -1e8, torch.full_like(bl, -1e9), bl)
-        xx, _, _ = layer(W, i, xx, kpos, bias_logit=bl, q_temp=at[j] if at is not None else None, q_row=r)
+        xx, _, _ = layer(W, i, xx, kpos, bias_logit=bl[j], q_scale=qs[j] if any_scale else None)
     last = torch.tensor([len(k) - 1 for k in keeps])
     rows = xx[torch.arange(B), last]
     logits = rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()
@@ -261,20 +290,23 @@ def decode_logits(W: Weights, head, ids: Sequence[int], art_start: int, art_end:
             xg, _, _ = layer_with_past(W, i, xg, gpos, k, v)
         x = xn
     sc = gate_scores(W, head, gate_layer, bnd[-1][0, art_start:art_end], x[0, art_start:art_end])
-    kb = torch.as_tensor(og.gate_bias(sc, np.asarray(keep), art_start, art_end), dtype=torch.float32)
-    gb = torch.cat([kb, torch.zeros(g)])
+    biases, scales = phase2_tables(head, np.asarray(sc, dtype=np.float32), np.asarray(keep), art_start, art_end)
     xx = torch.cat([x[0, kp], xg[0]])[None]
     pos2 = torch.cat([kp[None], gpos], 1)
-    gs = F.softplus(head.gate_scale.float().cpu()) * float(getattr(head, "bias_gain", 1.0))
-    at = F.softplus(head.attn_scale.float().cpu()) if head.attn_scale is not None else None
-    ssmax = bool(getattr(head, "scaled_softmax", False)) and at is not None
-    # scaled softmax: the ratio over kept ++ generated slots (a generated token's slot is n_kept + 1 + i)
-    r = torch.as_tensor(og.ssmax_ratio(pos2.numpy()), dtype=torch.float32) if ssmax else None
+    n_kept, H = len(kp), s.n_heads
+    temp = og.softplus32(head.attn_scale.float().cpu().numpy()) if head.attn_scale is not None else None
+    ssmax = bool(getattr(head, "scaled_softmax", False)) and temp is not None
+    # a generated token's ratio: slot n_kept + 1 + i at position nxt + i (FormDecodeState.step)
+    r_gen = og.ssmax_ratio(pos2.numpy())[0, n_kept:].astype(np.float32) if ssmax else None
     for j, i in enumerate(range(gate_layer + 1, s.n_layers)):
-        if ssmax:
-            bl = gb[None, None, :] * gs[j][None, :, None] * at[j].mean() * r[:, None, :]
-        else:
-            bl = gb[None, None, :] * gs[j][None, :, None]
-        xx, _, _ = layer(W, i, xx, pos2, bias_logit=bl, q_temp=at[j] if at is not None else None, q_row=r)
+        bl = torch.cat([biases[j], torch.zeros(H, g)], 1)[None]            # generated keys: 0
+        qs = None
+        if scales[j] is not None:
+            if ssmax:
+                sg = [og.decode_query_scale(temp[j], r_gen[t]) for t in range(g)]
+            else:
+                sg = [og.phase2_query_scale(temp[j])[:, 0]] * g
+            qs = torch.cat([scales[j]] + [torch.from_numpy(np.asarray(v, np.float32))[:, None] for v in sg], 1)[None]
+        xx, _, _ = layer(W, i, xx, pos2, bias_logit=bl, q_scale=qs)
     rows = xx[0, len(kp) - 1:]
     return rms(rows, W.final_norm, s.rms_eps) @ W.lm_head.t()

@@ -3,8 +3,15 @@
 Small shapes against the float64 numpy oracle; the reference's own GPU-test shapes
 (tests/attention/test_attention_backends_grad.py:21-31,65: S in {1024, 4096, 4093}, H16/Hkv8,
 inputs randn*0.5, bias randn*2 with the last 64 keys at -1e9) and the B4 x 8192 training shape
-against the float32 torch evaluation of the same math on the device.  Tolerance: max-abs
-<= 2e-2 relative to max(1, max|ref|) and rel-L2 <= 1e-2 (tests/attn_util.assert_close_grad).
+against the float32 torch evaluation of the same math on the device.  Both oracles take D and P
+from the forward output and log-sum-exp the kernel was handed (the reference's op saves the bf16
+`out` and the fp32 `lse`; its FA2 backward forms D = rowsum(dO * out) and P = exp(z - lse) from
+them).  Tolerances (tests/attn_util.check_bwd; absolute
+max-abs and rel-L2 of every gradient printed): dBias and softmax_d (fp32 outputs) max-abs <= 2e-2
+and rel-L2 <= 1e-2 against the exact math; dQ/dK/dV (bf16 outputs) rel-L2 <= 1e-2 and max-abs
+<= 2e-2 relative to max(1, max|ref|) against the exact math, and max-abs <= 2e-2 on entries below
+4 (2e-2 * |ref| / 4 above) against the same math with P and dS rounded to bf16 where the reference
+kernel rounds them (oracle bf16_operands).
 """
 import numpy as np
 import pytest
@@ -12,7 +19,13 @@ import torch
 
 from oracle import attention as ora
 from oracle import attention_torch as ort
-from tests.attn_util import assert_close_grad as assert_close, bias_logsigmoid, qkv, to_np
+from tests.attn_util import bias_logsigmoid, check_bwd, qkv, to_np
+
+
+def _np_oracles(dout, q, k, v, bias_raw, scale, causal, out, lse):
+    a = (to_np(dout), to_np(q), to_np(k), to_np(v), None if bias_raw is None else to_np(bias_raw), scale, causal)
+    kw = dict(out=to_np(out), lse=to_np(lse))
+    return ora.keybias_bwd(*a, **kw), ora.keybias_bwd(*a, **kw, bf16_operands=True)
 
 pytestmark = pytest.mark.gpu
 
@@ -23,7 +36,7 @@ def _fwd_bwd(q, k, v, bias_raw, dout, scale, causal):
     dq, dk, dv, sd, db = ext().bwd(dout, q, k, v, out, lse, None, None, None, bias_raw, 0.0, scale, causal,
                                    -1, -1, 0.0, False, None, None)
     torch.cuda.synchronize()
-    return dq, dk, dv, db, sd
+    return dq, dk, dv, db, sd, out, lse
 
 
 @pytest.mark.parametrize("S", [1, 33, 64, 100, 257])
@@ -35,10 +48,9 @@ def test_bwd_small_vs_oracle(cuda, S, H, Hkv, causal):
     scale = 128 ** -0.5
     bias_raw = (torch.randn(2, H, S, device=cuda, generator=g) * 2.0 / scale).contiguous()
     dout = torch.randn(2, S, H, 128, device=cuda, generator=g).to(torch.bfloat16)
-    dq, dk, dv, db, sd = _fwd_bwd(q, k, v, bias_raw, dout, scale, causal)
-    r = ora.keybias_bwd(to_np(dout), to_np(q), to_np(k), to_np(v), to_np(bias_raw), scale, causal)
-    for name, got, ref in zip(["dq", "dk", "dv", "dbias_raw", "softmax_d"], [dq, dk, dv, db, sd], r):
-        assert_close(f"{name} S={S} H={H}/{Hkv} causal={causal}", to_np(got), ref)
+    dq, dk, dv, db, sd, out, lse = _fwd_bwd(q, k, v, bias_raw, dout, scale, causal)
+    ex, fa = _np_oracles(dout, q, k, v, bias_raw, scale, causal, out, lse)
+    check_bwd(f"S={S} H={H}/{Hkv} causal={causal}", [to_np(t) for t in (dq, dk, dv, db, sd)], ex, fa)
 
 
 @pytest.mark.parametrize("Sq,Sk", [(100, 300), (300, 100), (129, 128)])
@@ -50,10 +62,9 @@ def test_bwd_unequal_lengths(cuda, Sq, Sk):
     bias_raw = (torch.randn(1, H, Sk, device=cuda, generator=g) / scale).contiguous()
     dout = torch.randn(1, Sq, H, 128, device=cuda, generator=g).to(torch.bfloat16)
     for causal in (True, False):
-        dq, dk, dv, db, sd = _fwd_bwd(q, k, v, bias_raw, dout, scale, causal)
-        r = ora.keybias_bwd(to_np(dout), to_np(q), to_np(k), to_np(v), to_np(bias_raw), scale, causal)
-        for name, got, ref in zip(["dq", "dk", "dv", "dbias_raw", "softmax_d"], [dq, dk, dv, db, sd], r):
-            assert_close(f"{name} Sq={Sq} Sk={Sk} causal={causal}", to_np(got), ref)
+        dq, dk, dv, db, sd, out, lse = _fwd_bwd(q, k, v, bias_raw, dout, scale, causal)
+        ex, fa = _np_oracles(dout, q, k, v, bias_raw, scale, causal, out, lse)
+        check_bwd(f"Sq={Sq} Sk={Sk} causal={causal}", [to_np(t) for t in (dq, dk, dv, db, sd)], ex, fa)
 
 
 def test_bwd_no_bias(cuda):
@@ -61,11 +72,10 @@ def test_bwd_no_bias(cuda):
     q, k, v = qkv(1, 200, 200, 16, 8, g, cuda)
     scale = 128 ** -0.5
     dout = torch.randn(1, 200, 16, 128, device=cuda, generator=g).to(torch.bfloat16)
-    dq, dk, dv, db, sd = _fwd_bwd(q, k, v, None, dout, scale, True)
+    dq, dk, dv, db, sd, out, lse = _fwd_bwd(q, k, v, None, dout, scale, True)
     assert db is None
-    r = ora.keybias_bwd(to_np(dout), to_np(q), to_np(k), to_np(v), None, scale, True)
-    for name, got, ref in zip(["dq", "dk", "dv"], [dq, dk, dv], r[:3]):
-        assert_close(f"{name} no-bias", to_np(got), ref)
+    ex, fa = _np_oracles(dout, q, k, v, None, scale, True, out, lse)
+    check_bwd("no-bias", [to_np(t) for t in (dq, dk, dv)] + [None, to_np(sd)], ex, fa)
 
 
 @pytest.mark.parametrize("S", [1024, 4096, 4093])
@@ -86,13 +96,15 @@ def test_reference_grad_test_shapes_autograd(cuda, S):
     out = flash_attn_key_bias(q, k, v, key_bias, scale, causal=True)
     out.backward(dO.transpose(1, 2))
     torch.cuda.synchronize()
-    rdq, rdk, rdv, rdb, _ = ort.bwd(dO.transpose(1, 2), q.detach(), k.detach(), v.detach(),
-                                    key_bias.detach().float() / scale, scale, True)
-    assert_close(f"dq S={S}", to_np(q.grad), to_np(rdq))
-    assert_close(f"dk S={S}", to_np(k.grad), to_np(rdk))
-    assert_close(f"dv S={S}", to_np(v.grad), to_np(rdv))
+    braw = (key_bias.detach().float() / scale).contiguous()
+    _, lse = torch.ops.recursive_kvs.fa2_keybias_fwd(q.detach(), k.detach(), v.detach(), braw, scale, True)
+    args = (dO.transpose(1, 2), q.detach(), k.detach(), v.detach(), braw, scale, True)
+    ex = ort.bwd(*args, out=out.detach(), lse=lse)
+    fa = ort.bwd(*args, out=out.detach(), lse=lse, bf16_operands=True)
     # d/d key_bias = (d/d bias_raw) / scale; the -1e9 keys get exactly zero gradient
-    assert_close(f"dbias S={S}", to_np(key_bias.grad), to_np(rdb / scale))
+    check_bwd(f"S={S}", [to_np(q.grad), to_np(k.grad), to_np(v.grad), to_np(key_bias.grad)],
+              [to_np(t) for t in (ex[0], ex[1], ex[2], ex[3] / scale)], [to_np(t) for t in fa[:3]] + [None],
+              names=("dq", "dk", "dv", "dbias"))
     assert float(key_bias.grad[0, :, -64:].abs().max()) == 0.0
 
 
@@ -110,13 +122,14 @@ def test_config_bwd_8k_b4(cuda):
     out = flash_attn_key_bias(q, k, v, kb[:, None, :].expand(B, H, S), scale, causal=True)
     out.backward(dO)
     torch.cuda.synchronize()
-    rdq, rdk, rdv, rdb, _ = ort.bwd(dO, q.detach(), k.detach(), v.detach(),
-                                    (kb.detach()[:, None, :].expand(B, H, S) / scale).contiguous(), scale, True,
-                                    chunk=2048)
-    assert_close("dq 8k", to_np(q.grad), to_np(rdq))
-    assert_close("dk 8k", to_np(k.grad), to_np(rdk))
-    assert_close("dv 8k", to_np(v.grad), to_np(rdv))
-    assert_close("dbias 8k (sum over heads)", to_np(kb.grad), to_np(rdb.sum(1) / scale))
+    braw = (kb.detach()[:, None, :].expand(B, H, S) / scale).contiguous()
+    _, lse = torch.ops.recursive_kvs.fa2_keybias_fwd(q.detach(), k.detach(), v.detach(), braw, scale, True)
+    args = (dO, q.detach(), k.detach(), v.detach(), braw, scale, True)
+    ex = ort.bwd(*args, chunk=2048, out=out.detach(), lse=lse)
+    fa = ort.bwd(*args, chunk=2048, out=out.detach(), lse=lse, bf16_operands=True)
+    check_bwd("8k b4", [to_np(q.grad), to_np(k.grad), to_np(v.grad), to_np(kb.grad)],
+              [to_np(t) for t in (ex[0], ex[1], ex[2], ex[3].sum(1) / scale)], [to_np(t) for t in fa[:3]] + [None],
+              names=("dq", "dk", "dv", "dbias (sum over heads)"))
 
 
 def test_varlen_bwd_vs_oracle(cuda):
@@ -138,14 +151,15 @@ def test_varlen_bwd_vs_oracle(cuda):
     dq, dk, dv, sd, db = ext().varlen_bwd(dout, q, k, v, out, lse, None, None, None, cu_t, cu_t, bias_raw,
                                           maxlen, maxlen, 0.0, scale, False, True, -1, -1, 0.0, False, None, None)
     torch.cuda.synchronize()
-    qn, kn, vn, dn, bn = to_np(q), to_np(k), to_np(v), to_np(dout), to_np(bias_raw)
+    qn, kn, vn, dn, bn, on, ln = to_np(q), to_np(k), to_np(v), to_np(dout), to_np(bias_raw), to_np(out), to_np(lse)
     for s, (st, n) in enumerate(ora.varlen_to_dense(cu)):
         if n == 0:
             continue
-        r = ora.keybias_bwd(dn[None, st:st + n], qn[None, st:st + n], kn[None, st:st + n], vn[None, st:st + n],
-                            bn[s:s + 1, :, :n], scale, True)
-        assert_close(f"varlen dq seq {s}", to_np(dq)[st:st + n], r[0][0])
-        assert_close(f"varlen dk seq {s}", to_np(dk)[st:st + n], r[1][0])
-        assert_close(f"varlen dv seq {s}", to_np(dv)[st:st + n], r[2][0])
-        assert_close(f"varlen dbias seq {s}", to_np(db)[s, :, :n], r[3][0])
-        assert_close(f"varlen softmax_d seq {s}", to_np(sd)[:, st:st + n], r[4][0])
+        a = (dn[None, st:st + n], qn[None, st:st + n], kn[None, st:st + n], vn[None, st:st + n],
+             bn[s:s + 1, :, :n], scale, True)
+        kw = dict(out=on[None, st:st + n], lse=ln[None, :, st:st + n])
+        ex = ora.keybias_bwd(*a, **kw)
+        fa = ora.keybias_bwd(*a, **kw, bf16_operands=True)
+        got = [to_np(dq)[None, st:st + n], to_np(dk)[None, st:st + n], to_np(dv)[None, st:st + n],
+               to_np(db)[s:s + 1, :, :n], to_np(sd)[None, :, st:st + n]]
+        check_bwd(f"varlen seq {s}", got, ex, fa)

@@ -15,6 +15,7 @@ import math
 import os
 
 import pytest
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -55,9 +56,23 @@ def test_load_gate_holds_bf16_images(tmp_path):
     assert torch.equal(head.w_row, sd["gate_branch.down_proj.weight"][0].to(torch.bfloat16))
     assert torch.equal(head.gate_scale, sd["gate_scale"]) and torch.equal(head.attn_scale, sd["attn_scale"])
     assert head.bias_gain == 1.25 and meta == {"gate_layer": 1}
-    coef, qs = head.layer_coefficients(0.25)
-    want = F.softplus(sd["gate_scale"]) * 1.25 * F.softplus(sd["attn_scale"]).mean(1, keepdim=True) / 0.25
-    assert torch.allclose(coef, want, rtol=1e-6)
+    # the Phase-2 constants of the loaded gate follow the reference's bf16 chain (oracle.gate)
+    from oracle import gate as og
+    g = torch.Generator().manual_seed(3)
+    T2 = 300
+    kept = torch.randn(T2, generator=g)
+    kept[:5] = 0                                                    # prefix rows
+    ratio = torch.rand(T2, generator=g) * 0.5 + 0.5
+    bias_raw, q_head, q_row = head.phase2_tables(kept, ratio, 0.25)
+    temp = og.softplus32(sd["attn_scale"].numpy())
+    b = (np.float32(1.25) * kept.numpy()).astype(np.float32)[:, None, None] * og.softplus32(sd["gate_scale"].numpy())[None]
+    gb = og.bf16(b.astype(np.float32))
+    for l in range(gb.shape[1]):
+        want = og.phase2_bias(gb[:, l, :], temp[l], ratio.numpy()).T / np.float32(0.25)
+        assert np.array_equal(bias_raw[l].numpy(), want.astype(np.float32))
+        s_want = og.phase2_query_scale(temp[l], ratio.numpy())
+        s_got = (q_head[l][:, None] * q_row[None, :]).to(torch.bfloat16).float().numpy()
+        assert np.array_equal(s_got, s_want)
 
 
 @pytest.mark.parametrize("over,match", [

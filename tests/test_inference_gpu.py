@@ -2,7 +2,7 @@
 oracle's teacher-forced decode (oracle.prefill.decode_logits: generated tokens through layers
 0..gate over the full prompt and through the layers above over the kept rows, prompt keys
 keeping their gate bias), logits within max-abs 2e-2 (relative to max(1, |ref|)) and rel-L2
-3e-2 (several bf16 layers); and the generate() contract: first-EOS truncation, the streamer,
+2e-2 (several bf16 layers; measured values printed); and the generate() contract: first-EOS truncation, the streamer,
 kept positions, per-sequence K, prune_below_gate."""
 import numpy as np
 import pytest
@@ -66,7 +66,8 @@ def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch):
         gen = [int(t[b]) for t in toks[:steps]]      # tokens fed to the decode steps
         ref = op.decode_logits(W, m.gate, clean, s, e, m.gate_layer, keep, gen, prune_below_gate)
         for i in range(steps):
-            assert_close_grad(f"seq {b} step {i}", to_np(logits[i][b]), to_np(ref[1 + i]), rel_l2=3e-2)
+            ma, rl = assert_close_grad(f"seq {b} step {i}", to_np(logits[i][b]), to_np(ref[1 + i]), rel_l2=2e-2)
+            print(f"[decode] seq {b} step {i}: logits max-abs/max(1,|ref|) {ma:.2e} rel-L2 {rl:.2e}", flush=True)
             assert int(toks[i + 1][b]) == int(logits[i][b].argmax())
 
 

@@ -181,3 +181,75 @@ def test_torch_oracle_matches_numpy(causal):
     got = ort.bwd(dout.float(), q.float(), k.float(), v.float(), b.float(), scale, causal, chunk=16)
     for r, t in zip(ref, got):
         np.testing.assert_allclose(t.numpy(), r, rtol=1e-3, atol=1e-4)
+
+
+def test_bwd_given_out_and_bf16_operands():
+    """The backward's two options.  out: D = rowsum(dO * out) from the output handed in — with the
+    oracle's own forward output it is the default; with the output perturbed, only D (softmax_d)
+    and the dS-derived gradients move (dV = P^T dO does not depend on D).  bf16_operands: exact
+    when P and dS are bf16 values (uniform attention over 8 keys, small-integer V / dO); on random
+    inputs every changed gradient stays within the rounding bound 2^-8 * sum |x_i y_i| of its
+    products and differs from the exact one."""
+    q, k, v, b = _inputs(1, 12, 12, 4, 2, 16, seed=31)
+    g = torch.Generator().manual_seed(32)
+    dout = torch.randn(1, 12, 4, 16, generator=g).double().numpy()
+    scale = 16 ** -0.5
+    args = (dout, q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    ref = ora.keybias_bwd(*args)
+    o, _ = ora.keybias_fwd(*args[1:])
+    same = ora.keybias_bwd(*args, out=o)
+    for r, t in zip(ref, same):
+        np.testing.assert_array_equal(r, t)
+    moved = ora.keybias_bwd(*args, out=o * 1.01)
+    np.testing.assert_allclose(moved[4], 1.01 * ref[4], rtol=1e-12)
+    np.testing.assert_array_equal(moved[2], ref[2])
+    assert not np.allclose(moved[0], ref[0]) and not np.allclose(moved[3], ref[3])
+
+    # bf16-exact operands: non-causal, q = 0 and bias 0 -> P = 1/8; V, dO in {-1, 0, 1}, head dim 4
+    rng = np.random.default_rng(33)
+    Dh = 4
+    qz = np.zeros((1, 8, 2, Dh))
+    kk = rng.integers(-1, 2, (1, 8, 1, Dh)).astype(np.float64)
+    vv = rng.integers(-1, 2, (1, 8, 1, Dh)).astype(np.float64)
+    dd = rng.integers(-1, 2, (1, 8, 2, Dh)).astype(np.float64)
+    e = ora.keybias_bwd(dd, qz, kk, vv, None, 0.5, False)
+    r = ora.keybias_bwd(dd, qz, kk, vv, None, 0.5, False, bf16_operands=True)
+    for x, y in zip(e[:3], r[:3]):      # exp(-ln 8) is 1/8 to within float64 rounding
+        np.testing.assert_allclose(x, y, rtol=1e-12, atol=1e-15)
+
+    # random operands: bounded, and not a no-op
+    q, k, v, b = _inputs(1, 40, 40, 2, 1, 16, seed=34)
+    dout = torch.randn(1, 40, 2, 16, generator=g).double().numpy()
+    e = ora.keybias_bwd(dout, q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    r = ora.keybias_bwd(dout, q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True, bf16_operands=True)
+    np.testing.assert_array_equal(e[3], r[3])
+    np.testing.assert_array_equal(e[4], r[4])
+    # |sum r(x) y - sum x y| <= 2^-8 sum |x| |y|, with x = P or dS (from the exact run's own P, dS)
+    out, lse = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    z = ora._logits(q.numpy()[0, :, 0], k.numpy()[0, :, 0], b.numpy()[0, 0], scale, True, np.arange(40), 40, 40)
+    p = np.exp(z - lse[0, 0][:, None])
+    do = dout[0, :, 0]
+    ds = p * (do @ v.numpy()[0, :, 0].T - (do * out[0, :, 0]).sum(1)[:, None])
+    # head 0's contribution to dq (one head per query row)
+    bound_dq = 2.0 ** -8 * scale * np.abs(ds) @ np.abs(k.numpy()[0, :, 0])
+    assert np.all(np.abs(r[0][0, :, 0] - e[0][0, :, 0]) <= bound_dq + 1e-12)
+    assert np.abs(r[0] - e[0]).max() > 0 and np.abs(r[1] - e[1]).max() > 0 and np.abs(r[2] - e[2]).max() > 0
+
+
+@pytest.mark.parametrize("bf16_operands", [False, True])
+def test_torch_oracle_bwd_options_match_numpy(bf16_operands):
+    from oracle import attention_torch as ort
+    q, k, v, b = _inputs(2, 33, 33, 4, 2, 16, seed=41)
+    scale = 16 ** -0.5
+    g = torch.Generator().manual_seed(6)
+    dout = torch.randn(2, 33, 4, 16, generator=g).double()
+    o, _ = ora.keybias_fwd(q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True)
+    o16 = ora.bf16_round(o).astype(np.float64)
+    ref = ora.keybias_bwd(dout.numpy(), q.numpy(), k.numpy(), v.numpy(), b.numpy(), scale, True, out=o16,
+                          bf16_operands=bf16_operands)
+    got = ort.bwd(dout.float(), q.float(), k.float(), v.float(), b.float(), scale, True, chunk=16,
+                  out=torch.from_numpy(o16).float(), bf16_operands=bf16_operands)
+    for name, r, t in zip(["dq", "dk", "dv", "dbias", "sd"], ref, got):
+        # fp32 vs float64 evaluation: an operand near a bf16 rounding boundary may round the other
+        # way (one bf16 unit of that operand), hence the absolute term
+        np.testing.assert_allclose(t.numpy(), r, rtol=2e-3, atol=2e-3, err_msg=name)

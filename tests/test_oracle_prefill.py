@@ -216,7 +216,7 @@ def test_branch_scores_boundary_and_split_match_transformers():
         mlp.down_proj.weight.copy_(head.w_row[None])
         norm.weight.copy_(lw.ln2)
         ref_sc = mlp(norm(ref_a))[..., 0]
-    ours_sc = op.branch_scores(head, a.reshape(-1, s.d_model), lw.ln2, s.rms_eps).view(B, n)
+    ours_sc = op.branch_scores_f32(head, a.reshape(-1, s.d_model), lw.ln2, s.rms_eps).view(B, n)
     assert _rel(ours_sc, ref_sc) < 1e-5
     assert float(ours_sc.std()) > 1e-3
     # split: the MLP half on a subset of rows == the whole layer's output on those rows
@@ -311,16 +311,18 @@ def test_scaled_softmax_reduces_to_mean_temperature_without_pruning():
     assert list(a["keep"][0]) == list(range(64))
     r = og.ssmax_ratio(np.arange(64))
     assert np.allclose(r, 1.0)
-    # the same run by hand: bias * mean(gamma), query * gamma_h
-    g = torch.nn.functional.softplus(head.attn_scale)
+    # the same run by hand, in the reference's bf16 arithmetic: bias = bf16(bf16(b * gs) *
+    # bf16(mean_h bf16(gamma_h))), query * bf16(gamma_h)
+    bf = lambda t: t.to(torch.bfloat16).float()
+    g = bf(torch.nn.functional.softplus(head.attn_scale))
     gs = torch.nn.functional.softplus(head.gate_scale)
     x = W.embed[torch.as_tensor(ids[0])][None]
     pos = torch.arange(64)[None]
     x, _, _ = op.layer(W, 0, x, pos)
     kb = torch.as_tensor(a["kept_bias"][0], dtype=torch.float32)
     for j, i in enumerate(range(1, 3)):
-        bl = kb[None, None, :] * gs[j][None, :, None] * g[j].mean()
-        x, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_temp=g[j], q_row=torch.ones(1, 64))
+        bl = bf(bf(kb[None, None, :] * gs[j][None, :, None]) * bf(g[j].mean()))
+        x, _, _ = op.layer(W, i, x, pos, bias_logit=bl, q_scale=g[j][None, :, None].expand(1, -1, 64))
     ref = op.rms(x[0, -1], W.final_norm, s.rms_eps) @ W.lm_head.t()
     assert _rel(a["logits"][0], ref) < 1e-5
     # and it differs from the per-head temperature mode

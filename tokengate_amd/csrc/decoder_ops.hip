@@ -135,13 +135,19 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = wf[e] * (x[e] * rinv);
     const float sgn = j < 8 ? -1.f : 1.f;
-    const float hs = is_q ? (q_head_scale ? q_head_scale[rr] : 1.f) * (q_row_scale ? q_row_scale[t] : 1.f) : 1.f;
+    // Query multiplier s = bf16(head * row), applied to the bf16-rounded rotated query with one
+    // more bf16 rounding: the reference scales its bf16 query states in bf16 (q * s_eff,
+    // qwen3_flex_attention.py:442-451, :400).  With no multiplier s = 1 and the second rounding
+    // is exact.
+    const float hs = is_q ? (float)(__bf16)((q_head_scale ? q_head_scale[rr] : 1.f) *
+                                            (q_row_scale ? q_row_scale[t] : 1.f))
+                          : 1.f;
     float y[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p = __shfl_xor(x[e], 8);
       const int fi = (8 * j + e) & 63;
-      y[e] = hs * (x[e] * cs[tt][fi][0] + sgn * p * cs[tt][fi][1]);
+      y[e] = hs * (float)(__bf16)(x[e] * cs[tt][fi][0] + sgn * p * cs[tt][fi][1]);
     }
     bf16_t *dst = is_q ? q_out + t * q_rs + (int64_t)rr * kHeadDim
                        : k_out + t * k_rs + (int64_t)(rr - H) * kHeadDim;

@@ -42,10 +42,8 @@ class DecodeState:
         dev = wts.device
         B = len(pf.n_kept)
         self.B = B
-        scale = 1.0 / math.sqrt(shape.head_dim)
-        coef, qs = head.layer_coefficients(scale)
+        q_head = head.decode_query_head()
         self.layers: List[_LayerCache] = []
-        kept_bias = pf.kept_bias
         for l in range(shape.n_layers):
             below = l <= gate_layer
             cu = pf.cu_prompt if (below and not prune_below_gate) else pf.cu_kept
@@ -63,14 +61,13 @@ class DecodeState:
             if not below:
                 j = l - gate_layer - 1
                 cap = max(n) + max_new_tokens
+                # kept keys keep their Phase-2 bias (decode_phase2_layer_tensors,
+                # qwen3_flex_attention.py:1010-1017); generated keys carry 0
                 bias = torch.zeros(B, shape.n_heads, cap, dtype=torch.float32, device=dev)
                 for b in range(B):
-                    kb = kept_bias[pf.cu_kept[b]:pf.cu_kept[b + 1]]
-                    if pf.kept_ratio is not None:            # scaled softmax: keys keep their prefill r
-                        kb = kb * pf.kept_ratio[pf.cu_kept[b]:pf.cu_kept[b + 1]]
-                    bias[b, :, :n[b]] = coef[j][:, None] * kb[None, :]
+                    bias[b, :, :n[b]] = pf.phase2_bias[j, :, pf.cu_kept[b]:pf.cu_kept[b + 1]]
                 lc.bias = bias
-                lc.qscale = qs[j].contiguous() if qs is not None else None
+                lc.qscale = q_head[j].contiguous() if q_head is not None else None
             self.layers.append(lc)
         last = torch.tensor([pf.cu_kept[b + 1] - 1 for b in range(B)], dtype=torch.int64)
         self.next_pos = pf.kept_positions.index_select(0, h2d(last, dev)) + 1

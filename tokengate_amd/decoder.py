@@ -135,8 +135,9 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, lw: LayerWeights, s
                  q_head_scale: Optional[torch.Tensor] = None,
                  q_row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Normalises and rotates q in place inside qkv (returned as a (T, H, D) view) and writes the
-    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous).  q is scaled by
-    q_head_scale (H,) and q_row_scale (T,) fp32 when given."""
+    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous).  With q_head_scale (H,)
+    and / or q_row_scale (T,) fp32 the bf16 query is multiplied by bf16(q_head_scale[h] *
+    q_row_scale[t]) and rounded to bf16 again (the reference's bf16 q * s_eff)."""
     T = qkv.shape[0]
     H, Hkv, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
     if positions.dtype != torch.int64 or positions.numel() != T:

@@ -206,19 +206,54 @@ class _BiasScales:
     def ssmax(self) -> bool:
         return self.scaled_softmax and self.attn_scale is not None
 
-    def layer_coefficients(self, softmax_scale: float) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
-        """(bias coefficient in raw-score units, per-head query scale) per (layer, head):
-        raw bias of key j = normalised score_j * coef[l, h] (* r_j in scaled-softmax mode), where
-        coef = bias_gain * softplus(gate_scale) * temperature / softmax_scale; the temperature is
-        softplus(attn_scale) per head, or its mean over heads in scaled-softmax mode."""
-        coef = torch.nn.functional.softplus(self.gate_scale.float())
+    def phase2_tables(self, kept_bias: torch.Tensor, ratio: Optional[torch.Tensor], softmax_scale: float
+                      ) -> Tuple[torch.Tensor, Optional[torch.Tensor], Optional[torch.Tensor]]:
+        """The Phase-2 constants of the packed kept rows, in the reference's own arithmetic.
+
+        kept_bias (T2,) fp32: each kept row's RMS-normalised score (0 on prefix / suffix rows);
+        ratio (T2,) fp32: each kept row's scaled-softmax ratio r, or None.  The stored bias is
+        gb[l, j, h] = bf16(fp32(bias_gain * kept_bias_j) * softplus(gate_scale[l, h])) (E2EGate.forward
+        e2e_gate_module.py:363-385, kept in the model dtype by build_gate_bias_vectorized
+        gate_forward.py:995-1008, :1450); the key bias and query multiplier follow _phase2_q_bias
+        (qwen3_flex_attention.py:433-473) in bf16: scaled softmax s_eff = bf16(bf16(gamma_h) *
+        bf16(r)), bias' = bf16(gb * bf16(mean_h s_eff)); per-head temperature bias' =
+        bf16(gb * bf16(gamma_h)), gamma = softplus(attn_scale) (attn_scale_eff :302-305).
+
+        Returns (bias_raw (L2, H, T2) fp32 = bias' / softmax_scale, the kernel's raw-score units as
+        flash_attn_key_bias forms them (kernels/fa2bias/keybias.py:86); q_head (L2, H) and q_row
+        (T2,) fp32 bf16 values, or None: the factors tg_qk_norm_rope multiplies (s = bf16(q_head *
+        q_row)))."""
+        bf = torch.bfloat16
+        gs = torch.nn.functional.softplus(self.gate_scale.float())              # (L2, H)
+        bn = kept_bias.float()
         if self.bias_gain != 1.0:
-            coef = coef * float(self.bias_gain)
-        qs = None
-        if self.attn_scale is not None:
-            qs = torch.nn.functional.softplus(self.attn_scale.float()).contiguous()
-            coef = coef * (qs.mean(1, keepdim=True) if self.scaled_softmax else qs)
-        return (coef / softmax_scale).contiguous(), qs
+            bn = bn * float(self.bias_gain)
+        gb = (bn[None, :, None] * gs[:, None, :]).to(bf)                        # (L2, T2, H)
+        q_head = q_row = None
+        if self.attn_scale is None:
+            bias = gb
+        else:
+            temp = torch.nn.functional.softplus(self.attn_scale.float()).to(bf)  # (L2, H)
+            q_head = temp.float().contiguous()
+            if self.ssmax:
+                if ratio is None:
+                    raise RuntimeError("phase2_tables: scaled softmax needs the kept rows' ratio")
+                rb = ratio.to(bf)
+                s_eff = temp[:, :, None] * rb[None, None, :]                     # (L2, H, T2) bf16
+                bias = gb * s_eff.mean(1)[:, :, None]
+                q_row = rb.float()
+            else:
+                bias = gb * temp[:, None, :]
+        return (bias.float().permute(0, 2, 1) / softmax_scale).contiguous(), q_head, q_row
+
+    def decode_query_head(self) -> Optional[torch.Tensor]:
+        """q_head for a decode step: the new token's multiplier is bf16(gamma_h * r) from fp32
+        factors in scaled-softmax mode (FormDecodeState.step, qwen3_flex_attention.py:1090-1101,
+        applied at :400), bf16(gamma_h) with a per-head temperature; None without one."""
+        if self.attn_scale is None:
+            return None
+        temp = torch.nn.functional.softplus(self.attn_scale.float())
+        return (temp if self.ssmax else temp.to(torch.bfloat16).float()).contiguous()
 
 
 @dataclass

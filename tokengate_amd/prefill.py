@@ -36,6 +36,7 @@ from tokengate_amd.decoder import (DecoderWeights, LayerKV, Ragged, Workspace, a
 @dataclass
 class PrefillResult:
     first_tokens: torch.Tensor        # (B,) int64 on the device
+    logits: torch.Tensor              # (B, vocab) bf16: the LM head at each sequence's last kept row
     kept_positions: torch.Tensor      # (total_kept,) int64, packed (cu_kept layout)
     cu_kept: List[int]
     n_kept: List[int]
@@ -44,6 +45,7 @@ class PrefillResult:
     cu_prompt: List[int]
     kept_bias: torch.Tensor           # (total_kept,) fp32 normalised gate score (0 on prefix / suffix)
     kept_ratio: Optional[torch.Tensor] = None   # (total_kept,) fp32 scaled-softmax ratio r (ssmax heads)
+    phase2_bias: Optional[torch.Tensor] = None  # (L2, H, total_kept) fp32 raw-unit key bias of each Phase-2 layer
     phase_ms: Dict[str, float] = field(default_factory=dict)
     capture: Optional[dict] = None
 
@@ -77,29 +79,32 @@ class Phase2Graphs:
         return (n + b - 1) // b * b
 
     def run(self, wts: DecoderWeights, layer_ids: List[int], hs: torch.Tensor, positions: torch.Tensor,
-            cu_dev: torch.Tensor, coef: torch.Tensor, bias_pad: torch.Tensor, qscale: Optional[torch.Tensor],
-            mlp_rows: int, row_scale: Optional[torch.Tensor] = None):
-        shape = wts.shape
+            cu_dev: torch.Tensor, biases_all: torch.Tensor, q_head: Optional[torch.Tensor], mlp_rows: int,
+            q_row: Optional[torch.Tensor] = None):
+        """biases_all (L2, nseq, H, max_kept) fp32 raw-unit key bias; q_head (L2, H) / q_row (T2,)
+        the query factors (None when absent)."""
         dev = hs.device
         nseq = cu_dev.numel() - 1
-        T2, max_kept = hs.shape[0], bias_pad.shape[1]
+        T2, max_kept = hs.shape[0], biases_all.shape[-1]
         Tb, Lb = self._up(T2, self.bucket_rows), self._up(max_kept, self.bucket_len)
-        key = (nseq, Tb, Lb, tuple(layer_ids), qscale is not None, row_scale is not None)
+        # the graph reads the weights' and workspaces' memory: a key per weights object (held
+        # alive by the entry) and per MLP chunking
+        key = (id(wts), nseq, Tb, Lb, tuple(layer_ids), q_head is not None, q_row is not None, int(mlp_rows))
         ent = self.graphs.get(key)
         if ent is None:
-            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, qscale is not None, row_scale is not None, mlp_rows,
-                                dev)
+            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, q_head is not None, q_row is not None, mlp_rows, dev)
+            ent["wts"] = wts
             self.graphs[key] = ent
-        if row_scale is not None:
-            ent["rs"][:T2].copy_(row_scale)
+        if q_row is not None:
+            ent["rs"][:T2].copy_(q_row)
         ent["x"][:T2].copy_(hs)
         ent["x"][T2:].zero_()
         ent["pos"][:T2].copy_(positions)
         ent["pos"][T2:].zero_()
         ent["cu"].copy_(cu_dev)
-        torch.mul(coef[:, None, :, None], bias_pad[None, :, None, :], out=ent["bias"][..., :max_kept])
-        if qscale is not None:
-            ent["qs"].copy_(qscale)
+        ent["bias"][..., :max_kept].copy_(biases_all)
+        if q_head is not None:
+            ent["qs"].copy_(q_head)
         ent["graph"].replay()
         return ent["out"][:T2], {l: LayerKV(ent["kv"][l].k[:T2], ent["kv"][l].v[:T2]) for l in layer_ids}
 
@@ -210,35 +215,30 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
             cap["hs_boundary"] = hs
         hs = mlp_sublayer(wts, gate_layer, hs, ws2)
     max_kept = max(p.n_kept)
-    # per-sequence padded view of the packed bias: row b, column t <- packed row cu_kept[b] + t
+    ratio = G.ssmax_ratio_rows(kept_pos, p.cu_kept) if head.ssmax else None   # (T2,)
+    bias_rows, q_head, q_row = head.phase2_tables(kept_bias, ratio, 1.0 / math.sqrt(shape.head_dim))
+    # per-sequence padded view of the packed rows' bias: row b, column t <- packed row
+    # cu_kept[b] + t (columns past a sequence's end repeat its last row; the kernel never reads them)
     t_ = torch.arange(max_kept, dtype=torch.int64)
     st = torch.tensor(p.cu_kept[:-1], dtype=torch.int64)[:, None]
     en = torch.tensor(p.cu_kept[1:], dtype=torch.int64)[:, None] - 1
-    idx = torch.minimum(st + t_[None, :], en)
-    idx_d = h2d(idx, dev)
-    bias_pad = kept_bias[idx_d]                                               # (B, max_kept)
-    ratio = None
-    if head.ssmax:
-        ratio = G.ssmax_ratio_rows(kept_pos, p.cu_kept)                       # (T2,)
-        bias_pad = bias_pad * ratio[idx_d]
-    coef, qscale = head.layer_coefficients(1.0 / math.sqrt(shape.head_dim))  # (L2, H)
+    idx_d = h2d(torch.minimum(st + t_[None, :], en), dev)
+    biases_all = bias_rows[:, :, idx_d].permute(0, 2, 1, 3).contiguous()      # (L2, B, H, max_kept)
     cu2_dev = h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev)
     above = list(range(gate_layer + 1, n_layers))
-    biases_all = None
     if phase2_graphs is not None and cap is None:
-        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, coef, bias_pad, qscale, mlp_rows, ratio)
+        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, biases_all, q_head, mlp_rows, q_row)
         for l in above:
             kv[l] = kv2[l]
     else:
-        biases_all = coef[:, None, :, None] * bias_pad[None, :, None, :]       # (L2, B, H, max_kept)
         geo2 = Ragged(p.cu_kept, cu2_dev, kept_pos, max_kept)
         biases = {l: biases_all[j] for j, l in enumerate(above)}
-        qs = {l: qscale[j] for j, l in enumerate(above)} if qscale is not None else None
+        qs = {l: q_head[j] for j, l in enumerate(above)} if q_head is not None else None
         for l in above:
             kv[l] = alloc_kv(shape, T2, dev)
         ws2 = ws2 if ws2 is not None else Workspace(shape, T2, dev, mlp_rows=mlp_rows)
         h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
-                        capture=cap["phase2"] if cap else None, q_row_scale=ratio)
+                        capture=cap["phase2"] if cap else None, q_row_scale=q_row)
 
     mark("head")
     last = h2d(torch.tensor(p.cu_kept[1:], dtype=torch.int64).sub_(1), dev)
@@ -252,9 +252,9 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
             phase_ms[n0] = e0.elapsed_time(e1)
     if cap is not None:
         cap.update(scores=scores, keep=keep, hs_packed=hs, h2=h2, logits=logits, biases_all=biases_all,
-                   qscale=qscale, bias_pad=bias_pad)
-    return PrefillResult(first, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, ratio, phase_ms,
-                         cap)
+                   q_head=q_head, q_row=q_row)
+    return PrefillResult(first, logits, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, ratio, bias_rows,
+                         phase_ms, cap)
 
 
 def ttft_ms(fn, reps: int = 5, warmup: int = 1) -> List[float]:
