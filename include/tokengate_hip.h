@@ -64,6 +64,27 @@ int tg_keybias_fwd(const void *q, const void *k, const void *v, const float *bia
 int64_t tg_keybias_fwd_workspace_size(int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
                                       int32_t num_heads, int32_t num_heads_k, int32_t causal);
 
+/* tg_keybias_fwd for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference, whose
+ * mha_fwd allocates its split-KV accumulators itself.  Same arguments and results as
+ * tg_keybias_fwd; the key-range split's partials live in a static 24 MiB device array of the
+ * library (one per device, held until the process ends; a split needs at most CUs x 73,728 bytes,
+ * 18 MiB on MI355X) instead of a caller workspace.  Calls no hipMalloc / hipFree.  Returns an
+ * error, before launching anything, if a launch would need more than the static size.  All calls
+ * on one device share that array: calls that overlap on one device (different streams, or
+ * graphs replayed concurrently) race; calls ordered on one stream do not.  Its contents need no
+ * initialisation (every partial a launch reads is written by that launch). */
+int tg_keybias_fwd_noalloc(const void *q, const void *k, const void *v, const float *bias_raw,
+                           void *out, float *lse,
+                           int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                           int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                           int64_t q_batch_stride, int64_t q_row_stride, int64_t q_head_stride,
+                           int64_t k_batch_stride, int64_t k_row_stride, int64_t k_head_stride,
+                           int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
+                           int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
+                           int64_t bias_batch_stride, int64_t bias_head_stride,
+                           float softmax_scale, int32_t causal, hipStream_t stream);
+
 /* Variable-length key-bias attention forward (one causal attention per packed sequence).
  * Replaces ext().varlen_fwd(q, k, v, None, cu, cu, None, None, None, bias_raw, max, max, 0.0,
  * scale, False, causal, -1, -1, 0.0, False, None) (kernels/fa2bias/keybias.py:90-100; varlen

@@ -24,6 +24,10 @@ SIGNATURES = {
                        i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
                        i64, i64, f32, i32, vp, i64, vp],
     "tg_keybias_fwd_workspace_size": [i32, i32, i32, i32, i32, i32],
+    "tg_keybias_fwd_noalloc": [vp, vp, vp, vp, vp, vp,
+                               i32, i32, i32, i32, i32, i32,
+                               i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64, i64,
+                               i64, i64, f32, i32, vp],
     "tg_keybias_varlen_fwd": [vp, vp, vp, vp, vp, vp, vp,
                               i32, i32, i32, i32, i32, i32,
                               i64, i64, i64, i64, i64, i64, i64, i64,

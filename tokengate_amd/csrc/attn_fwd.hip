@@ -30,6 +30,7 @@
 // fastest, so that consecutive workgroups, which land on different XCDs, keep one KV head per
 // XCD when Hkv is a multiple of 8.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "tg_common.h"
@@ -714,16 +715,18 @@ bool strides_ok(std::initializer_list<int64_t> s) {
 
 using namespace tg;
 
-extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
-                              void *out, float *lse, int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
-                              int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
-                              int64_t q_batch_stride, int64_t q_row_stride, int64_t q_head_stride,
-                              int64_t k_batch_stride, int64_t k_row_stride, int64_t k_head_stride,
-                              int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
-                              int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
-                              int64_t bias_batch_stride, int64_t bias_head_stride, float softmax_scale,
-                              int32_t causal, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
-  clear_error();
+namespace tg {
+namespace {
+// The dense forward behind tg_keybias_fwd and tg_keybias_fwd_noalloc (workspace: the key-range
+// split's partials, or NULL for an unsplit launch).
+int keybias_fwd_dense(const void *q, const void *k, const void *v, const float *bias_raw, void *out, float *lse,
+                      int32_t batch, int32_t seqlen_q, int32_t seqlen_k, int32_t num_heads, int32_t num_heads_k,
+                      int32_t head_dim, int64_t q_batch_stride, int64_t q_row_stride, int64_t q_head_stride,
+                      int64_t k_batch_stride, int64_t k_row_stride, int64_t k_head_stride, int64_t v_batch_stride,
+                      int64_t v_row_stride, int64_t v_head_stride, int64_t o_batch_stride, int64_t o_row_stride,
+                      int64_t o_head_stride, int64_t bias_batch_stride, int64_t bias_head_stride,
+                      float softmax_scale, int32_t causal, void *workspace, int64_t workspace_bytes,
+                      hipStream_t stream) {
   if (int e = check_common(q, k, v, out, lse, num_heads, num_heads_k, head_dim)) return e;
   TG_CHECK(batch >= 0 && seqlen_q >= 0 && seqlen_k >= 0, "negative size");
   TG_CHECK(strides_ok({q_batch_stride, q_row_stride, q_head_stride, k_batch_stride, k_row_stride,
@@ -761,6 +764,89 @@ extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const
   dispatch_fwd<false>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
+}
+
+int64_t fwd_workspace_size(int32_t units_batch, int32_t seqlen_q, int32_t seqlen_k, int32_t num_heads,
+                           int32_t num_heads_k, int32_t causal) {
+  if (units_batch <= 0 || seqlen_q <= 0 || seqlen_k <= 0 || num_heads <= 0 || num_heads_k <= 0 ||
+      num_heads % num_heads_k != 0)
+    return 0;
+  const int hp = ((num_heads / num_heads_k) % 2 == 0) ? 2 : 1;
+  const int64_t units = (int64_t)units_batch * (num_heads / hp);
+  int nw = 8, nq = 0;
+  pick_tiling(hp, seqlen_q, units, nw, nq);
+  return plan_split(nw, hp, nq, units, seqlen_q, seqlen_k, causal != 0).bytes;
+}
+
+// Device scratch of tg_keybias_fwd_noalloc: the key-range split's partial results.  A split is
+// planned only for grids that leave a quarter of the resident-workgroup slots empty, and its
+// chunks fill at most every slot, so it needs at most CUs x 8 waves x 64 lanes x 144 B
+// (18 MiB on a 256-CU MI355X); 24 MiB covers devices of up to 341 CUs.  One copy per device,
+// held until the process ends; every call on a device shares it.
+constexpr int64_t kScratchBytes = 24ll << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[64] = {};
+
+// The device address of this device's scratch, looked up once per device with it current.
+int scratch_address(void **ptr) {
+  int dev = 0;
+  TG_HIP_CHECK(hipGetDevice(&dev));
+  TG_CHECK(dev >= 0 && dev < 64, "device id %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *p = nullptr;
+    TG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    TG_CHECK(p != nullptr && aligned16(p), "scratch address lookup failed");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+}  // namespace tg
+
+extern "C" int tg_keybias_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
+                              void *out, float *lse, int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                              int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                              int64_t q_batch_stride, int64_t q_row_stride, int64_t q_head_stride,
+                              int64_t k_batch_stride, int64_t k_row_stride, int64_t k_head_stride,
+                              int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
+                              int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
+                              int64_t bias_batch_stride, int64_t bias_head_stride, float softmax_scale,
+                              int32_t causal, void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  return keybias_fwd_dense(q, k, v, bias_raw, out, lse, batch, seqlen_q, seqlen_k, num_heads, num_heads_k,
+                           head_dim, q_batch_stride, q_row_stride, q_head_stride, k_batch_stride, k_row_stride,
+                           k_head_stride, v_batch_stride, v_row_stride, v_head_stride, o_batch_stride,
+                           o_row_stride, o_head_stride, bias_batch_stride, bias_head_stride, softmax_scale, causal,
+                           workspace, workspace_bytes, stream);
+}
+
+extern "C" int tg_keybias_fwd_noalloc(const void *q, const void *k, const void *v, const float *bias_raw,
+                                      void *out, float *lse, int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
+                                      int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                                      int64_t q_batch_stride, int64_t q_row_stride, int64_t q_head_stride,
+                                      int64_t k_batch_stride, int64_t k_row_stride, int64_t k_head_stride,
+                                      int64_t v_batch_stride, int64_t v_row_stride, int64_t v_head_stride,
+                                      int64_t o_batch_stride, int64_t o_row_stride, int64_t o_head_stride,
+                                      int64_t bias_batch_stride, int64_t bias_head_stride, float softmax_scale,
+                                      int32_t causal, hipStream_t stream) {
+  clear_error();
+  const int64_t need = fwd_workspace_size(batch, seqlen_q, seqlen_k, num_heads, num_heads_k, causal);
+  TG_CHECK(need <= kScratchBytes,
+           "tg_keybias_fwd_noalloc: this launch's key-range split needs %lld bytes of scratch, above the "
+           "library's static %lld; call tg_keybias_fwd with a workspace instead",
+           (long long)need, (long long)kScratchBytes);
+  void *ws = nullptr;
+  if (need > 0)
+    if (int e = scratch_address(&ws)) return e;
+  return keybias_fwd_dense(q, k, v, bias_raw, out, lse, batch, seqlen_q, seqlen_k, num_heads, num_heads_k,
+                           head_dim, q_batch_stride, q_row_stride, q_head_stride, k_batch_stride, k_row_stride,
+                           k_head_stride, v_batch_stride, v_row_stride, v_head_stride, o_batch_stride,
+                           o_row_stride, o_head_stride, bias_batch_stride, bias_head_stride, softmax_scale, causal,
+                           ws, need, stream);
 }
 
 extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
@@ -814,19 +900,6 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
   return 0;
 }
 
-namespace {
-int64_t fwd_workspace_size(int32_t units_batch, int32_t seqlen_q, int32_t seqlen_k, int32_t num_heads,
-                           int32_t num_heads_k, int32_t causal) {
-  if (units_batch <= 0 || seqlen_q <= 0 || seqlen_k <= 0 || num_heads <= 0 || num_heads_k <= 0 ||
-      num_heads % num_heads_k != 0)
-    return 0;
-  const int hp = ((num_heads / num_heads_k) % 2 == 0) ? 2 : 1;
-  const int64_t units = (int64_t)units_batch * (num_heads / hp);
-  int nw = 8, nq = 0;
-  pick_tiling(hp, seqlen_q, units, nw, nq);
-  return plan_split(nw, hp, nq, units, seqlen_q, seqlen_k, causal != 0).bytes;
-}
-}  // namespace
 
 extern "C" int64_t tg_keybias_fwd_workspace_size(int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
                                                   int32_t num_heads, int32_t num_heads_k, int32_t causal) {
