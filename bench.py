@@ -185,6 +185,10 @@ def bench_gate(dev, iters=50):
         topk_bytes = n_art * 4 + T * 8
         both = (pack_bytes + topk_bytes) / ((ms_topk + ms_pack) * 1e-3) / 1e9
         pair = (pack_bytes + topk_bytes) / (ms_pair * 1e-3) / 1e9
+        # the prefill's path: multi-workgroup selection, then the pack (gate.select_pack)
+        ms_sel = time_graph(lambda: gate.select_pack(scores, p, [], positions=pos, bias_out=bias, keep_out=keep))
+        ms_sp = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
+        sp = (pack_bytes + topk_bytes) / (ms_sp * 1e-3) / 1e9
         res[f"K{K}"] = {"kept": T, "topk_ms": round(ms_topk, 4), "pack_ms": round(ms_pack, 4),
                         "pack_gbs": round(pack_bytes / (ms_pack * 1e-3) / 1e9, 1),
                         "pack_frac_hbm": round(pack_bytes / (ms_pack * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -192,8 +196,51 @@ def bench_gate(dev, iters=50):
                         "topk_plus_pack_frac_hbm": round(both / PEAK_HBM_GBS, 4),
                         "topk_pack_one_graph_ms": round(ms_pair, 4),
                         "topk_pack_one_graph_frac_hbm": round(pair / PEAK_HBM_GBS, 4),
+                        "select_multi_wg_ms": round(ms_sel, 4),
+                        "select_pack_ms": round(ms_sp, 4), "select_pack_gbs": round(sp, 1),
+                        "select_pack_frac_hbm": round(sp / PEAK_HBM_GBS, 4),
                         "bytes": pack_bytes + topk_bytes}
     return res
+
+
+def bench_gate_ragged8(dev):
+    """Top-K + pack at the ragged prefill's scale: 8 prompts of 16k-128k tokens (prefix 64, suffix
+    256), K from {100, 500, 2000, 4000}, bf16-valued scores, the hidden rows (2048 bf16) and 2 layers
+    of K/V (8 x 128 bf16) gathered.  Single-workgroup top-K + pack against the multi-workgroup
+    selection + pack (gate.select_pack); graph-replayed."""
+    import torch
+    from tokengate_amd import gate
+    lens = [114517, 57946, 113394, 80391, 42386, 123699, 106754, 74151]
+    Ks = [2000, 4000, 100, 4000, 100, 100, 4000, 500]
+    starts, ends = [64] * 8, [L - 256 for L in lens]
+    R = sum(lens)
+    row0 = [sum(lens[:b]) for b in range(8)]
+    g = torch.Generator(device=dev).manual_seed(8)
+    scores = torch.randn(R, generator=g, device=dev).to(torch.bfloat16).float()
+    x = torch.randn(R, 2048, generator=g, device=dev).to(torch.bfloat16)
+    kv = [torch.randn(R, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    p = gate.plan(row0, lens, starts, ends, Ks, dev)
+    T = p.total_kept
+    outs = [torch.empty(T, 2048, dtype=torch.bfloat16, device=dev)] + \
+           [torch.empty(T, 8, 128, dtype=torch.bfloat16, device=dev) for _ in kv]
+    pos = torch.empty(T, dtype=torch.int64, device=dev)
+    bias = torch.empty(T, dtype=torch.float32, device=dev)
+    keep = torch.empty(T, dtype=torch.int64, device=dev)
+    ss = torch.empty(8, dtype=torch.float32, device=dev)
+    pairs = list(zip([x] + kv, outs))
+    ms_old = time_graph(lambda: (gate.select_keep(scores, p, keep_out=keep, sumsq_out=ss),
+                                 gate.pack(keep, p, pairs, positions=pos, bias_src=scores, sumsq=ss, bias_out=bias)))
+    ms_topk = time_graph(lambda: gate.select_keep(scores, p, keep_out=keep, sumsq_out=ss))
+    ms_sel = time_graph(lambda: gate.select_pack(scores, p, [], positions=pos, bias_out=bias, keep_out=keep))
+    ms_new = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
+    n_art = sum(e - s for s, e in zip(starts, ends))
+    byts = 2 * T * (2048 * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4) + n_art * 4
+    gbs = lambda ms: byts / (ms * 1e-3) / 1e9
+    return {"kept": T, "lens": lens, "K": Ks, "bytes": byts,
+            "topk_single_wg_ms": round(ms_topk, 4), "topk_pack_ms": round(ms_old, 4),
+            "topk_pack_frac_hbm": round(gbs(ms_old) / PEAK_HBM_GBS, 4),
+            "select_multi_wg_ms": round(ms_sel, 4), "select_pack_ms": round(ms_new, 4),
+            "select_pack_gbs": round(gbs(ms_new), 1), "select_pack_frac_hbm": round(gbs(ms_new) / PEAK_HBM_GBS, 4)}
 
 
 def bench_ttft(dev, reps=5):
@@ -416,6 +463,7 @@ def main():
         del q1, k1, v1, b1
         extra["bwd_8k_b4"] = bench_bwd(dev)
         extra["gate_32k"] = bench_gate(dev)
+        extra["gate_ragged8"] = bench_gate_ragged8(dev)
         if args.cpu_seconds > 0:
             extra["gate_32k"]["cpu_prune_baseline"] = cpu_prune_baseline()
         extra["ttft"] = bench_ttft(dev)

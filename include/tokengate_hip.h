@@ -185,6 +185,33 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
                  const float *bias_src, const float *sumsq, float rms_eps, float *bias_out,
                  hipStream_t stream);
 
+/* tg_gate_topk_keep then tg_gate_pack, with the keep lists selected by many workgroups per
+ * sequence (the reference's per-sample score -> topk -> sort -> cat -> index_select loop,
+ * gate_forward.py:1396-1522, for a whole ragged batch); four stream-ordered launches.  Sequence
+ * b's state span is cut into chunks of 512 * keys_per_thread scores (keys_per_thread 8, 16 or 32)
+ * selected by one workgroup each: wg_start (num_seqs + 1, int32, device) lists them, sequence b
+ * owning chunks [wg_start[b], wg_start[b + 1]) (none when its span is empty, at most 64),
+ * n_select_wgs = wg_start[num_seqs].  Outputs: keep (total_kept, int64, the same lists as
+ * tg_gate_topk_keep), positions_out = keep (optional), bias_out (optional) = the kept state rows'
+ * scores times rsqrt(mean of the span's squared scores + rms_eps), 0 on prefix / suffix rows, and
+ * every stream's rows gathered as tg_gate_pack does.  workspace:
+ * tg_gate_select_pack_workspace_size(seq_capacity, chunk_capacity) bytes, 256-byte aligned,
+ * zero-filled before its first use, for calls of at most seq_capacity sequences and
+ * chunk_capacity chunks (every call on one workspace passes the same capacities: its layout
+ * depends on them alone).  Every call leaves its counters zeroed again, so stream-ordered calls
+ * reuse it without clearing; calls that overlap on one workspace race.  Global word 2 of the
+ * workspace is an error flag no call clears (nonzero: a wait timed out or an internal count was
+ * inconsistent; no row outside a sequence is ever written).  No workgroup waits for one that may
+ * not have started: every call completes whatever the scheduling. */
+int tg_gate_select_pack(const float *scores, const int32_t *geom, const int32_t *wg_start, int32_t num_seqs,
+                        int32_t n_select_wgs, int32_t keys_per_thread, const tg_pack_stream *streams,
+                        int32_t n_streams, int64_t total_kept, int64_t *keep, int64_t *positions_out,
+                        float *bias_out, float rms_eps, void *workspace, int32_t seq_capacity,
+                        int32_t chunk_capacity, hipStream_t stream);
+
+/* Workspace bytes of tg_gate_select_pack for these capacities. */
+int64_t tg_gate_select_pack_workspace_size(int32_t seq_capacity, int32_t chunk_capacity);
+
 /* ---- decoder ops of the gated prefill (Qwen3 layer, transformers 5.x modeling_qwen3.py) ------
  * Called by this library's prefill around the attention; the reference runs them as eager torch
  * modules inside each decoder layer (qwen3_flex_attention.py:533-544 for q/k norm + RoPE). */

@@ -29,11 +29,39 @@ def _run_select(scores_np, seqs, dev):
     return keep.cpu().numpy(), sumsq.cpu().numpy(), p
 
 
+def _check_select_pack(scores_np, seqs, ref, p, dev):
+    """The fused launch (gate.select_pack): keep lists bit-exact, positions, gate bias of the kept
+    rows (float32 chain of the oracle), and a row stream gathered at the kept positions."""
+    from tokengate_amd import gate
+    scores = torch.tensor(scores_np, dtype=torch.float32, device=dev)
+    rows = len(scores_np)
+    src = torch.arange(rows * 8, dtype=torch.int32, device=dev).view(rows, 8)
+    dst = torch.full((p.total_kept, 8), -1, dtype=torch.int32, device=dev)
+    pos = torch.full((p.total_kept,), -7, dtype=torch.int64, device=dev)
+    bias = torch.full((p.total_kept,), float("nan"), dtype=torch.float32, device=dev)
+    keep = gate.select_pack(scores, p, [(src, dst)], positions=pos, bias_out=bias, check=True)
+    torch.cuda.synchronize()
+    k = keep.cpu().numpy()
+    assert np.array_equal(k, ref), "select_pack keep list differs from the oracle"
+    assert np.array_equal(pos.cpu().numpy(), ref)
+    row_of = np.concatenate([seqs[b][0] + ref[p.cu_kept[b]:p.cu_kept[b + 1]] for b in range(len(seqs))]) \
+        if p.total_kept else np.zeros(0, np.int64)
+    assert np.array_equal(dst.cpu().numpy(), src.cpu().numpy()[row_of])
+    bo = bias.cpu().numpy()
+    for b, (r0, L, s_, e, K) in enumerate(seqs):
+        art = scores_np[r0 + s_:r0 + e]
+        if len(art) == 0 or not np.isfinite(art).all() or np.sum(art.astype(np.float64) ** 2) > 1e37:
+            continue
+        want = og.gate_bias(art, ref[p.cu_kept[b]:p.cu_kept[b + 1]], s_, e)
+        np.testing.assert_allclose(bo[p.cu_kept[b]:p.cu_kept[b + 1]], want, rtol=2e-6, atol=1e-30)
+
+
 def _check_select(scores_np, seqs, dev):
     keep, sumsq, p = _run_select(scores_np, seqs, dev)
     ref, starts, kcs = og.select_and_pack(scores_np.astype(np.float64), seqs)
     assert p.k_clamped == kcs and p.cu_kept[:-1] == starts
     assert keep.dtype == np.int64 and np.array_equal(keep, ref)
+    _check_select_pack(scores_np, seqs, ref, p, dev)
     for b, (r0, L, s, e, K) in enumerate(seqs):
         art = scores_np[r0 + s:r0 + e].astype(np.float64)
         art = art[np.isfinite(art)] if not np.isfinite(scores_np).all() else art
@@ -192,6 +220,18 @@ def test_pack_bit_exact_row_and_head_major(cuda):
     ref_bias = np.concatenate([og.gate_bias(sc[x[0] + x[2]:x[0] + x[3]], keep.cpu().numpy()[p.cu_kept[b]:p.cu_kept[b + 1]],
                                             x[2], x[3]) for b, x in enumerate(seqs)])
     assert_close("pack bias", to_np(bias), ref_bias, max_abs=1e-5, rel_l2=1e-6)
+    # the fused launch: the same rows, head-major source included
+    outs2 = [torch.empty_like(t) for t in (hs_out, k_out, v_out)]
+    pos2 = torch.empty_like(pos)
+    bias2 = torch.empty_like(bias)
+    keep2 = gate.select_pack(scores, p, [(hidden, outs2[0]), (k_rows, outs2[1]),
+                                         (v_head_major.transpose(0, 1), outs2[2])],
+                             positions=pos2, bias_out=bias2, check=True)
+    torch.cuda.synchronize()
+    assert torch.equal(keep2, keep) and torch.equal(pos2, pos)
+    for a_, b_ in zip(outs2, (hs_out, k_out, v_out)):
+        assert torch.equal(a_, b_)
+    np.testing.assert_allclose(bias2.cpu().numpy(), bias.cpu().numpy(), rtol=2e-6, atol=0)
 
 
 def _xavier(shape, g, dev):
@@ -234,3 +274,70 @@ def test_config_scoring_and_pruning_32k(cuda, K):
     assert np.array_equal(pos.cpu().numpy(), ref_keep)
     ref_bias = og.gate_bias(scores.cpu().numpy()[s:e].astype(np.float64), ref_keep, s, e)
     assert_close("bias", to_np(bias), ref_bias, max_abs=1e-5, rel_l2=1e-6)
+    # the fused launch on the same workload
+    outs2 = [torch.empty_like(t) for t in outs]
+    pos2, bias2 = torch.empty_like(pos), torch.empty_like(bias)
+    keep2 = gate.select_pack(scores, p, list(zip([x] + kv, outs2)), positions=pos2, bias_out=bias2, check=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(keep2.cpu().numpy(), ref_keep) and torch.equal(pos2, pos)
+    for a_, b_ in zip(outs2, outs):
+        assert torch.equal(a_, b_)
+    assert_close("fused bias", to_np(bias2), ref_bias, max_abs=1e-5, rel_l2=1e-6)
+
+
+def test_ragged8_select_pack(cuda):
+    """The ragged pruned-prefill batch at full size: 8 prompts of 16k-128k tokens (prefix 64,
+    suffix 256), K from {100, 500, 2000, 4000}, bf16-valued scores (ties at every threshold), the
+    hidden rows (2048 bf16) and two layers of K/V (8 x 128 bf16) gathered; keep lists, positions
+    and rows bit-exact, bias against the oracle's float32 chain."""
+    from tokengate_amd import gate
+    rng = np.random.default_rng(8)
+    lens = [int(x) for x in rng.integers(16384, 131073, size=8)]
+    Ks = [int(x) for x in rng.choice([100, 500, 2000, 4000], size=8)]
+    seqs, r0 = [], 0
+    for L, K in zip(lens, Ks):
+        seqs.append((r0, L, 64, L - 256, K))
+        r0 += L
+    print(f"[ragged8] lens={lens} K={Ks}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(8)
+    scores = torch.randn(r0, generator=g, device=cuda).to(torch.bfloat16).float()
+    hidden = torch.randn(r0, 2048, generator=g, device=cuda).to(torch.bfloat16)
+    kv = [torch.randn(r0, 8, 128, generator=g, device=cuda).to(torch.bfloat16) for _ in range(4)]
+    p = gate.plan([x[0] for x in seqs], lens, [x[2] for x in seqs], [x[3] for x in seqs], Ks, cuda)
+    T = p.total_kept
+    outs = [torch.empty(T, 2048, dtype=torch.bfloat16, device=cuda)] + \
+           [torch.empty(T, 8, 128, dtype=torch.bfloat16, device=cuda) for _ in kv]
+    pos = torch.empty(T, dtype=torch.int64, device=cuda)
+    bias = torch.empty(T, dtype=torch.float32, device=cuda)
+    keep = gate.select_pack(scores, p, list(zip([hidden] + kv, outs)), positions=pos, bias_out=bias, check=True)
+    torch.cuda.synchronize()
+    sc = scores.cpu().numpy()
+    ref, starts, kcs = og.select_and_pack(sc, seqs)
+    assert np.array_equal(keep.cpu().numpy(), ref) and np.array_equal(pos.cpu().numpy(), ref)
+    rows = torch.from_numpy(np.concatenate([x[0] + ref[p.cu_kept[b]:p.cu_kept[b + 1]]
+                                            for b, x in enumerate(seqs)])).to(cuda)
+    for src, out in zip([hidden] + kv, outs):
+        assert torch.equal(out, src.index_select(0, rows))
+    ref_bias = np.concatenate([og.gate_bias(sc[x[0] + x[2]:x[0] + x[3]], ref[p.cu_kept[b]:p.cu_kept[b + 1]], x[2], x[3])
+                               for b, x in enumerate(seqs)])
+    np.testing.assert_allclose(bias.cpu().numpy(), ref_bias, rtol=2e-6, atol=0)
+
+
+def test_select_pack_workspace_reuse_across_batch_sizes(cuda):
+    """Stream-ordered select_pack calls of different batch sizes share one workspace: its counters
+    sit at offsets fixed by the capacities, so a call after a smaller one starts from zeroed
+    counters (the regression: a layout that moved with the batch size let a later call read the
+    previous call's records as counters).  Every call bit-exact; the error flag stays clear."""
+    rng = np.random.default_rng(12)
+    for nseq in (3, 8, 1, 6, 2, 8):
+        seqs, r0 = [], 0
+        for _ in range(nseq):
+            L = int(rng.integers(300, 20000))
+            s = int(rng.integers(0, 200))
+            e = int(rng.integers(s + 1, L + 1))
+            seqs.append((r0, L, s, e, int(rng.choice([1, 100, 500, 2000, 10_000_000]))))
+            r0 += L
+        scores = rng.standard_normal(r0).astype(np.float32)
+        p = _run_select(scores, seqs, cuda)[2]
+        ref, _, _ = og.select_and_pack(scores.astype(np.float64), seqs)
+        _check_select_pack(scores, seqs, ref, p, cuda)

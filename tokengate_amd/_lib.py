@@ -38,6 +38,8 @@ SIGNATURES = {
     "tg_gate_score_mlp": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
     "tg_gate_topk_keep": [vp, vp, i32, i32, vp, vp, vp],
     "tg_gate_pack": [vp, i32, vp, vp, i32, i64, vp, vp, vp, f32, vp, vp],
+    "tg_gate_select_pack": [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, vp, vp, f32, vp, i32, i32, vp],
+    "tg_gate_select_pack_workspace_size": [i32, i32],
     "tg_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, f32, vp],
     "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp],
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
@@ -45,7 +47,7 @@ SIGNATURES = {
     "tg_lm_head": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,
-            "tg_keybias_varlen_fwd_workspace_size": C.c_int64}
+            "tg_keybias_varlen_fwd_workspace_size": C.c_int64, "tg_gate_select_pack_workspace_size": C.c_int64}
 
 
 def lib_path(site: str = None) -> str:
@@ -81,6 +83,9 @@ def fwd_workspace(size_fn: str, device, *size_args):
     import torch
     ws = torch.empty(n, dtype=torch.uint8, device=device)
     return ws, ws.data_ptr(), n
+
+
+SELECT_PACK_ERROR_OFFSET = 8   # byte offset of tg_gate_select_pack's wait-timeout flag (global word 2)
 
 
 def call(name: str, *args) -> None:

@@ -46,6 +46,9 @@ class KeepPlan:
     k_clamped: List[int]
     cu_kept: List[int]             # nseq + 1 (the packed Phase-2 cu_seqlens)
     max_article: int
+    sel_kpt: int = 0               # select_pack: keys per thread (0: spans too long for it)
+    sel_starts: Optional[List[int]] = None        # select_pack: first chunk of each sequence (nseq + 1)
+    sel_starts_dev: Optional[torch.Tensor] = None   # the same, on the device
 
     @property
     def total_kept(self) -> int:
@@ -73,9 +76,13 @@ def plan(row_starts: Sequence[int], seq_lens: Sequence[int], art_starts: Sequenc
     if cu[-1] >= 2 ** 31:
         raise ValueError("more than 2^31 kept rows")
     gh = torch.tensor(rows, dtype=torch.int32).reshape(n, 6)
-    gd = gh.pin_memory().to(device, non_blocking=True) if torch.device(device).type == "cuda" else gh
     max_art = max((int(art_ends[b]) - int(art_starts[b]) for b in range(n)), default=0)
-    return KeepPlan(gh, gd, n_kept, kcs, cu, max_art)
+    kpt, starts = _select_layout([r[3] - r[2] for r in rows])
+    # one host-to-device copy: the geometry table and select_pack's chunk starts
+    both = torch.cat([gh.reshape(-1), torch.tensor(starts if starts else [0], dtype=torch.int32)])
+    bd = both.pin_memory().to(device, non_blocking=True) if torch.device(device).type == "cuda" else both
+    gd = bd[:6 * n].view(n, 6)
+    return KeepPlan(gh, gd, n_kept, kcs, cu, max_art, kpt, starts, bd[6 * n:] if starts else None)
 
 
 def select_keep(scores: torch.Tensor, p: KeepPlan, with_sumsq: bool = True,
@@ -100,6 +107,87 @@ def select_keep(scores: torch.Tensor, p: KeepPlan, with_sumsq: bool = True,
         _lib.call("tg_gate_topk_keep", scores.data_ptr(), p.geom.data_ptr(), len(p.n_kept), p.max_article,
                   keep.data_ptr(), sumsq.data_ptr() if sumsq is not None else None, _stream(scores))
     return keep, sumsq
+
+
+_SEL_WS = {}          # (device index, stream) -> zero-initialised select-pack workspace (uint8)
+_SEL_KPT = (8, 16, 32)
+_SEL_MAX_CHUNKS = 64
+
+
+def _select_layout(n_art: Sequence[int]):
+    """Keys per thread and per-sequence chunk starts of tg_gate_select_pack for spans of these
+    lengths, or (0, None) when a span needs more than 64 chunks of the largest size."""
+    for kpt in _SEL_KPT:
+        chunk = 512 * kpt
+        g = [(n + chunk - 1) // chunk if n > 0 else 0 for n in n_art]
+        if max(g, default=0) <= _SEL_MAX_CHUNKS:
+            starts = [0]
+            for x in g:
+                starts.append(starts[-1] + x)
+            return kpt, starts
+    return 0, None
+
+
+def _sel_workspace(device, stream: int, nseq: int, n_chunks: int):
+    """(workspace, seq_capacity, chunk_capacity) for this device and stream, zero-filled when
+    created.  Its layout depends on the capacities alone and the kernels leave its counters
+    zeroed after every call, so it is reused as is while the batch fits; a larger batch gets a
+    new zeroed one with doubled capacities."""
+    key = (torch.device(device).index, stream)
+    ent = _SEL_WS.get(key)
+    if ent is None or ent[1] < nseq or ent[2] < n_chunks:
+        seq_cap = max(64, nseq, 2 * ent[1] if ent else 0)
+        chunk_cap = max(512, n_chunks, 2 * ent[2] if ent else 0)
+        nbytes = int(_lib.load().tg_gate_select_pack_workspace_size(seq_cap, chunk_cap))
+        ent = (torch.zeros(nbytes, dtype=torch.uint8, device=device), seq_cap, chunk_cap)
+        _SEL_WS[key] = ent
+    return ent
+
+
+def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]] = (),
+                positions: Optional[torch.Tensor] = None, bias_out: Optional[torch.Tensor] = None,
+                keep_out: Optional[torch.Tensor] = None, rms_eps: float = RMS_EPS,
+                check: bool = False) -> torch.Tensor:
+    """select_keep and pack with the keep lists selected by many workgroups per state span
+    (tg_gate_select_pack): the keep lists of every sequence (returned, int64, packed), the rows of
+    every (src, dst) pair gathered at them, the kept positions and the kept rows' RMS-normalised
+    gate bias.  Spans beyond its limits (more than 64 x 16384 scores) run select_keep then pack.
+    check: read back the wait-timeout flag (a host synchronisation) and raise if it is set."""
+    if scores.dtype != torch.float32 or scores.dim() != 1 or not scores.is_contiguous():
+        raise RuntimeError("scores must be a contiguous 1-D float32 tensor")
+    keep = keep_out if keep_out is not None else torch.empty(p.total_kept, dtype=torch.int64, device=scores.device)
+    if keep.dtype != torch.int64 or keep.numel() < p.total_kept or not keep.is_contiguous():
+        raise RuntimeError("keep_out must be contiguous int64 with room for every kept row")
+    if len(pairs) > 16:
+        raise RuntimeError("select_pack: at most 16 row streams per launch")
+    for t, dt in ((positions, torch.int64), (bias_out, torch.float32)):
+        if t is not None and (t.dtype != dt or not t.is_contiguous()):
+            raise RuntimeError("select_pack: positions must be contiguous int64, bias_out contiguous float32")
+    arr = (PackStream * max(1, len(pairs)))()
+    for i, (src, dst) in enumerate(pairs):
+        if dst.shape[0] < p.total_kept:
+            raise RuntimeError("select_pack: destination has fewer rows than kept tokens")
+        arr[i] = _row_stream(src, dst)
+    if p.total_kept == 0:
+        return keep
+    if not p.sel_kpt:
+        k2, sumsq = select_keep(scores, p, keep_out=keep)
+        pack(k2, p, pairs, positions=positions, bias_src=scores, sumsq=sumsq, bias_out=bias_out, rms_eps=rms_eps)
+        return k2
+    kpt, starts, st_d = p.sel_kpt, p.sel_starts, p.sel_starts_dev
+    nseq = len(p.n_kept)
+    stream = _stream(scores)
+    ws, seq_cap, chunk_cap = _sel_workspace(scores.device, stream, nseq, starts[-1])
+    _lib.call("tg_gate_select_pack", scores.data_ptr(), p.geom.data_ptr(), st_d.data_ptr(), nseq, starts[-1], kpt,
+              ctypes.cast(arr, ctypes.c_void_p), len(pairs), p.total_kept, keep.data_ptr(),
+              positions.data_ptr() if positions is not None else None,
+              bias_out.data_ptr() if bias_out is not None else None, float(rms_eps), ws.data_ptr(), seq_cap, chunk_cap,
+              stream)
+    if check:
+        off = _lib.SELECT_PACK_ERROR_OFFSET
+        if int(ws[off:off + 4].view(torch.int32).item()):
+            raise RuntimeError("tg_gate_select_pack: error flag set (a wait timed out or a count was inconsistent)")
+    return keep
 
 
 def _row_stream(src: torch.Tensor, dst: torch.Tensor) -> PackStream:

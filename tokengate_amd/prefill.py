@@ -16,7 +16,8 @@ and the gate layer's own MLP runs on the packed kept rows only, at Phase-2 entry
 
 MI355X layout: the batch is never padded.  Phase 1 packs all prompts back to back (cu_seqlens)
 and runs one varlen attention launch per layer; the keep lists of all sequences come from one
-top-K launch and every gather from one pack launch; Phase 2 runs the packed kept rows, with
+multi-workgroup selection (gate.select_pack: every state span cut into chunks of 4096 scores) and
+every gather from one pack launch; Phase 2 runs the packed kept rows, with
 the -1e9 pad-slot bias of the reference replaced by the cu_seqlens boundaries.  Every size is
 known on the host from the prompt lengths, spans and K, so nothing synchronises before the
 first token.
@@ -182,16 +183,15 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
                    attn_only_last=split)
     del x
 
-    mark("score+select")
+    mark("score")
     if split:
         scores = head.scores_from_boundary(h, wts.layers[gate_layer].ln2, shape.rms_eps, normed=ws1.normed,
                                            chunk_rows=mlp_rows)
     else:
         scores = head.scores(h)
-    p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
-    keep, sumsq = G.select_keep(scores, p)
 
-    mark("pack")
+    mark("select+pack")
+    p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
     T2 = p.total_kept
     hs = torch.empty(T2, shape.d_model, dtype=h.dtype, device=dev)
     kept_pos = torch.empty(T2, dtype=torch.int64, device=dev)
@@ -202,7 +202,7 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
             nk = alloc_kv(shape, T2, dev)
             pairs += [(kv[i].k, nk.k), (kv[i].v, nk.v)]
             kv[i] = nk
-    G.pack(keep, p, pairs, positions=kept_pos, bias_src=scores, sumsq=sumsq, bias_out=kept_bias)
+    keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias)
     if cap is not None:
         cap["h1"] = h
     del h, ws1, pairs
