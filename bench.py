@@ -253,7 +253,8 @@ def bench_ttft(dev, reps=5):
     runs the finalized gate instead: the MLP scoring branch (a copy of the gate layer's SwiGLU, I
     6144, with an absorbed (1, I) readout row) on the gate layer's attention boundary, the gate
     layer's MLP on the kept rows only, scaled softmax in Phase 2.  decode_ms_per_token (32k, K=2000
-    and K=all): greedy decode steps after the prefill, median of 8 after 2 warmup steps."""
+    and K=all, ragged8): greedy decode steps after a prefill run with 16 rows of decode headroom in
+    every cache, median of 8 after 2 warmup steps."""
     import statistics
     import torch
     from tokengate_amd import decoder as dec
@@ -290,7 +291,9 @@ def bench_ttft(dev, reps=5):
         ends = [n - 256 for n in lens]
         fn = lambda: P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
         times = P.ttft_ms(fn, reps=reps, warmup=1)
-        r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, phase_timing=True)
+        # the measured prefill leaves decode headroom in every cache (decode appends in place)
+        r = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, phase_timing=True,
+                            decode_headroom=16 if decode else 0)
         out[name] = {"ttft_ms": round(statistics.median(times), 3), "reps_ms": [round(t, 3) for t in times],
                      "prompt_tokens": sum(lens), "kept_tokens": r.cu_kept[-1],
                      "phase_ms": {k: round(v, 3) for k, v in r.phase_ms.items()}}
@@ -318,7 +321,7 @@ def bench_ttft(dev, reps=5):
     rng = torch.Generator().manual_seed(17)
     lens = [int(x) for x in torch.randint(16384, 131073, (8,), generator=rng)]
     Ks = [[100, 500, 2000, 4000][int(i)] for i in torch.randint(0, 4, (8,), generator=rng)]
-    run("ragged8", lens, Ks)
+    run("ragged8", lens, Ks, decode=True)
     del wts
     torch.cuda.empty_cache()
     return out

@@ -106,6 +106,36 @@ int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const flo
 int64_t tg_keybias_varlen_fwd_workspace_size(int32_t num_seqs, int32_t max_seqlen,
                                              int32_t num_heads, int32_t num_heads_k, int32_t causal);
 
+/* Variable-length forward with the keys of each sequence stored apart from its queries: the
+ * general form of the same ext().varlen_fwd binding, whose cu_seqlens_k and seqused_k arguments
+ * the reference's own call leaves at cu and None (kernels/fa2bias/keybias.py:90-100).  Query rows
+ * of sequence b are cu_seqlens_q[b] .. cu_seqlens_q[b + 1] - 1 (at most max_seqlen_q of them);
+ * its keys are k / v rows cu_seqlens_k[b] .. cu_seqlens_k[b] + n_b - 1 with n_b = seqused_k[b]
+ * (seqused_k NULL: n_b = cu_seqlens_k[b + 1] - cu_seqlens_k[b]), at most max_seqlen_k.  Causal
+ * masking is bottom-right aligned (query i of m sees keys j <= i + n_b - m).  bias_raw
+ * (num_seqs, H, >= max_seqlen_k) fp32, column j = key j of the sequence.  lse (H, total_q).
+ * This is the layout of a KV cache with room for generated tokens after every sequence: the
+ * gated prefill's Phase 2 writes its kept rows there and every decode step attends over it for
+ * all sequences in one launch (the reference's decode attention over its pruned, padded cache,
+ * qwen3_flex_attention.py:978-1117, gate_decode.py:143-235).  workspace: sized by
+ * tg_keybias_varlen_kv_fwd_workspace_size(). */
+int tg_keybias_varlen_kv_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
+                             void *out, float *lse, const int32_t *cu_seqlens_q,
+                             const int32_t *cu_seqlens_k, const int32_t *seqused_k, int32_t num_seqs,
+                             int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t total_q,
+                             int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                             int64_t q_row_stride, int64_t q_head_stride,
+                             int64_t k_row_stride, int64_t k_head_stride,
+                             int64_t v_row_stride, int64_t v_head_stride,
+                             int64_t o_row_stride, int64_t o_head_stride,
+                             int64_t bias_seq_stride, int64_t bias_head_stride,
+                             float softmax_scale, int32_t causal,
+                             void *workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes tg_keybias_varlen_kv_fwd uses for these sizes on the current device. */
+int64_t tg_keybias_varlen_kv_fwd_workspace_size(int32_t num_seqs, int32_t max_seqlen_q, int32_t max_seqlen_k,
+                                                int32_t num_heads, int32_t num_heads_k, int32_t causal);
+
 /* Dense key-bias attention backward.
  * Replaces ext().bwd(dout, q, k, v, out, lse, None, None, None, bias_raw, 0.0, scale, causal,
  * -1, -1, 0.0, False, None, None) -> (dq, dk, dv, softmax_d, dbias) (kernels/fa2bias/keybias.py:52-63;
@@ -171,6 +201,9 @@ typedef struct tg_pack_stream {
   int64_t src_chunk_stride;
   int32_t chunk_bytes;
   int32_t n_chunks;
+  int64_t dst_seq_gap;   /* rows left free after each sequence's destination rows: kept row j of
+                            sequence b goes to destination row j + b * dst_seq_gap (0: back to
+                            back) -- a KV cache with room for generated tokens */
 } tg_pack_stream;
 
 /* Ragged gather of the kept rows (gate_forward.py:1454-1522: hs_pruned, kept_positions,
@@ -232,13 +265,15 @@ int tg_rmsnorm(const void *x, int64_t x_row_stride, const void *residual, int64_
  * positions[t] (int64): angle_i = float(positions[t]) * inv_freq[i] (fp32, i < 64); q head h ->
  * q_out row t (may alias qkv); where q_head_scale / q_row_scale are non-NULL the rotated query,
  * rounded to bf16, is multiplied by s = bf16(q_head_scale[h] * q_row_scale[t]) (a missing factor
- * is 1) and rounded again — the reference's bf16 q * s_eff; k head g -> k_out row t (the layer's KV cache, (rows, num_heads_k, 128)); v head g copied to
- * v_out row t. */
+ * is 1) and rounded again — the reference's bf16 q * s_eff; k head g -> k_out row c and v head g
+ * copied to v_out row c (the layer's KV cache, (rows, num_heads_k, 128)), with c = kv_rows[t]
+ * (int32) when kv_rows is non-NULL (a cache with free rows after each sequence), else c = t. */
 int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const int64_t *positions, int64_t n_tokens,
                     int32_t num_heads, int32_t num_heads_k, int32_t head_dim, const void *q_norm_weight,
                     const void *k_norm_weight, float eps, const float *inv_freq, const float *q_head_scale,
                     const float *q_row_scale, void *q_out, int64_t q_row_stride, void *k_out,
-                    int64_t k_row_stride, void *v_out, int64_t v_row_stride, hipStream_t stream);
+                    int64_t k_row_stride, void *v_out, int64_t v_row_stride, const int32_t *kv_rows,
+                    hipStream_t stream);
 
 /* out[r, i] = bf16(silu(gate_up[r, i]) * gate_up[r, inter + i]) (Qwen3MLP act_fn(gate) * up on
  * the fused gate/up projection). */

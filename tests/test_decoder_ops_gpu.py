@@ -85,6 +85,19 @@ def test_qk_norm_rope(cuda, T, H, Hkv, maxpos, scaled):
     assert torch.equal(v.view(T, -1), qkv0[:, (H + Hkv) * D:])
     assert torch.equal(qkv[:, H * D:], qkv0[:, H * D:])          # k/v columns untouched
     assert q.data_ptr() == qkv.data_ptr()                         # q rotated in place
+    # k / v rows written to a cache through a row map (rows t -> 3t + 1 of a larger cache)
+    rows = torch.arange(T, dtype=torch.int32, device=cuda) * 3 + 1
+    kc = torch.zeros(3 * T + 2, Hkv, D, dtype=torch.bfloat16, device=cuda)
+    vc = torch.zeros_like(kc)
+    qkv2 = qkv0.clone()
+    q2 = dec.qk_norm_rope(qkv2, pos, lw, shape, inv, kc, vc, qs, rs, kv_rows=rows)
+    torch.cuda.synchronize()
+    assert torch.equal(q2, q)
+    ri = rows.long()
+    assert torch.equal(kc.index_select(0, ri), k) and torch.equal(vc.index_select(0, ri), v)
+    others = torch.ones(3 * T + 2, dtype=torch.bool, device=cuda)
+    others[ri] = False
+    assert bool((kc[others] == 0).all()) and bool((vc[others] == 0).all())
 
 
 @pytest.mark.parametrize("rows,inter", [(1, 8), (1000, 6144), (37, 1000)])

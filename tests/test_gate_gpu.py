@@ -232,6 +232,29 @@ def test_pack_bit_exact_row_and_head_major(cuda):
     for a_, b_ in zip(outs2, (hs_out, k_out, v_out)):
         assert torch.equal(a_, b_)
     np.testing.assert_allclose(bias2.cpu().numpy(), bias.cpu().numpy(), rtol=2e-6, atol=0)
+    # destinations with free rows after each sequence (a KV cache with decode headroom): kept row j
+    # of sequence b lands on row j + b * gap, the free rows keep their contents
+    gap = 5
+    nseq = len(seqs)
+    for fused in (False, True):
+        kg = torch.full((T + nseq * gap, 8, 128), 7.0, dtype=torch.bfloat16, device=cuda)
+        vg = torch.full_like(kg, 7.0)
+        hg = torch.empty_like(hs_out)
+        pairs = [(hidden, hg), (k_rows, kg, gap), (v_head_major.transpose(0, 1), vg, gap)]
+        if fused:
+            gate.select_pack(scores, p, pairs, check=True)
+        else:
+            gate.pack(keep, p, pairs)
+        torch.cuda.synchronize()
+        assert torch.equal(hg, hs_out)
+        for b in range(nseq):
+            c0, c1 = p.cu_kept[b], p.cu_kept[b + 1]
+            assert torch.equal(kg[c0 + b * gap:c1 + b * gap], k_out[c0:c1])
+            assert torch.equal(vg[c0 + b * gap:c1 + b * gap], v_out[c0:c1])
+            assert bool((kg[c1 + b * gap:c1 + (b + 1) * gap] == 7.0).all())
+            assert bool((vg[c1 + b * gap:c1 + (b + 1) * gap] == 7.0).all())
+    with pytest.raises(RuntimeError, match="fewer rows"):
+        gate.pack(keep, p, [(k_rows, torch.empty(T + gap, 8, 128, dtype=torch.bfloat16, device=cuda), gap)])
 
 
 def _xavier(shape, g, dev):

@@ -40,18 +40,24 @@ def _prompts(lens, spans, seed):
     return out
 
 
-@pytest.mark.parametrize("prune_below_gate,ssmax,branch", [(False, False, False), (True, False, False),
-                                                             (False, True, False), (True, True, True)])
-def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch):
+@pytest.mark.parametrize("prune_below_gate,ssmax,branch,headroom", [
+    (False, False, False, True), (True, False, False, True), (False, True, False, True), (True, True, True, True),
+    (False, True, False, False), (True, False, False, False)])
+def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom):
+    """Greedy decode steps against the oracle, appending in place to the prefill's caches (headroom)
+    or to a copy laid out with room (a prefill without headroom)."""
     from tokengate_amd import inference as I
     from tokengate_amd.decode import DecodeState
     torch.set_num_threads(min(16, torch.get_num_threads()))
     m = _model(cuda, ssmax=ssmax, branch=branch)
     lens, spans, Ks = [600, 333], [(20, 500), (0, 300)], [64, 1000]
     split = [I.split_state_span(p) for p in _prompts(lens, spans, 5)]
-    pf = m.prefill(split, Ks, prune_below_gate=prune_below_gate)
     steps = 4
+    pf = m.prefill(split, Ks, prune_below_gate=prune_below_gate, decode_headroom=steps + 1 if headroom else 0)
     st = DecodeState(m.weights, m.gate, m.gate_layer, pf, steps + 1, prune_below_gate)
+    assert st.in_place == headroom
+    if headroom:
+        assert all(st.kv[l].k.data_ptr() == pf.kv[l].k.data_ptr() for l in range(len(st.kv)))
     cur = pf.first_tokens
     toks, logits = [cur], []
     for _ in range(steps):

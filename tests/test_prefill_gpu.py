@@ -231,6 +231,47 @@ def test_prefill_prune_below_gate(cuda):
         assert torch.equal(pruned.kv[i].k, full.kv[i].k)
 
 
+@pytest.mark.parametrize("prune_below_gate,graphs", [(False, False), (True, False), (False, True)])
+def test_prefill_decode_headroom_layout(cuda, prune_below_gate, graphs):
+    """decode_headroom lays every cache out with free rows after each sequence: the same bits as
+    the back-to-back layout (first tokens, logits, every cache row), each sequence's rows at
+    cu[b] + b * gap, and the Phase-2 bias by sequence zero past its kept rows."""
+    from tokengate_amd import prefill as P
+    lens, starts, ends, Ks = CASES["ragged3"]
+    shape, wts, head = _setup(cuda, seed=4)
+    g = torch.Generator().manual_seed(14)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    gap = 7
+    gr = P.Phase2Graphs() if graphs else None
+    base = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, prune_below_gate=prune_below_gate,
+                           phase2_graphs=gr)
+    base_kv = [(kv.k.clone(), kv.v.clone()) for kv in base.kv]
+    base_logits = base.logits.clone()
+    hr = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks, prune_below_gate=prune_below_gate,
+                         phase2_graphs=gr, decode_headroom=gap)
+    torch.cuda.synchronize()
+    B = len(lens)
+    assert hr.decode_headroom == gap and hr.cache_below is not None and hr.cache_above is not None
+    assert torch.equal(hr.first_tokens, base.first_tokens)
+    assert torch.equal(hr.logits, base_logits)
+    for l in range(shape.n_layers):
+        cu = (base.cu_prompt if (l <= 1 and not prune_below_gate) else base.cu_kept)
+        cg = hr.cache_below if l <= 1 else hr.cache_above
+        assert cg.seg == [cu[b] + b * gap for b in range(B + 1)]
+        assert hr.kv[l].k.shape[0] >= cu[-1] + B * gap
+        for b in range(B):
+            s0 = cu[b] + b * gap
+            n = cu[b + 1] - cu[b]
+            assert torch.equal(hr.kv[l].k[s0:s0 + n], base_kv[l][0][cu[b]:cu[b + 1]]), f"layer {l} seq {b} k"
+            assert torch.equal(hr.kv[l].v[s0:s0 + n], base_kv[l][1][cu[b]:cu[b + 1]]), f"layer {l} seq {b} v"
+    bs = hr.phase2_bias_seq
+    assert bs.shape == (shape.n_layers - 2, B, shape.n_heads, max(hr.n_kept) + gap)
+    for b in range(B):
+        n = hr.n_kept[b]
+        assert torch.equal(bs[:, b, :, :n], hr.phase2_bias[:, :, hr.cu_kept[b]:hr.cu_kept[b + 1]])
+        assert bool((bs[:, b, :, n:] == 0).all())
+
+
 def test_phase2_graph_replay_matches_oracle(cuda):
     """Phase 2 replayed from captured graphs (bucketed rows / lengths): three batches of one
     geometry with different tokens and a second model of the same geometry, eager work and

@@ -33,6 +33,11 @@ SIGNATURES = {
                               i64, i64, i64, i64, i64, i64, i64, i64,
                               i64, i64, f32, i32, vp, i64, vp],
     "tg_keybias_varlen_fwd_workspace_size": [i32, i32, i32, i32, i32],
+    "tg_keybias_varlen_kv_fwd": [vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                 i32, i32, i32, i32, i32, i32, i32,
+                                 i64, i64, i64, i64, i64, i64, i64, i64,
+                                 i64, i64, f32, i32, vp, i64, vp],
+    "tg_keybias_varlen_kv_fwd_workspace_size": [i32, i32, i32, i32, i32, i32],
     "tg_keybias_bwd": [vp] * 12 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_keybias_varlen_bwd": [vp] * 13 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_gate_score_mlp": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
@@ -41,13 +46,15 @@ SIGNATURES = {
     "tg_gate_select_pack": [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, vp, vp, f32, vp, i32, i32, vp],
     "tg_gate_select_pack_workspace_size": [i32, i32],
     "tg_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, f32, vp],
-    "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp],
+    "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp,
+                        vp],
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
     "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
     "tg_lm_head": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,
-            "tg_keybias_varlen_fwd_workspace_size": C.c_int64, "tg_gate_select_pack_workspace_size": C.c_int64}
+            "tg_keybias_varlen_fwd_workspace_size": C.c_int64, "tg_keybias_varlen_kv_fwd_workspace_size": C.c_int64,
+            "tg_gate_select_pack_workspace_size": C.c_int64}
 
 
 def lib_path(site: str = None) -> str:

@@ -58,7 +58,11 @@ struct FwdArgs {
   const float *bias;
   bf16_t *o;
   float *lse;
-  const int32_t *cu_seqlens;   // varlen only
+  const int32_t *cu_seqlens;   // varlen only: query rows of sequence b are cu_seqlens[b] .. [b+1]-1
+  // varlen key geometry when the keys live elsewhere (a cache with room after each sequence):
+  // keys of sequence b are rows cu_k[b] .. cu_k[b] + used_k[b] - 1 (used_k NULL: cu_k[b + 1] - 1);
+  // cu_k NULL: the keys are the query rows
+  const int32_t *cu_k, *used_k;
   int64_t q_bs, q_rs, q_hs, k_bs, k_rs, k_hs, v_bs, v_rs, v_hs, o_bs, o_rs, o_hs;
   int64_t bias_bs, bias_hs;
   int64_t lse_total;           // varlen: total rows (lse is (H, total)); dense: unused
@@ -167,21 +171,28 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   const int qt = a.n_qtiles - 1 - rank;
 
   int sq = a.sq, sk = a.sk;
-  int64_t row0 = 0;
+  int64_t row0 = 0, krow0 = 0;
   if constexpr (VARLEN) {
     const int s0 = a.cu_seqlens[b], s1 = a.cu_seqlens[b + 1];
     row0 = s0;
     sq = min(s1 - s0, a.sq);   // rows past max_seqlen are outside the bias row: not computed
-    sk = sq;
+    if (a.cu_k != nullptr) {
+      krow0 = a.cu_k[b];
+      const int nk = a.used_k != nullptr ? a.used_k[b] : a.cu_k[b + 1] - a.cu_k[b];
+      sk = max(0, min(nk, a.sk));
+    } else {
+      krow0 = row0;
+      sk = sq;
+    }
   }
   const int q0 = qt * BM;
   if (q0 >= sq) return;   // workgroup-uniform: past the end of this sequence
-  const int off = sk - sq;
+  const int off = sk - sq;   // causal: query i sees keys j <= i + off (bottom-right aligned)
   const int h0 = kh * a.group + hg * HP;
 
   const bf16_t *qbase = a.q + (VARLEN ? row0 * a.q_rs : (int64_t)b * a.q_bs) + (int64_t)h0 * a.q_hs;
-  const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
-  const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
+  const bf16_t *kbase = a.k + (VARLEN ? krow0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
+  const bf16_t *vbase = a.v + (VARLEN ? krow0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
   bf16_t *obase = a.o + (VARLEN ? row0 * a.o_rs : (int64_t)b * a.o_bs) + (int64_t)h0 * a.o_hs;
 
   // Buffer descriptors: exactly the bytes of rows [0, sk) of this (sequence, kv head).
@@ -189,9 +200,12 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   const uint32_t vspan = sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.v_rs + kD) * 2) : 0u;
   const brsrc_t krs = make_rsrc(kbase, kspan);
   const brsrc_t vrs = make_rsrc(vbase, vspan);
-  const float *bbase = HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)h0 * a.bias_hs : nullptr;
-  const brsrc_t brs =
-      make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
+  // the bias row of head h0 + w is loaded by wave w < HP, through a descriptor of exactly its sk
+  // columns: columns past the sequence's keys read as 0 (whatever the table holds there)
+  const int bwave = __builtin_amdgcn_readfirstlane(wave < HP ? wave : 0);
+  const float *bbase =
+      HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)(h0 + bwave) * a.bias_hs : nullptr;
+  const brsrc_t brs = make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)sk * 4u : 0u);
 
   // ---- this wave's queries and its Q fragments (B operand of S^T = K Q^T, 32 d per k-step) ----
   const int qw0 = q0 + wave * QW;
@@ -248,7 +262,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     }
     if constexpr (HAS_BIAS) {
       if (wave < HP)
-        dma4(brs, &bslot(buf_c)[wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
+        dma4(brs, &bslot(buf_c)[wave][0], (uint32_t)((tile * kBN + lane) * 4));
     }
   };
 
@@ -849,6 +863,67 @@ extern "C" int tg_keybias_fwd_noalloc(const void *q, const void *k, const void *
                            ws, need, stream);
 }
 
+namespace tg {
+namespace {
+// The varlen forward behind tg_keybias_varlen_fwd (keys = the query rows) and
+// tg_keybias_varlen_kv_fwd (keys at cu_k / used_k).
+int keybias_fwd_varlen(const void *q, const void *k, const void *v, const float *bias_raw, void *out, float *lse,
+                       const int32_t *cu_seqlens, const int32_t *cu_k, const int32_t *used_k, int32_t num_seqs,
+                       int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t total_q, int32_t num_heads,
+                       int32_t num_heads_k, int32_t head_dim, int64_t q_row_stride, int64_t q_head_stride,
+                       int64_t k_row_stride, int64_t k_head_stride, int64_t v_row_stride, int64_t v_head_stride,
+                       int64_t o_row_stride, int64_t o_head_stride, int64_t bias_seq_stride,
+                       int64_t bias_head_stride, float softmax_scale, int32_t causal, void *workspace,
+                       int64_t workspace_bytes, hipStream_t stream) {
+  if (int e = check_common(q, k, v, out, lse, num_heads, num_heads_k, head_dim)) return e;
+  TG_CHECK(cu_seqlens != nullptr, "cu_seqlens is null");
+  TG_CHECK(num_seqs >= 0 && max_seqlen_q >= 0 && max_seqlen_k >= 0 && total_q >= 0, "negative size");
+  TG_CHECK(strides_ok({q_row_stride, q_head_stride, k_row_stride, k_head_stride, v_row_stride, v_head_stride,
+                       o_row_stride, o_head_stride}),
+           "q/k/v/out strides must be multiples of 8 elements");
+  TG_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
+  if (num_seqs == 0 || max_seqlen_q == 0 || total_q == 0) return 0;
+  // kernel addresses are 64-bit per sequence; one sequence's k/v/bias rows go through a buffer
+  // descriptor (< 4 GiB)
+  TG_CHECK(span_ok(max_seqlen_k, k_row_stride) && span_ok(max_seqlen_k, v_row_stride) &&
+               (cu_k != nullptr || (span_ok(total_q, k_row_stride) && span_ok(total_q, v_row_stride))) &&
+               (bias_raw == nullptr || span_ok(max_seqlen_k + bias_head_stride, 2)),
+           "the k/v/bias rows of one sequence must span less than 4 GiB");
+  FwdArgs a{};
+  a.q = static_cast<const bf16_t *>(q);
+  a.k = static_cast<const bf16_t *>(k);
+  a.v = static_cast<const bf16_t *>(v);
+  a.bias = bias_raw;
+  a.o = static_cast<bf16_t *>(out);
+  a.lse = lse;
+  a.cu_seqlens = cu_seqlens;
+  a.cu_k = cu_k;
+  a.used_k = used_k;
+  a.q_rs = q_row_stride; a.q_hs = q_head_stride;
+  a.k_rs = k_row_stride; a.k_hs = k_head_stride;
+  a.v_rs = v_row_stride; a.v_hs = v_head_stride;
+  a.o_rs = o_row_stride; a.o_hs = o_head_stride;
+  a.bias_bs = bias_seq_stride; a.bias_hs = bias_head_stride;
+  a.lse_total = total_q;
+  a.batch = num_seqs; a.sq = max_seqlen_q; a.sk = max_seqlen_k;
+  a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
+  a.scale_log2 = softmax_scale * kLog2e;
+  const int hp = (a.group % 2 == 0) ? 2 : 1;
+  int nw = 8;
+  const int64_t units = (int64_t)num_seqs * (num_heads / hp);
+  pick_tiling(hp, max_seqlen_q, units, nw, a.n_qtiles);
+  TG_CHECK(workspace == nullptr || aligned16(workspace), "workspace must be 16-byte aligned");
+  const int64_t nblocks = apply_split(
+      a, plan_split(nw, hp, a.n_qtiles, units, max_seqlen_q, max_seqlen_k, causal != 0), nw, units, workspace,
+      workspace_bytes);
+  TG_CHECK(nblocks < (1ll << 31), "grid too large");
+  dispatch_fwd<true>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
+  TG_HIP_CHECK(hipPeekAtLastError());
+  return 0;
+}
+}  // namespace
+}  // namespace tg
+
 extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
                                      void *out, float *lse, const int32_t *cu_seqlens, int32_t num_seqs,
                                      int32_t max_seqlen, int32_t total, int32_t num_heads,
@@ -859,47 +934,37 @@ extern "C" int tg_keybias_varlen_fwd(const void *q, const void *k, const void *v
                                      int64_t bias_head_stride, float softmax_scale, int32_t causal,
                                      void *workspace, int64_t workspace_bytes, hipStream_t stream) {
   clear_error();
-  if (int e = check_common(q, k, v, out, lse, num_heads, num_heads_k, head_dim)) return e;
-  TG_CHECK(cu_seqlens != nullptr, "cu_seqlens is null");
-  TG_CHECK(num_seqs >= 0 && max_seqlen >= 0 && total >= 0, "negative size");
-  TG_CHECK(strides_ok({q_row_stride, q_head_stride, k_row_stride, k_head_stride, v_row_stride, v_head_stride,
-                       o_row_stride, o_head_stride}),
-           "q/k/v/out strides must be multiples of 8 elements");
-  TG_CHECK(softmax_scale > 0.f, "softmax_scale must be positive");
-  if (num_seqs == 0 || max_seqlen == 0 || total == 0) return 0;
-  TG_CHECK(span_ok(total, k_row_stride) && span_ok(total, v_row_stride) &&
-               (bias_raw == nullptr || span_ok(max_seqlen + bias_head_stride, 2)),
-           "the packed k/v/bias must span less than 4 GiB");
-  FwdArgs a{};
-  a.q = static_cast<const bf16_t *>(q);
-  a.k = static_cast<const bf16_t *>(k);
-  a.v = static_cast<const bf16_t *>(v);
-  a.bias = bias_raw;
-  a.o = static_cast<bf16_t *>(out);
-  a.lse = lse;
-  a.cu_seqlens = cu_seqlens;
-  a.q_rs = q_row_stride; a.q_hs = q_head_stride;
-  a.k_rs = k_row_stride; a.k_hs = k_head_stride;
-  a.v_rs = v_row_stride; a.v_hs = v_head_stride;
-  a.o_rs = o_row_stride; a.o_hs = o_head_stride;
-  a.bias_bs = bias_seq_stride; a.bias_hs = bias_head_stride;
-  a.lse_total = total;
-  a.batch = num_seqs; a.sq = max_seqlen; a.sk = max_seqlen;
-  a.h = num_heads; a.hkv = num_heads_k; a.group = num_heads / num_heads_k;
-  a.scale_log2 = softmax_scale * kLog2e;
-  const int hp = (a.group % 2 == 0) ? 2 : 1;
-  int nw = 8;
-  const int64_t units = (int64_t)num_seqs * (num_heads / hp);
-  pick_tiling(hp, max_seqlen, units, nw, a.n_qtiles);
-  TG_CHECK(workspace == nullptr || aligned16(workspace), "workspace must be 16-byte aligned");
-  const int64_t nblocks = apply_split(a, plan_split(nw, hp, a.n_qtiles, units, max_seqlen, max_seqlen, causal != 0),
-                                      nw, units, workspace, workspace_bytes);
-  TG_CHECK(nblocks < (1ll << 31), "grid too large");
-  dispatch_fwd<true>(a, nw, hp, causal != 0, bias_raw != nullptr, (int)nblocks, stream);
-  TG_HIP_CHECK(hipPeekAtLastError());
-  return 0;
+  return keybias_fwd_varlen(q, k, v, bias_raw, out, lse, cu_seqlens, nullptr, nullptr, num_seqs, max_seqlen,
+                            max_seqlen, total, num_heads, num_heads_k, head_dim, q_row_stride, q_head_stride,
+                            k_row_stride, k_head_stride, v_row_stride, v_head_stride, o_row_stride, o_head_stride,
+                            bias_seq_stride, bias_head_stride, softmax_scale, causal, workspace, workspace_bytes,
+                            stream);
 }
 
+extern "C" int tg_keybias_varlen_kv_fwd(const void *q, const void *k, const void *v, const float *bias_raw,
+                                        void *out, float *lse, const int32_t *cu_seqlens_q,
+                                        const int32_t *cu_seqlens_k, const int32_t *seqused_k, int32_t num_seqs,
+                                        int32_t max_seqlen_q, int32_t max_seqlen_k, int32_t total_q,
+                                        int32_t num_heads, int32_t num_heads_k, int32_t head_dim,
+                                        int64_t q_row_stride, int64_t q_head_stride, int64_t k_row_stride,
+                                        int64_t k_head_stride, int64_t v_row_stride, int64_t v_head_stride,
+                                        int64_t o_row_stride, int64_t o_head_stride, int64_t bias_seq_stride,
+                                        int64_t bias_head_stride, float softmax_scale, int32_t causal,
+                                        void *workspace, int64_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  TG_CHECK(cu_seqlens_k != nullptr, "cu_seqlens_k is null");
+  return keybias_fwd_varlen(q, k, v, bias_raw, out, lse, cu_seqlens_q, cu_seqlens_k, seqused_k, num_seqs,
+                            max_seqlen_q, max_seqlen_k, total_q, num_heads, num_heads_k, head_dim, q_row_stride,
+                            q_head_stride, k_row_stride, k_head_stride, v_row_stride, v_head_stride, o_row_stride,
+                            o_head_stride, bias_seq_stride, bias_head_stride, softmax_scale, causal, workspace,
+                            workspace_bytes, stream);
+}
+
+extern "C" int64_t tg_keybias_varlen_kv_fwd_workspace_size(int32_t num_seqs, int32_t max_seqlen_q,
+                                                            int32_t max_seqlen_k, int32_t num_heads,
+                                                            int32_t num_heads_k, int32_t causal) {
+  return fwd_workspace_size(num_seqs, max_seqlen_q, max_seqlen_k, num_heads, num_heads_k, causal);
+}
 
 extern "C" int64_t tg_keybias_fwd_workspace_size(int32_t batch, int32_t seqlen_q, int32_t seqlen_k,
                                                   int32_t num_heads, int32_t num_heads_k, int32_t causal) {

@@ -91,7 +91,8 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
                                                       const float *__restrict__ q_head_scale,
                                                       const float *__restrict__ q_row_scale, bf16_t *q_out,
                                                       int64_t q_rs, bf16_t *__restrict__ k_out, int64_t k_rs,
-                                                      bf16_t *__restrict__ v_out, int64_t v_rs) {
+                                                      bf16_t *__restrict__ v_out, int64_t v_rs,
+                                                      const int32_t *__restrict__ kv_rows) {
   __shared__ float cs[kRopeTok][kHeadDim / 2][2];
   const int tid = threadIdx.x;
   const int64_t tok0 = (int64_t)blockIdx.x * kRopeTok;
@@ -116,8 +117,9 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
     if (t >= T) continue;  // uniform over the 16-lane group
     const bf16_t *src = qkv + t * qkv_rs + (int64_t)rr * kHeadDim + 8 * j;
     const u32x4 raw = ld16(src);
+    const int64_t crow = kv_rows ? (int64_t)kv_rows[t] : t;   // this token's KV-cache row
     if (rr >= H + Hkv) {  // value row: copied into the cache
-      st16(v_out + t * v_rs + (int64_t)(rr - H - Hkv) * kHeadDim + 8 * j, raw);
+      st16(v_out + crow * v_rs + (int64_t)(rr - H - Hkv) * kHeadDim + 8 * j, raw);
       continue;
     }
     const bool is_q = rr < H;
@@ -150,7 +152,7 @@ __global__ __launch_bounds__(256) void qk_rope_kernel(const bf16_t *qkv, int64_t
       y[e] = hs * (float)(__bf16)(x[e] * cs[tt][fi][0] + sgn * p * cs[tt][fi][1]);
     }
     bf16_t *dst = is_q ? q_out + t * q_rs + (int64_t)rr * kHeadDim
-                       : k_out + t * k_rs + (int64_t)(rr - H) * kHeadDim;
+                       : k_out + crow * k_rs + (int64_t)(rr - H) * kHeadDim;
     st16(dst + 8 * j, pack8(y));
   }
 }
@@ -312,7 +314,8 @@ extern "C" int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const in
                                int32_t num_heads, int32_t num_heads_k, int32_t head_dim, const void *q_norm_weight,
                                const void *k_norm_weight, float eps, const float *inv_freq, const float *q_head_scale,
                                const float *q_row_scale, void *q_out, int64_t q_row_stride, void *k_out,
-                               int64_t k_row_stride, void *v_out, int64_t v_row_stride, hipStream_t stream) {
+                               int64_t k_row_stride, void *v_out, int64_t v_row_stride, const int32_t *kv_rows,
+                               hipStream_t stream) {
   clear_error();
   TG_CHECK(qkv && positions && q_norm_weight && k_norm_weight && inv_freq && q_out && k_out && v_out,
            "qk_norm_rope: null pointer");
@@ -337,7 +340,8 @@ extern "C" int tg_qk_norm_rope(const void *qkv, int64_t qkv_row_stride, const in
                      static_cast<const bf16_t *>(qkv), qkv_row_stride, positions, n_tokens, num_heads, num_heads_k,
                      static_cast<const bf16_t *>(q_norm_weight), static_cast<const bf16_t *>(k_norm_weight), eps,
                      inv_freq, q_head_scale, q_row_scale, static_cast<bf16_t *>(q_out), q_row_stride,
-                     static_cast<bf16_t *>(k_out), k_row_stride, static_cast<bf16_t *>(v_out), v_row_stride);
+                     static_cast<bf16_t *>(k_out), k_row_stride, static_cast<bf16_t *>(v_out), v_row_stride,
+                     kv_rows);
   TG_HIP_CHECK(hipGetLastError());
   return 0;
 }

@@ -773,7 +773,8 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
           const char *src = static_cast<const char *>(st.src) + srow * st.src_row_stride +
                             (int64_t)ch * st.src_chunk_stride + 16 * cu;
           v[k] = *reinterpret_cast<const u32x4 *>(src);
-          dst[k] = static_cast<char *>(st.dst) + (j0 + rr) * st.dst_row_stride + (int64_t)ch * st.chunk_bytes + 16 * cu;
+          const int64_t drow = j0 + rr + (int64_t)s_seq[rr] * st.dst_seq_gap;
+          dst[k] = static_cast<char *>(st.dst) + drow * st.dst_row_stride + (int64_t)ch * st.chunk_bytes + 16 * cu;
         }
       }
     }
@@ -866,6 +867,7 @@ extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, co
                s.dst_row_stride | s.src_chunk_stride) & 15) == 0,
              "stream %d: pointers and strides must be 16-byte aligned", i);
     TG_CHECK(s.dst_row_stride >= (int64_t)s.chunk_bytes * s.n_chunks, "stream %d: destination rows overlap", i);
+    TG_CHECK(s.dst_seq_gap >= 0, "stream %d: negative destination gap", i);
     a.st[i] = s;
   }
   a.n_streams = n_streams;

@@ -133,23 +133,27 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, residual: Optional[tor
 def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, lw: LayerWeights, shape: DecoderShape,
                  inv_freq: torch.Tensor, k_out: torch.Tensor, v_out: torch.Tensor,
                  q_head_scale: Optional[torch.Tensor] = None,
-                 q_row_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 q_row_scale: Optional[torch.Tensor] = None,
+                 kv_rows: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Normalises and rotates q in place inside qkv (returned as a (T, H, D) view) and writes the
-    rotated k and the v rows into k_out / v_out ((T, Hkv, D) contiguous).  With q_head_scale (H,)
-    and / or q_row_scale (T,) fp32 the bf16 query is multiplied by bf16(q_head_scale[h] *
-    q_row_scale[t]) and rounded to bf16 again (the reference's bf16 q * s_eff)."""
+    rotated k and the v rows into k_out / v_out ((rows, Hkv, D) contiguous rows) at row t, or at
+    row kv_rows[t] (int32) when given.  With q_head_scale (H,) and / or q_row_scale (T,) fp32 the
+    bf16 query is multiplied by bf16(q_head_scale[h] * q_row_scale[t]) and rounded to bf16 again
+    (the reference's bf16 q * s_eff)."""
     T = qkv.shape[0]
     H, Hkv, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
     if positions.dtype != torch.int64 or positions.numel() != T:
         raise RuntimeError("qk_norm_rope: positions must be int64 with one entry per token")
     if q_row_scale is not None and (q_row_scale.dtype != torch.float32 or q_row_scale.numel() < T):
         raise RuntimeError("qk_norm_rope: q_row_scale must be fp32 with one entry per token")
+    if kv_rows is not None and (kv_rows.dtype != torch.int32 or kv_rows.numel() < T or not kv_rows.is_contiguous()):
+        raise RuntimeError("qk_norm_rope: kv_rows must be contiguous int32 with one entry per token")
     _lib.call("tg_qk_norm_rope", qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), T, H, Hkv, D,
               lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), float(shape.rms_eps), inv_freq.data_ptr(),
               q_head_scale.data_ptr() if q_head_scale is not None else None,
               q_row_scale.data_ptr() if q_row_scale is not None else None,
               qkv.data_ptr(), qkv.stride(0), k_out.data_ptr(), k_out.stride(0), v_out.data_ptr(), v_out.stride(0),
-              _stream(qkv))
+              kv_rows.data_ptr() if kv_rows is not None else None, _stream(qkv))
     return qkv[:, :H * D].view(T, H, D) if qkv.is_contiguous() else qkv[:, :H * D].unflatten(1, (H, D))
 
 
@@ -185,19 +189,91 @@ def varlen_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqle
     return out
 
 
+def varlen_kv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_q: torch.Tensor, kv_cu: torch.Tensor,
+                        kv_used: torch.Tensor, max_q: int, max_k: int, scale: float,
+                        bias_raw: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                        lse: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of every packed query segment over its own key segment of a cache
+    (tg_keybias_varlen_kv_fwd): queries cu_q[b] .. cu_q[b+1]-1 over cache rows kv_cu[b] ..
+    kv_cu[b] + kv_used[b] - 1, bottom-right aligned; bias_raw (nseq, H, >= max_k) fp32 with
+    column j the sequence's key j."""
+    T, H, D = q.shape
+    Hkv = k.shape[1]
+    out = torch.empty(T, H, D, dtype=q.dtype, device=q.device) if out is None else out
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device) if lse is None else lse
+    nseq = cu_q.numel() - 1
+    for t in (cu_q, kv_cu, kv_used):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise RuntimeError("varlen_kv_attention: cu_q, kv_cu and kv_used must be contiguous int32")
+    if kv_cu.numel() < nseq or kv_used.numel() < nseq:
+        raise RuntimeError("varlen_kv_attention: kv_cu / kv_used need an entry per sequence")
+    if bias_raw is not None and (bias_raw.dtype != torch.float32 or bias_raw.stride(-1) != 1
+                                 or bias_raw.shape[-1] < max_k):
+        raise RuntimeError("varlen_kv_attention: bias must be fp32 with a contiguous key axis of >= max_k")
+    ws, ws_ptr, ws_bytes = _lib.fwd_workspace("tg_keybias_varlen_kv_fwd_workspace_size", q.device, nseq,
+                                              int(max_q), int(max_k), H, Hkv, 1)
+    _lib.call("tg_keybias_varlen_kv_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(),
+              bias_raw.data_ptr() if bias_raw is not None else None, out.data_ptr(), lse.data_ptr(),
+              cu_q.data_ptr(), kv_cu.data_ptr(), kv_used.data_ptr(), nseq, int(max_q), int(max_k), T, H, Hkv, D,
+              q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+              out.stride(0), out.stride(1),
+              bias_raw.stride(0) if bias_raw is not None else 0, bias_raw.stride(1) if bias_raw is not None else 0,
+              float(scale), 1, ws_ptr, ws_bytes, _stream(q))
+    return out
+
+
 # ---- layer runner ------------------------------------------------------------------------------
 
 @dataclass
+class CacheGap:
+    """KV-cache layout with `gap` free rows after each sequence (room for generated tokens): the
+    cache rows of sequence b start at seg[b] = cu[b] + b * gap."""
+    gap: int
+    seg: List[int]                 # (nseq + 1,) host: segment starts, seg[nseq] = cu[nseq] + nseq * gap
+    seg_dev: torch.Tensor          # int32 (nseq + 1,)
+    used_dev: torch.Tensor         # int32 (nseq,) rows written per sequence
+    rows_dev: torch.Tensor         # int32 (T,) cache row of every packed row
+    pad: int = 0                   # rows after the last sequence (mapped past every segment)
+
+    @property
+    def rows(self) -> int:
+        """Cache rows the layout needs."""
+        return self.seg[-1] + self.pad
+
+    @staticmethod
+    def build(cu: List[int], gap: int, device, pad_rows: int = 0) -> "CacheGap":
+        """pad_rows rows after the last sequence (a bucketed graph's padding) map past every segment."""
+        n = len(cu) - 1
+        seg = [cu[b] + b * gap for b in range(n + 1)]
+        lens = [cu[b + 1] - cu[b] for b in range(n)]
+        off = torch.tensor([b * gap for b in range(n)] + [n * gap], dtype=torch.int32)
+        reps = torch.tensor(lens + [pad_rows], dtype=torch.int64)
+        T = cu[-1] + pad_rows
+        rows_h = torch.arange(T, dtype=torch.int32) + torch.repeat_interleave(off, reps, output_size=T)
+        packed = torch.cat([torch.tensor(seg, dtype=torch.int32), torch.tensor(lens, dtype=torch.int32), rows_h])
+        d = h2d(packed, device)
+        return CacheGap(gap, seg, d[:n + 1], d[n + 1:2 * n + 1], d[2 * n + 1:], pad_rows)
+
+
+@dataclass
 class Ragged:
-    """Token geometry of a packed batch: rows of sequence b are cu[b] .. cu[b+1]-1."""
+    """Token geometry of a packed batch: rows of sequence b are cu[b] .. cu[b+1]-1.  With `cache`
+    the layer's KV rows go to a cache with free rows after each sequence (CacheGap) and attention
+    reads its keys there."""
     cu: List[int]
     cu_dev: torch.Tensor       # int32 (nseq + 1,) on the device
     positions: torch.Tensor    # int64 (T,) RoPE position of every row
     max_len: int
+    cache: Optional[CacheGap] = None
 
     @property
     def total(self) -> int:
         return self.cu[-1]
+
+    @property
+    def kv_rows(self) -> int:
+        """Rows a layer's KV cache needs for this geometry."""
+        return self.cache.rows if self.cache is not None else self.total
 
     @staticmethod
     def from_lengths(lengths: List[int], device) -> "Ragged":
@@ -272,10 +348,16 @@ def run_layers(wts: DecoderWeights, layer_ids, x: torch.Tensor, geo: Ragged, ws:
         if capture is not None:
             capture.append(res.clone())
         torch.matmul(normed, lw.w_qkv.t(), out=qkv)
+        cg = geo.cache
         q = qk_norm_rope(qkv, geo.positions, lw, shape, wts.inv_freq, kv[i].k, kv[i].v,
-                         q_scales[i] if q_scales is not None else None, q_row_scale)
-        varlen_attention(q, kv[i].k, kv[i].v, geo.cu_dev, geo.max_len, scale,
-                         biases[i] if biases is not None else None, out=attn, lse=lse)
+                         q_scales[i] if q_scales is not None else None, q_row_scale,
+                         kv_rows=cg.rows_dev if cg is not None else None)
+        if cg is None:
+            varlen_attention(q, kv[i].k, kv[i].v, geo.cu_dev, geo.max_len, scale,
+                             biases[i] if biases is not None else None, out=attn, lse=lse)
+        else:
+            varlen_kv_attention(q, kv[i].k, kv[i].v, geo.cu_dev, cg.seg_dev, cg.used_dev, geo.max_len,
+                                geo.max_len, scale, biases[i] if biases is not None else None, out=attn, lse=lse)
         torch.matmul(attn.view(T, -1), lw.w_o.t(), out=hid)
         if attn_only_last and n_done == len(layer_ids) - 1:
             break

@@ -26,7 +26,7 @@ class PackStream(ctypes.Structure):
     """C layout of tg_pack_stream (include/tokengate_hip.h)."""
     _fields_ = [("src", ctypes.c_void_p), ("dst", ctypes.c_void_p), ("src_row_stride", ctypes.c_int64),
                 ("dst_row_stride", ctypes.c_int64), ("src_chunk_stride", ctypes.c_int64),
-                ("chunk_bytes", ctypes.c_int32), ("n_chunks", ctypes.c_int32)]
+                ("chunk_bytes", ctypes.c_int32), ("n_chunks", ctypes.c_int32), ("dst_seq_gap", ctypes.c_int64)]
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -144,7 +144,7 @@ def _sel_workspace(device, stream: int, nseq: int, n_chunks: int):
     return ent
 
 
-def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]] = (),
+def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple] = (),
                 positions: Optional[torch.Tensor] = None, bias_out: Optional[torch.Tensor] = None,
                 keep_out: Optional[torch.Tensor] = None, rms_eps: float = RMS_EPS,
                 check: bool = False) -> torch.Tensor:
@@ -163,11 +163,7 @@ def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[Tuple[torch.T
     for t, dt in ((positions, torch.int64), (bias_out, torch.float32)):
         if t is not None and (t.dtype != dt or not t.is_contiguous()):
             raise RuntimeError("select_pack: positions must be contiguous int64, bias_out contiguous float32")
-    arr = (PackStream * max(1, len(pairs)))()
-    for i, (src, dst) in enumerate(pairs):
-        if dst.shape[0] < p.total_kept:
-            raise RuntimeError("select_pack: destination has fewer rows than kept tokens")
-        arr[i] = _row_stream(src, dst)
+    arr = _streams(pairs, p)
     if p.total_kept == 0:
         return keep
     if not p.sel_kpt:
@@ -190,7 +186,23 @@ def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[Tuple[torch.T
     return keep
 
 
-def _row_stream(src: torch.Tensor, dst: torch.Tensor) -> PackStream:
+def _streams(pairs, p: KeepPlan):
+    """PackStream array of (src, dst) or (src, dst, gap) entries: with a gap, kept row j of
+    sequence b goes to dst row j + b * gap (a cache with `gap` free rows after each sequence)."""
+    arr = (PackStream * max(1, len(pairs)))()
+    nseq = len(p.n_kept)
+    for i, pr in enumerate(pairs):
+        src, dst = pr[0], pr[1]
+        gap = int(pr[2]) if len(pr) > 2 else 0
+        if gap < 0:
+            raise RuntimeError("pack: negative destination gap")
+        if dst.shape[0] < p.total_kept + gap * max(0, nseq - 1):
+            raise RuntimeError("pack: destination has fewer rows than kept tokens")
+        arr[i] = _row_stream(src, dst, gap)
+    return arr
+
+
+def _row_stream(src: torch.Tensor, dst: torch.Tensor, gap: int = 0) -> PackStream:
     """A (rows, ...) source / destination pair.  The source may be (rows, chunks, chunk_elems) with
     any row and chunk strides (head-major caches); everything after the row axis of dst, and the
     chunk axis of src, must be contiguous."""
@@ -209,22 +221,19 @@ def _row_stream(src: torch.Tensor, dst: torch.Tensor) -> PackStream:
     if not dst[0].is_contiguous() or dst[0].numel() * dst.element_size() != n_chunks * chunk:
         raise RuntimeError("pack: destination rows must be contiguous and as long as a source row")
     return PackStream(src.data_ptr(), dst.data_ptr(), src.stride(0) * es, dst.stride(0) * es, chunk_stride,
-                      chunk, n_chunks)
+                      chunk, n_chunks, gap)
 
 
-def pack(keep: torch.Tensor, p: KeepPlan, pairs: Sequence[Tuple[torch.Tensor, torch.Tensor]],
+def pack(keep: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple],
          positions: Optional[torch.Tensor] = None, bias_src: Optional[torch.Tensor] = None,
          sumsq: Optional[torch.Tensor] = None, bias_out: Optional[torch.Tensor] = None,
          rms_eps: float = RMS_EPS) -> None:
-    """One launch: dst[j] = src[row_start[b] + keep[j]] for every (src, dst) pair; positions[j] =
+    """One launch: dst[j] = src[row_start[b] + keep[j]] for every (src, dst) pair (or dst[j + b * gap]
+    for a (src, dst, gap) entry); positions[j] =
     keep[j]; bias_out[j] = RMS-normalised bias_src score of kept article rows, 0 elsewhere."""
     if len(pairs) > 16:
         raise RuntimeError("pack: at most 16 row streams per launch")
-    arr = (PackStream * max(1, len(pairs)))()
-    for i, (s, d) in enumerate(pairs):
-        if d.shape[0] < p.total_kept:
-            raise RuntimeError("pack: destination has fewer rows than kept tokens")
-        arr[i] = _row_stream(s, d)
+    arr = _streams(pairs, p)
     for t, dt in ((positions, torch.int64), (bias_src, torch.float32), (sumsq, torch.float32),
                   (bias_out, torch.float32)):
         if t is not None and (t.dtype != dt or not t.is_contiguous()):

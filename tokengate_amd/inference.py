@@ -139,11 +139,14 @@ class TokenGateModel:
     def device(self) -> torch.device:
         return self.weights.device
 
-    def prefill(self, ids: Sequence, max_kept_prefill_tokens=None, prune_below_gate: bool = False):
-        """Gated prefill of already-split prompts: ids = [(clean_ids, start, end), ...]."""
+    def prefill(self, ids: Sequence, max_kept_prefill_tokens=None, prune_below_gate: bool = False,
+                decode_headroom: int = 0):
+        """Gated prefill of already-split prompts: ids = [(clean_ids, start, end), ...];
+        decode_headroom: free cache rows left after each sequence for the decode to append to."""
         k = _NO_PRUNING if max_kept_prefill_tokens is None else max_kept_prefill_tokens
         return P.prefill_batch(self.weights, self.gate, [x[0] for x in ids], [x[1] for x in ids],
-                               [x[2] for x in ids], self.gate_layer, k, prune_below_gate=prune_below_gate)
+                               [x[2] for x in ids], self.gate_layer, k, prune_below_gate=prune_below_gate,
+                               decode_headroom=decode_headroom)
 
     @torch.no_grad()
     def generate(self, ids: Union[List[int], List[List[int]]], tokenizer=None, *, max_new_tokens: int = 20,
@@ -162,7 +165,8 @@ class TokenGateModel:
         split = [split_state_span(list(seq)) for seq in ids]
         _sync()
         t0 = time.perf_counter()
-        pf = self.prefill(split, max_kept_prefill_tokens, prune_below_gate)
+        pf = self.prefill(split, max_kept_prefill_tokens, prune_below_gate,
+                          decode_headroom=max_new_tokens if max_new_tokens > 1 else 0)
         first = pf.first_tokens
         _sync()
         prefill_s = time.perf_counter() - t0

@@ -30,7 +30,7 @@ from typing import Dict, List, Optional, Sequence
 import torch
 
 from tokengate_amd import gate as G
-from tokengate_amd.decoder import (DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, h2d, logits_last,
+from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, h2d, logits_last,
                                    mlp_sublayer, run_layers)
 
 
@@ -49,6 +49,14 @@ class PrefillResult:
     phase2_bias: Optional[torch.Tensor] = None  # (L2, H, total_kept) fp32 raw-unit key bias of each Phase-2 layer
     phase_ms: Dict[str, float] = field(default_factory=dict)
     capture: Optional[dict] = None
+    # decode headroom: every layer's cache keeps `decode_headroom` free rows after each sequence
+    # (cache_below: layers at / below the gate, cache_above: Phase-2 layers); phase2_bias_seq
+    # (L2, B, H, max_kept + decode_headroom) fp32 is each Phase-2 layer's key bias by sequence and
+    # key index, 0 past the kept rows (the generated keys' bias)
+    decode_headroom: int = 0
+    cache_below: Optional[CacheGap] = None
+    cache_above: Optional[CacheGap] = None
+    phase2_bias_seq: Optional[torch.Tensor] = None
 
 
 def _cat_ids(ids_list: Sequence, device) -> torch.Tensor:
@@ -81,19 +89,26 @@ class Phase2Graphs:
 
     def run(self, wts: DecoderWeights, layer_ids: List[int], hs: torch.Tensor, positions: torch.Tensor,
             cu_dev: torch.Tensor, biases_all: torch.Tensor, q_head: Optional[torch.Tensor], mlp_rows: int,
-            q_row: Optional[torch.Tensor] = None):
-        """biases_all (L2, nseq, H, max_kept) fp32 raw-unit key bias; q_head (L2, H) / q_row (T2,)
-        the query factors (None when absent)."""
+            q_row: Optional[torch.Tensor] = None, cu_kept: Optional[List[int]] = None, gap: int = 0):
+        """biases_all (L2, nseq, H, >= max_kept) fp32 raw-unit key bias; q_head (L2, H) / q_row (T2,)
+        the query factors (None when absent); gap > 0: the caches keep `gap` free rows after each
+        sequence (cu_kept, the host copy of cu_dev, is then required) and are returned whole."""
         dev = hs.device
         nseq = cu_dev.numel() - 1
-        T2, max_kept = hs.shape[0], biases_all.shape[-1]
+        T2 = hs.shape[0]
+        max_kept = max(cu_kept[b + 1] - cu_kept[b] for b in range(nseq)) if cu_kept is not None \
+            else biases_all.shape[-1]
         Tb, Lb = self._up(T2, self.bucket_rows), self._up(max_kept, self.bucket_len)
+        if gap and cu_kept is None:
+            raise ValueError("Phase2Graphs.run: a cache gap needs the host cu_kept")
         # the graph reads the weights' and workspaces' memory: a key per weights object (held
         # alive by the entry) and per MLP chunking
-        key = (id(wts), nseq, Tb, Lb, tuple(layer_ids), q_head is not None, q_row is not None, int(mlp_rows))
+        key = (id(wts), nseq, Tb, Lb, tuple(layer_ids), q_head is not None, q_row is not None, int(mlp_rows),
+               int(gap))
         ent = self.graphs.get(key)
         if ent is None:
-            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, q_head is not None, q_row is not None, mlp_rows, dev)
+            ent = self._capture(wts, layer_ids, nseq, Tb, Lb, q_head is not None, q_row is not None, mlp_rows, dev,
+                                int(gap))
             ent["wts"] = wts
             self.graphs[key] = ent
         if q_row is not None:
@@ -103,13 +118,21 @@ class Phase2Graphs:
         ent["pos"][:T2].copy_(positions)
         ent["pos"][T2:].zero_()
         ent["cu"].copy_(cu_dev)
-        ent["bias"][..., :max_kept].copy_(biases_all)
+        ent["bias"][..., :max_kept].copy_(biases_all[..., :max_kept])
         if q_head is not None:
             ent["qs"].copy_(q_head)
+        if gap:
+            cg = CacheGap.build(cu_kept, gap, dev, pad_rows=Tb - T2)
+            sc = ent["cache"]
+            sc.seg_dev.copy_(cg.seg_dev)
+            sc.used_dev.copy_(cg.used_dev)
+            sc.rows_dev.copy_(cg.rows_dev)
         ent["graph"].replay()
+        if gap:
+            return ent["out"][:T2], {l: ent["kv"][l] for l in layer_ids}
         return ent["out"][:T2], {l: LayerKV(ent["kv"][l].k[:T2], ent["kv"][l].v[:T2]) for l in layer_ids}
 
-    def _capture(self, wts, layer_ids, nseq, Tb, Lb, with_qs, with_rs, mlp_rows, dev):
+    def _capture(self, wts, layer_ids, nseq, Tb, Lb, with_qs, with_rs, mlp_rows, dev, gap=0):
         shape = wts.shape
         L2 = len(layer_ids)
         x = torch.zeros(Tb, shape.d_model, dtype=torch.bfloat16, device=dev)
@@ -119,11 +142,16 @@ class Phase2Graphs:
         bias = torch.zeros(L2, nseq, shape.n_heads, Lb, dtype=torch.float32, device=dev)
         qs = torch.ones(L2, shape.n_heads, dtype=torch.float32, device=dev) if with_qs else None
         rs = torch.ones(Tb, dtype=torch.float32, device=dev) if with_rs else None
+        cache = None
+        if gap:
+            # static cache geometry, as the static cu (every row in the last sequence) until a
+            # replay copies the batch's own; the caches hold the bucket's rows plus every gap
+            cache = CacheGap.build([0] * nseq + [Tb], gap, dev)
         kv: List[Optional[LayerKV]] = [None] * shape.n_layers
         for l in layer_ids:
-            kv[l] = alloc_kv(shape, Tb, dev)
+            kv[l] = alloc_kv(shape, Tb + nseq * gap, dev)
         ws = Workspace(shape, Tb, dev, mlp_rows=mlp_rows)
-        geo = Ragged([0, Tb], cu, pos, Lb)
+        geo = Ragged([0, Tb], cu, pos, Lb, cache=cache)
         biases = {l: bias[j] for j, l in enumerate(layer_ids)}
         q_scales = {l: qs[j] for j, l in enumerate(layer_ids)} if with_qs else None
         side = torch.cuda.Stream(device=dev)
@@ -134,19 +162,21 @@ class Phase2Graphs:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             out = run_layers(wts, layer_ids, x, geo, ws, kv, biases=biases, q_scales=q_scales, q_row_scale=rs)
-        return dict(graph=g, x=x, pos=pos, cu=cu, bias=bias, qs=qs, rs=rs, kv=kv, ws=ws, out=out)
+        return dict(graph=g, x=x, pos=pos, cu=cu, bias=bias, qs=qs, rs=rs, kv=kv, ws=ws, out=out, cache=cache)
 
 
 @torch.no_grad()
 def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Sequence[int],
                   art_ends: Sequence[int], gate_layer: int, K, prune_below_gate: bool = False,
                   phase_timing: bool = False, capture: bool = False, mlp_rows: int = 131072,
-                  phase2_graphs: Optional[Phase2Graphs] = None) -> PrefillResult:
+                  phase2_graphs: Optional[Phase2Graphs] = None, decode_headroom: int = 0) -> PrefillResult:
     """ids_list: B prompts (lists of ints or 1-D tensors); the state span of prompt b is
     [art_starts[b], art_ends[b]); K: scalar or per-prompt list; head: gate.ScoringHead or
     gate.BranchHead (split gate layer).  phase2_graphs: replay Phase 2
     from captured graphs (captured on first use per geometry); the Phase-2 KV caches are then views
-    of the graph's buffers, valid until its next replay."""
+    of the graph's buffers, valid until its next replay.  decode_headroom: every layer's KV cache
+    is laid out with that many free rows after each sequence (written there by the prefill's own
+    launches and the pack), so that decode appends in place."""
     shape = wts.shape
     dev = wts.device
     B = len(ids_list)
@@ -160,6 +190,9 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     lens = [int(x.numel()) if torch.is_tensor(x) else len(x) for x in ids_list]
     if min(lens) < 1:
         raise ValueError("every prompt needs at least one token")
+    gap = int(decode_headroom)
+    if gap < 0:
+        raise ValueError("decode_headroom must be >= 0")
     ev = [] if phase_timing else None
 
     def mark(name):
@@ -172,12 +205,14 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     mark("phase1")
     ids = _cat_ids(ids_list, dev)
     geo1 = Ragged.from_lengths(lens, dev)
+    if gap and not prune_below_gate:    # the Phase-1 caches are the decode caches of these layers
+        geo1.cache = CacheGap.build(geo1.cu, gap, dev)
     T = geo1.total
     x = torch.nn.functional.embedding(ids, wts.embed)
     ws1 = Workspace(shape, T, dev, mlp_rows=mlp_rows)
     kv: List[Optional[LayerKV]] = [None] * n_layers
     for i in range(gate_layer + 1):
-        kv[i] = alloc_kv(shape, T, dev)
+        kv[i] = alloc_kv(shape, geo1.kv_rows, dev)
     split = bool(getattr(head, "split_gate_layer", False))
     h = run_layers(wts, range(gate_layer + 1), x, geo1, ws1, kv, capture=cap["phase1"] if cap else None,
                    attn_only_last=split)
@@ -197,10 +232,11 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     kept_pos = torch.empty(T2, dtype=torch.int64, device=dev)
     kept_bias = torch.empty(T2, dtype=torch.float32, device=dev)
     pairs = [(h, hs)]
+    B_ = len(lens)
     if prune_below_gate:
         for i in range(gate_layer + 1):
-            nk = alloc_kv(shape, T2, dev)
-            pairs += [(kv[i].k, nk.k), (kv[i].v, nk.v)]
+            nk = alloc_kv(shape, T2 + B_ * gap, dev)
+            pairs += [(kv[i].k, nk.k, gap), (kv[i].v, nk.v, gap)]
             kv[i] = nk
     keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias)
     if cap is not None:
@@ -217,25 +253,32 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     max_kept = max(p.n_kept)
     ratio = G.ssmax_ratio_rows(kept_pos, p.cu_kept) if head.ssmax else None   # (T2,)
     bias_rows, q_head, q_row = head.phase2_tables(kept_bias, ratio, 1.0 / math.sqrt(shape.head_dim))
-    # per-sequence padded view of the packed rows' bias: row b, column t <- packed row
-    # cu_kept[b] + t (columns past a sequence's end repeat its last row; the kernel never reads them)
-    t_ = torch.arange(max_kept, dtype=torch.int64)
+    # per-sequence view of the packed rows' bias: row b, column t <- packed row cu_kept[b] + t,
+    # 0 past the sequence's kept rows (the decode's generated keys; Phase 2 never reads them)
+    W = max_kept + gap
+    t_ = torch.arange(W, dtype=torch.int64)[None, :]
     st = torch.tensor(p.cu_kept[:-1], dtype=torch.int64)[:, None]
-    en = torch.tensor(p.cu_kept[1:], dtype=torch.int64)[:, None] - 1
-    idx_d = h2d(torch.minimum(st + t_[None, :], en), dev)
-    biases_all = bias_rows[:, :, idx_d].permute(0, 2, 1, 3).contiguous()      # (L2, B, H, max_kept)
+    nk_ = torch.tensor(p.n_kept, dtype=torch.int64)[:, None]
+    idx_d = h2d(torch.where(t_ < nk_, st + t_, T2), dev)                      # T2: the zero column
+    bias_z = torch.cat([bias_rows, bias_rows.new_zeros(bias_rows.shape[0], bias_rows.shape[1], 1)], -1)
+    biases_all = bias_z[:, :, idx_d].permute(0, 2, 1, 3).contiguous()          # (L2, B, H, W)
     cu2_dev = h2d(torch.tensor(p.cu_kept, dtype=torch.int32), dev)
     above = list(range(gate_layer + 1, n_layers))
+    cache2 = None
     if phase2_graphs is not None and cap is None:
-        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, biases_all, q_head, mlp_rows, q_row)
+        h2, kv2 = phase2_graphs.run(wts, above, hs, kept_pos, cu2_dev, biases_all, q_head, mlp_rows, q_row,
+                                    cu_kept=p.cu_kept, gap=gap)
         for l in above:
             kv[l] = kv2[l]
+        if gap:
+            cache2 = CacheGap.build(p.cu_kept, gap, dev)
     else:
-        geo2 = Ragged(p.cu_kept, cu2_dev, kept_pos, max_kept)
+        cache2 = CacheGap.build(p.cu_kept, gap, dev) if gap else None
+        geo2 = Ragged(p.cu_kept, cu2_dev, kept_pos, max_kept, cache=cache2)
         biases = {l: biases_all[j] for j, l in enumerate(above)}
         qs = {l: q_head[j] for j, l in enumerate(above)} if q_head is not None else None
         for l in above:
-            kv[l] = alloc_kv(shape, T2, dev)
+            kv[l] = alloc_kv(shape, geo2.kv_rows, dev)
         ws2 = ws2 if ws2 is not None else Workspace(shape, T2, dev, mlp_rows=mlp_rows)
         h2 = run_layers(wts, above, hs, geo2, ws2, kv, biases=biases, q_scales=qs,
                         capture=cap["phase2"] if cap else None, q_row_scale=q_row)
@@ -253,8 +296,11 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     if cap is not None:
         cap.update(scores=scores, keep=keep, hs_packed=hs, h2=h2, logits=logits, biases_all=biases_all,
                    q_head=q_head, q_row=q_row)
-    return PrefillResult(first, logits, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, ratio, bias_rows,
-                         phase_ms, cap)
+    cache1 = None
+    if gap:
+        cache1 = geo1.cache if not prune_below_gate else CacheGap.build(p.cu_kept, gap, dev)
+    return PrefillResult(first, logits, kept_pos, p.cu_kept, p.n_kept, p.k_clamped, kv, geo1.cu, kept_bias, ratio,
+                         bias_rows, phase_ms, cap, gap, cache1, cache2, biases_all if gap else None)
 
 
 def ttft_ms(fn, reps: int = 5, warmup: int = 1) -> List[float]:
