@@ -11,20 +11,27 @@ gradient with respect to bias_raw (scale * sum_i dS) as in kernels/fa2bias/keybi
 import torch
 
 
-def _logits(qh, kg, brow, scale, causal, i0, i1, sq, sk):
+def _logits(qh, kg, brow, scale, causal, i0, i1, sq, sk, q_pos=None):
     z = qh[i0:i1] @ kg.t()
     if brow is not None:
         z = z + brow[None, :]
     z = z * scale
     if causal:
-        i = torch.arange(i0, i1, device=z.device)[:, None]
         j = torch.arange(sk, device=z.device)[None, :]
-        z = z.masked_fill(j > i + (sk - sq), float("-inf"))
+        if q_pos is None:
+            i = torch.arange(i0, i1, device=z.device)[:, None]
+            z = z.masked_fill(j > i + (sk - sq), float("-inf"))
+        else:
+            z = z.masked_fill(j > q_pos[i0:i1, None], float("-inf"))
     return z
 
 
-def fwd(q, k, v, bias_raw, scale, causal=True, chunk=1024):
+def fwd(q, k, v, bias_raw, scale, causal=True, chunk=1024, q_pos=None):
+    """q_pos (Sq,) int64, optional: q holds only these rows of a self-attention over the Sk keys
+    (row q_pos[i] sees keys j <= q_pos[i]) -- sampled rows of a long sequence."""
     B, Sq, H, D = q.shape
+    if q_pos is not None:
+        q_pos = torch.as_tensor(q_pos, dtype=torch.int64, device=q.device)
     Sk, Hkv = k.shape[1], k.shape[2]
     G = H // Hkv
     out = torch.zeros(B, Sq, H, D, dtype=torch.float32, device=q.device)
@@ -38,7 +45,7 @@ def fwd(q, k, v, bias_raw, scale, causal=True, chunk=1024):
             brow = None if bias_raw is None else bias_raw[b, h].float()
             for i0 in range(0, Sq, chunk):
                 i1 = min(Sq, i0 + chunk)
-                z = _logits(qh, kg, brow, scale, causal, i0, i1, Sq, Sk)
+                z = _logits(qh, kg, brow, scale, causal, i0, i1, Sq, Sk, q_pos)
                 m = z.amax(dim=1)
                 ok = torch.isfinite(m)
                 p = torch.exp(z - torch.where(ok, m, torch.zeros_like(m))[:, None])

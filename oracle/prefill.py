@@ -53,10 +53,10 @@ def rotate_half(x: torch.Tensor) -> torch.Tensor:
 class Weights:
     """float32 copies of a decoder's weights (any object with the DecoderWeights fields)."""
 
-    def __init__(self, wts):
+    def __init__(self, wts, device="cpu"):
         s = wts.shape
         self.shape = s
-        f = lambda t: t.detach().float().cpu()
+        f = lambda t: t.detach().float().to(device)
         self.embed = f(wts.embed)
         self.final_norm = f(wts.final_norm)
         self.lm_head = f(wts.lm_head)
@@ -72,28 +72,34 @@ class Weights:
 
 def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Optional[torch.Tensor] = None,
           q_temp: Optional[torch.Tensor] = None, q_scale: Optional[torch.Tensor] = None,
-          boundary: Optional[list] = None):
+          boundary: Optional[list] = None, rows: Optional[torch.Tensor] = None):
     """One decoder layer on a batch x (B, n, d) float32 at positions pos (B, n); bias_logit
     (B, H, n) per-key logit bias or None.  q_temp (H,): a per-head temperature multiplying the
     query and the bias (the fp32 form of the per-head branch of _phase2_q_bias); q_scale
     (B, H, n): a per-(head, row) query multiplier, the bias used as given (the caller passes the
     reference's bf16 Phase-2 values, phase2_tables).  Returns (x_out, k, v) with k/v
     (B, n, Hkv, D) after norm and RoPE; boundary (a list), if given, receives the attention
-    residual a = x + o_proj(attn)."""
+    residual a = x + o_proj(attn).  rows (int64, optional): evaluate only these query rows (each
+    over every key it sees); x_out (and boundary) then hold those rows only."""
     s = W.shape
     L = W.layers[i]
     B, n, _ = x.shape
     H, Hkv, D = s.n_heads, s.n_kv_heads, s.head_dim
     h = rms(x, L["ln1"], s.rms_eps)
-    q = (h @ L["wq"].t()).view(B, n, H, D)
     k = (h @ L["wk"].t()).view(B, n, Hkv, D)
     v = (h @ L["wv"].t()).view(B, n, Hkv, D)
-    q = rms(q, L["q_norm"], s.rms_eps)
     k = rms(k, L["k_norm"], s.rms_eps)
     cos, sin = rope_cos_sin(pos, W.inv_freq)                  # (B, n, D)
     cos, sin = cos[:, :, None, :], sin[:, :, None, :]
-    q = q * cos + rotate_half(q) * sin
     k = k * cos + rotate_half(k) * sin
+    if rows is not None:
+        rows = torch.as_tensor(rows, dtype=torch.int64, device=x.device)
+        h, cos, sin, x = h[:, rows], cos[:, rows], sin[:, rows], x[:, rows]
+        if q_scale is not None:
+            q_scale = q_scale[:, :, rows]
+    nq = h.shape[1]
+    q = rms((h @ L["wq"].t()).view(B, nq, H, D), L["q_norm"], s.rms_eps)
+    q = q * cos + rotate_half(q) * sin
     scale = 1.0 / math.sqrt(D)
     braw = None
     if bias_logit is not None:
@@ -103,8 +109,8 @@ def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Op
         q = q * q_temp[None, None, :, None]
     if q_scale is not None:
         q = q * q_scale.permute(0, 2, 1)[..., None]
-    attn, _ = oat.fwd(q, k, v, braw, scale, causal=True)
-    x = x + attn.reshape(B, n, H * D) @ L["wo"].t()
+    attn, _ = oat.fwd(q, k, v, braw, scale, causal=True, q_pos=rows)
+    x = x + attn.reshape(B, nq, H * D) @ L["wo"].t()
     if boundary is not None:
         boundary.append(x)
     return mlp_half(W, i, x), k, v

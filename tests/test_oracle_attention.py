@@ -181,6 +181,15 @@ def test_torch_oracle_matches_numpy(causal):
     got = ort.bwd(dout.float(), q.float(), k.float(), v.float(), b.float(), scale, causal, chunk=16)
     for r, t in zip(ref, got):
         np.testing.assert_allclose(t.numpy(), r, rtol=1e-3, atol=1e-4)
+    if causal:
+        # sampled query rows of a self-attention (Sq = Sk) against the numpy oracle's `rows`
+        q2, k2, v2, b2 = _inputs(1, 45, 45, 6, 2, 16, seed=22)
+        rows = np.array([0, 3, 20, 44])
+        o2, l2 = ora.keybias_fwd(q2.numpy(), k2.numpy(), v2.numpy(), b2.numpy(), scale, True, rows=rows)
+        t2, tl2 = ort.fwd(q2[:, rows].float(), k2.float(), v2.float(), b2.float(), scale, True, chunk=3,
+                          q_pos=torch.from_numpy(rows))
+        np.testing.assert_allclose(t2.numpy(), o2, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(tl2.numpy(), l2, rtol=1e-5, atol=1e-5)
 
 
 def test_bwd_given_out_and_bf16_operands():

@@ -151,6 +151,15 @@ def test_layer_matches_transformers_bias_and_temperature():
                     q_norm_mult=a)
     assert _rel(ours_t, ref_t) < 1e-5
     assert _rel(ours_t, ours) > 1e-3          # the temperature does change the result
+    # sampled query rows (each over every key it sees) against the same rows of the full layer
+    rows = torch.tensor([0, 1, 17, 50, 94, 95])
+    ours_r, k_r, _ = op.layer(W, 1, x, pos, bias_logit=bias, rows=rows)
+    assert ours_r.shape == (B, len(rows), s.d_model)
+    assert _rel(ours_r, ref[:, rows]) < 1e-5
+    qs = 0.5 + torch.rand(B, s.n_heads, n, generator=g)
+    full_q, k_f, _ = op.layer(W, 1, x, pos, bias_logit=bias, q_scale=qs)
+    rows_q, _, _ = op.layer(W, 1, x, pos, bias_logit=bias, q_scale=qs, rows=rows)
+    assert _rel(rows_q, full_q[:, rows]) < 1e-6 and torch.equal(k_r, k_f)
 
 
 @dataclass
