@@ -357,57 +357,90 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_prune_baseline(seconds=3.0):
-    """The oracle's top-K + keep + gathers (numpy, host cores) at the 32k gate workload, K=2000:
-    topk order, sort, keep list, hidden + 2 layers' K/V row gathers."""
-    import numpy as np
-    from oracle import gate as og
-    rng = np.random.default_rng(0)
-    S, s, e, K = 32768, 64, 32512, 2000
-    sc = rng.standard_normal(e - s).astype(np.float32)
-    hid = rng.standard_normal((S, 2048)).astype(np.float16)       # 2-byte rows like bf16
-    kvs = [rng.standard_normal((S, 8, 128)).astype(np.float16) for _ in range(4)]
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        kp = og.keep_indices(sc, K, s, e, S)
-        _ = hid[kp]
-        for t in kvs:
-            _ = t[kp]
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    return {"ms": round(dt * 1e3, 3), "cores": 1, "kind": "port", "cpu_model": cpu_model(),
-            "sample": "oracle numpy top-K + keep + gathers of hidden and 2 layers of K/V, 32k / K=2000"}
+def cpu_threads() -> int:
+    """Host threads for the CPU legs: the job's CPU share (OMP_NUM_THREADS when the environment
+    sets it), else every core this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    n = len(os.sched_getaffinity(0))
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
 
 
-def cpu_baseline(q, k, v, bias_raw, scale, seconds):
-    """Time the float32 oracle on the last query rows of the 32k workload (all heads) for about
-    `seconds` of CPU work; returns TFLOP/s of that sample and a description."""
-    import numpy as np
-    from oracle import attention as ora
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    except Exception:
-        threads = len(os.sched_getaffinity(0))
-    qn = q.float().cpu().numpy()
-    kn = k.float().cpu().numpy()
-    vn = v.float().cpu().numpy()
-    bn = bias_raw.cpu().numpy()
-    S, H = qn.shape[1], qn.shape[2]
-    chunk = 32
-    done_rows, flops = 0, 0.0
+def _median_s(fn, reps=3, warmup=1):
+    import statistics
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_prune_baseline():
+    """The reference's CPU pruning path (oracle.cpu_path.prune: torch.topk -> sort -> cat ->
+    index_select, gate_forward.py:1396-1470) at the 32k gate workload for each K: the state span's
+    fp32 scores, the hidden rows (32768 x 2048 bf16) and 2 layers of K/V (32768 x 8 x 128 bf16)
+    gathered; torch on the host's threads, median of 3 after 1 warmup."""
+    import torch
+    from oracle import cpu_path as cp
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    S, s, e = 32768, 64, 32512
+    g = torch.Generator().manual_seed(5)
+    sc = torch.randn(e - s, generator=g)
+    hid = torch.randn(S, 2048, generator=g).to(torch.bfloat16)
+    kvs = [torch.randn(S, 8, 128, generator=g).to(torch.bfloat16) for _ in range(4)]
+    res = {}
+    for K in (100, 500, 2000):
+        t = _median_s(lambda: cp.prune(sc, K, s, e, S, [hid] + kvs))
+        res[f"K{K}_ms"] = round(t * 1e3, 3)
+    res.update({"cores": threads, "kind": "port", "cpu_model": cpu_model(),
+                "sample": "reference CPU pruning path restated in torch (topk, sort, cat, index_select of "
+                          "hidden + 2 layers' K/V), 32k / K in {100, 500, 2000}, median of 3"})
+    return res
+
+
+def cpu_baseline(seconds):
+    """The reference's CPU attention path (oracle.cpu_path.sdpa_chunked: the SDPA compatibility
+    prefill, chunks of 128 query rows, additive float mask = key bias + causal -inf, K/V heads
+    repeated for GQA; sdpa_compat.py:6-37) in float32 on the host's threads.  value: a bounded
+    sample of the 32k workload -- the last query chunks (each over every key it sees), as many as
+    fit in about `seconds` -- in causal-counted TFLOP/s; c1: the whole 4k workload (batch 1, 16/8
+    heads, bias log(sigmoid(z)) z~N(0,2)), median of 3 after 1 warmup."""
+    import torch
+    from oracle import cpu_path as cp
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    H, Hkv, D = 16, 8, 128
+
+    def inputs(S, sigma, seed):
+        g = torch.Generator().manual_seed(seed)
+        q = torch.randn(1, H, S, D, generator=g) / math.sqrt(D)
+        k = torch.randn(1, Hkv, S, D, generator=g) / math.sqrt(D)
+        v = torch.randn(1, Hkv, S, D, generator=g)
+        b = torch.nn.functional.logsigmoid(torch.randn(1, S, generator=g) * sigma)
+        return q, k, v, b
+
+    q, k, v, b = inputs(4096, 2.0, 0)
+    t1 = _median_s(lambda: cp.sdpa_chunked(q, k, v, b))
+    c1 = {"ms": round(t1 * 1e3, 1), "tflops": round(causal_flops(1, H, 4096) / t1 / 1e12, 4)}
+    S = 32768
+    q, k, v, b = inputs(S, 3.0, 2)
+    chunk, done, flop = 128, 0, 0.0
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds and done_rows < S:
-        hi = S - done_rows
-        rows = np.arange(max(0, hi - chunk), hi)
-        ora.keybias_fwd(qn, kn, vn, bn, scale, True, rows=rows, dtype=np.float32)
-        flops += H * float(np.sum(4.0 * 128 * (rows + 1)))
-        done_rows += len(rows)
+    while time.perf_counter() - t0 < seconds and done < S:
+        hi = S - done
+        cp.sdpa_chunked(q, k, v, b, rows=range(hi - chunk, hi))
+        flop += 4.0 * H * D * sum(r + 1 for r in range(hi - chunk, hi))
+        done += chunk
     dt = time.perf_counter() - t0
-    return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "cpu_model": cpu_model(),
-            "sample": f"oracle float32 numpy fwd, last {done_rows} query rows x {H} heads of the 32k causal "
-                      f"workload (full key range each), {flops:.3e} FLOP in {dt:.1f} s"}
+            "sample": f"reference CPU attention path restated in torch (chunked SDPA, float mask, GQA by "
+                      f"repeat), float32: the last {done} query rows of the 32k causal workload in "
+                      f"{dt:.1f} s ({flop:.3e} causal FLOP)",
+            "c1_4k_whole": c1}
 
 
 def traffic_from_profile():
@@ -478,7 +511,8 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    cpu = cpu_baseline(q, k, v, bias_raw, scale, args.cpu_seconds) if args.cpu_seconds > 0 else None
+    del q, k, v, bias_raw
+    cpu = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 else None
     line = {
         "metric": "key-bias attn TFLOP/s at 32k bf16 (% MFMA peak); pruned-prefill TTFT ms",
         "value": round(value, 2),
