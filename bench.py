@@ -357,6 +357,61 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def gate_counter_run(dev, reps=5):
+    """Eager launches of the gate kernels for a per-dispatch counter profile: scoring at 32k; at 32k
+    for K in {100, 500, 2000} and on the ragged8 batch, the single-workgroup top-K, the pack, and
+    the multi-workgroup selection + pack (gate.select_pack), `reps` times each; then three plain
+    1 GiB device copies (counter calibration)."""
+    import torch
+    from tokengate_amd import gate
+    S, d, s, e = 32768, 2048, 64, 32512
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(S, d, generator=g, device=dev).to(torch.bfloat16)
+    a1 = math.sqrt(6.0 / (d + 256))
+    w1 = ((torch.rand(256, d, generator=g, device=dev) * 2 - 1) * a1).to(torch.bfloat16)
+    w2 = (torch.rand(256, generator=g, device=dev) * 2 - 1) * math.sqrt(6.0 / 257)
+    b1 = torch.zeros(256, device=dev)
+    scores = torch.zeros(S, dtype=torch.float32, device=dev)
+    for _ in range(reps):
+        gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e])
+    torch.cuda.synchronize()
+    print("gate counters: scoring done", flush=True)
+    kv = [torch.randn(S, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+
+    def one(sc, p, srcs, tag):
+        T = p.total_kept
+        outs = [torch.empty(T, *t.shape[1:], dtype=t.dtype, device=dev) for t in srcs]
+        pos = torch.empty(T, dtype=torch.int64, device=dev)
+        bias = torch.empty(T, dtype=torch.float32, device=dev)
+        pairs = list(zip(srcs, outs))
+        for _ in range(reps):
+            keep, ss = gate.select_keep(sc, p)
+            gate.pack(keep, p, pairs, positions=pos, bias_src=sc, sumsq=ss, bias_out=bias)
+        for _ in range(reps):
+            gate.select_pack(sc, p, pairs, positions=pos, bias_out=bias)
+        torch.cuda.synchronize()
+        print(f"gate counters: {tag} done ({T} kept)", flush=True)
+
+    for K in (100, 500, 2000):
+        one(scores, gate.plan([0], [S], [s], [e], [K], dev), [x] + kv, f"32k K{K}")
+    del x, kv
+    lens = [114517, 57946, 113394, 80391, 42386, 123699, 106754, 74151]
+    Ks = [2000, 4000, 100, 4000, 100, 100, 4000, 500]
+    R = sum(lens)
+    sc8 = torch.randn(R, generator=g, device=dev).to(torch.bfloat16).float()
+    x8 = torch.randn(R, 2048, generator=g, device=dev).to(torch.bfloat16)
+    kv8 = [torch.randn(R, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    p8 = gate.plan([sum(lens[:b]) for b in range(8)], lens, [64] * 8, [L - 256 for L in lens], Ks, dev)
+    one(sc8, p8, [x8] + kv8, "ragged8")
+    del x8, kv8
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("gate counters: calibration copies done", flush=True)
+
+
 def cpu_threads() -> int:
     """Host threads for the CPU legs: the job's CPU share (OMP_NUM_THREADS when the environment
     sets it), else every core this process may run on."""
@@ -465,6 +520,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run three plain 1 GiB device copies (counter calibration for HBM bytes)")
+    ap.add_argument("--gate-counters", action="store_true",
+                    help="only run eager launches of the gate kernels (for a per-dispatch counter profile)")
     ap.add_argument("--ttft-only", action="store_true",
                     help="only run 8 back-to-back gated prefills at 32k / K=2000 (for a kernel trace)")
     args = ap.parse_args()
@@ -481,6 +538,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.ttft_only:
         prefill_trace_run(dev)
+        return
+    if args.gate_counters:
+        gate_counter_run(dev)
         return
 
     S, H, Hkv = 32768, 16, 8
