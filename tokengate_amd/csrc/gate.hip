@@ -33,20 +33,27 @@ namespace {
 
 // ---------------------------------------------------------------------------------------------
 // Scoring head: s = w2 . silu(W1 x + b1) + b2, x in R^2048 (bf16), W1 (256 x 2048) bf16.
-// Workgroup: 8 waves, 128 rows; wave w owns rows 32(w%4)..+31 and hidden units 128(w/4)..+127
-// (4 column blocks of 32): two waves per SIMD, the partial w2 dot products of a row's two halves
-// added through LDS at the end.  K loop over the 2048 inputs in steps of 32 through a 4-deep LDS ring
-// (X tile 128 x 32 = 8 KiB, W1 tile 256 x 32 = 16 KiB per stage), unrolled so that every ring slot
-// index is a compile-time constant.  Accumulators are C^T blocks
-// (hidden unit = MFMA row, token = column) so each lane ends with one token's 16 hidden units
-// per block and the SiLU . w2 reduction is in-lane plus one cross-half exchange.
+// Workgroup: 8 waves, 128 rows; wave w owns rows 64(w%2)..+63 and hidden units 64(w/2)..+63
+// (2 x 2 blocks of 32 x 32): the shape that reads the fewest LDS bytes per MFMA (8 KiB of X and W
+// fragments per wave per k step).  K loop over the 2048 inputs in steps of 32 through a 6-deep
+// LDS ring filled by DMA (X tile 128 x 32 = 8 KiB, W1 tile 256 x 32 = 16 KiB per stage; 144 KiB),
+// unrolled so that every ring slot index is a compile-time constant, and software-pipelined: a
+// wave reads step k+1's fragments from LDS while its MFMAs of step k run, so the LDS reads and the
+// matrix cores overlap instead of alternating between the per-step barriers.  Accumulators are
+// C^T blocks (hidden unit = MFMA row, token = column): each lane ends with one token's hidden
+// units of each block, the SiLU . w2 reduction is in-lane plus one cross-half exchange, and the four
+// hidden quarters of a row are added through LDS in a fixed order.
+// Measured limiter: every 128-row tile re-streams all of W1 (1 MiB, L2-resident) through the LDS
+// DMA path next to its 512 KiB of X, and that path moves about 11-12 TB/s over the whole chip: with
+// the matrix work alone a launch takes 0.33x, with X alone 0.49x, with W1 alone 0.54x of the full
+// kernel's time at 710k rows.
 // ---------------------------------------------------------------------------------------------
 constexpr int kDin = 2048;
 constexpr int kDh = 256;
 constexpr int kSRows = 128;
 constexpr int kSK = 32;
 constexpr int kSThreads = 512;
-constexpr int kSStages = 4;
+constexpr int kSStages = 6;
 
 struct ScoreArgs {
   const bf16_t *x;
@@ -59,46 +66,49 @@ struct ScoreArgs {
 };
 
 __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
-  // X tile: 128 rows x 64 B, W tile: 256 rows x 64 B; 16-byte chunks, 4 per row, XOR-swizzled
+  // X tile: 128 rows x 64 B, W tile: 256 rows x 64 B; 16-byte chunks, 4 per row, XOR-swizzled.
   // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads
-  // only across distinct objects, so slot s+3's DMA does not hold up the reads of slot s.
+  // only across distinct objects, so a slot's DMA does not hold up the reads of the others.
   __shared__ __attribute__((aligned(1024))) char xs0[kSRows * kSK * 2], xs1[kSRows * kSK * 2],
-      xs2[kSRows * kSK * 2], xs3[kSRows * kSK * 2];
+      xs2[kSRows * kSK * 2], xs3[kSRows * kSK * 2], xs4[kSRows * kSK * 2], xs5[kSRows * kSK * 2];
   __shared__ __attribute__((aligned(1024))) char ws0[kDh * kSK * 2], ws1[kDh * kSK * 2], ws2[kDh * kSK * 2],
-      ws3[kDh * kSK * 2];
-  static_assert(kSStages == 4, "one named LDS object per ring slot");
+      ws3[kDh * kSK * 2], ws4[kDh * kSK * 2], ws5[kDh * kSK * 2];
+  static_assert(kSStages == 6, "one named LDS object per ring slot");
   auto xsl = [&](auto b) -> char * {
     constexpr int B = decltype(b)::value;
     if constexpr (B == 0) return xs0; else if constexpr (B == 1) return xs1; else if constexpr (B == 2) return xs2;
-    else return xs3;
+    else if constexpr (B == 3) return xs3; else if constexpr (B == 4) return xs4; else return xs5;
   };
   auto wsl = [&](auto b) -> char * {
     constexpr int B = decltype(b)::value;
     if constexpr (B == 0) return ws0; else if constexpr (B == 1) return ws1; else if constexpr (B == 2) return ws2;
-    else return ws3;
+    else if constexpr (B == 3) return ws3; else if constexpr (B == 4) return ws4; else return ws5;
   };
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
-  const int rg = wave & 3, hh = wave >> 2;   // row group, hidden half
+  const int rg = wave & 1, hq = wave >> 1;   // row half, hidden quarter
   const int64_t r0 = (int64_t)blockIdx.x * kSRows;
 
   const int64_t rows_here = min((int64_t)kSRows, a.n_rows - r0);
   const brsrc_t xrs = make_rsrc(a.x + r0 * a.x_rs, (uint32_t)(((rows_here - 1) * a.x_rs + kDin) * 2));
   const brsrc_t wrs = make_rsrc(a.w1, (uint32_t)(kDh * kDin * 2));
   // DMA slots: X tile = 512 chunks (one 1 KiB issue per wave), W tile = 1024 chunks (two);
-  // LDS row r, physical chunk p holds logical chunk p ^ ((r>>1)&3).  Per-lane source offsets
-  // (bytes) within a k step; the step's byte offset is added per issue.
+  // LDS row r (64 B), physical chunk p holds logical chunk p ^ ((r>>2)&3): the 16 rows that 16
+  // lanes read with one chunk index then land on 16 distinct 16-byte bank groups of the 64-bank
+  // LDS (rows r and r+1..3 share a 256-byte bank line at different quarters; rows 4 apart get
+  // different chunks).  Per-lane source offsets (bytes) within a k step; the step's byte offset is
+  // added per issue.
   uint32_t xoff, woff[2];
   {
     const int slot = wave * 64 + lane;                   // 0..511
     const int r = slot >> 2, p = slot & 3;
-    const int c = p ^ ((r >> 1) & 3);
+    const int c = p ^ ((r >> 2) & 3);
     xoff = (uint32_t)((r * a.x_rs + 8 * c) * 2);
   }
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int slot = (wave * 2 + it) * 64 + lane;        // 0..1023
     const int r = slot >> 2, p = slot & 3;
-    const int c = p ^ ((r >> 1) & 3);
+    const int c = p ^ ((r >> 2) & 3);
     woff[it] = (uint32_t)((r * kDin + 8 * c) * 2);
   }
   auto issue = [&](int kstep, auto buf_c) {
@@ -109,82 +119,116 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     for (int it = 0; it < 2; ++it) dma16(wrs, wd + (wave * 2 + it) * 1024, woff[it] + k0b);
   };
 
-  f32x16 acc[4];
+  // fragments of one k step: [substep s][block]: X^T columns (B operand, token 64rg + 32t + lq) and
+  // W1 rows (A operand, hidden unit 64hq + 32j + lq), k = 16s + 8g .. +7
+  struct Frags {
+    bf16x8 x[2][2], w[2][2];
+  };
+  auto read = [&](auto buf_c, Frags &f) {
+    const char *xb_lds = xsl(buf_c), *wb_lds = wsl(buf_c);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const uint32_t c = (uint32_t)(2 * s2 + g);
 #pragma unroll
-    for (int v = 0; v < 16; ++v) acc[j][v] = 0.f;
+      for (int b = 0; b < 2; ++b) {
+        const int xr = 64 * rg + 32 * b + lq;
+        const int wr = 64 * hq + 32 * b + lq;
+        f.x[s2][b] = lds_load16(xb_lds, xr * 64 + ((c ^ ((xr >> 2) & 3)) << 4));
+        f.w[s2][b] = lds_load16(wb_lds, wr * 64 + ((c ^ ((wr >> 2) & 3)) << 4));
+      }
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[j][t][v] = 0.f;
+  auto mma = [&](const Frags &f) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[j][t] = mfma32(f.w[s2][j], f.x[s2][t], acc[j][t]);
+  };
 
   constexpr int nk = kDin / kSK;
   constexpr int kOps = 3;   // DMA ops per thread per step (1 X + 2 W)
-  static_assert(nk % kSStages == 0, "the k loop is unrolled by the ring depth");
-  // One k step with a compile-time ring slot: reads of slot BUF and the DMA into slot
-  // (BUF + kSStages - 1) % kSStages are then provably disjoint, so the compiler does not make the
-  // reads wait for that DMA (with a run-time slot index it waits for every DMA in flight).
-  // WAITN: DMA ops this wave may leave in flight (the steps after ks already issued).
-  auto step = [&](int ks, auto buf_c, auto waitn_c) {
-    constexpr int BUF = decltype(buf_c)::value;
-    constexpr int NXT = (BUF + kSStages - 1) % kSStages;
-    wait_vm<decltype(waitn_c)::value>();   // step ks resident for this wave
-    ring_barrier();                        // ... for every wave; the slot of step ks-1 is free
-    if (ks + kSStages - 1 < nk) issue(ks + kSStages - 1, std::integral_constant<int, NXT>());
-    // B operand: X^T column (token) = lane's row 32*rg + lq; k = 16*s + 8g + j
-    const char *xb_lds = xsl(buf_c), *wb_lds = wsl(buf_c);
-    const int xr = 32 * rg + lq;
-    bf16x8 xb[2], wa[2][4];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int c = 2 * s + g;
-      xb[s] = lds_load16(xb_lds, xr * 64 + (((uint32_t)c ^ ((xr >> 1) & 3)) << 4));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int wr = 32 * (4 * hh + j) + lq;   // A operand: W1 row (hidden unit)
-        wa[s][j] = lds_load16(wb_lds, wr * 64 + (((uint32_t)c ^ ((wr >> 1) & 3)) << 4));
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);   // all 10 reads in flight before the first MFMA
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = mfma32(wa[s][j], xb[s], acc[j]);
+  static_assert(nk % kSStages == 4, "the k loop is unrolled by the ring depth, with a four-step tail");
+  // Iteration ks (compile-time ring slots): cur holds step ks's fragments (read in the previous
+  // iteration).  Wait until step ks+1's DMA of this wave is done (WAITN = DMA ops of later steps
+  // this wave may leave in flight), barrier (step ks+1 resident for every wave; the slot of step
+  // ks-1 is free), refill that slot with step ks+S-1, read step ks+1's fragments into nxt, then run
+  // step ks's MFMAs while those reads are in flight.
+  auto iter = [&](int ks, Frags &cur, Frags &nxt, auto next_c, auto waitn_c) {
+    constexpr int NX = decltype(next_c)::value;                   // slot of step ks+1
+    constexpr int FREE = (NX + kSStages - 2) % kSStages;          // slot of step ks-1
+    if (ks + 1 < nk) wait_vm<decltype(waitn_c)::value>();
+    ring_barrier();
+    if (ks + kSStages - 1 < nk) issue(ks + kSStages - 1, std::integral_constant<int, FREE>());
+    if (ks + 1 < nk) read(std::integral_constant<int, NX>(), nxt);
+    mma(cur);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
+  using I4 = std::integral_constant<int, 4>;
+  using I5 = std::integral_constant<int, 5>;
+  using W3 = std::integral_constant<int, 3 * kOps>;
   using W2 = std::integral_constant<int, 2 * kOps>;
   using W1 = std::integral_constant<int, kOps>;
+  using W0 = std::integral_constant<int, 0>;
+  Frags fa, fb;
   issue(0, I0());
   issue(1, I1());
   issue(2, I2());
+  issue(3, I3());
+  issue(4, I4());
+  wait_vm<4 * kOps>();   // step 0 resident for this wave
+  ring_barrier();
+  read(I0(), fa);
   int ks = 0;
-  for (; ks < nk - kSStages; ks += kSStages) {   // steady state: two later steps in flight
-    step(ks, I0(), W2());
-    step(ks + 1, I1(), W2());
-    step(ks + 2, I2(), W2());
-    step(ks + 3, I3(), W2());
+  // steady state: at iteration ks, steps ks+2 .. ks+4 may stay in flight while waiting for ks+1
+  for (; ks + kSStages <= nk - 4; ks += kSStages) {
+    iter(ks, fa, fb, I1(), W3());
+    iter(ks + 1, fb, fa, I2(), W3());
+    iter(ks + 2, fa, fb, I3(), W3());
+    iter(ks + 3, fb, fa, I4(), W3());
+    iter(ks + 4, fa, fb, I5(), W3());
+    iter(ks + 5, fb, fa, I0(), W3());
   }
-  step(ks, I0(), W2());
-  step(ks + 1, I1(), W2());
-  step(ks + 2, I2(), W1());
-  step(ks + 3, I3(), I0());
-  // epilogue: lane holds token (32*rg + lq), hidden units 32(4hh + j) + 8(v/4) + 4g + v%4
-  float part = 0.f;
+  // the last four steps (60..63, slots 0..3); nothing more is issued after step 63's DMA
+  iter(ks, fa, fb, I1(), W2());
+  iter(ks + 1, fb, fa, I2(), W1());
+  iter(ks + 2, fa, fb, I3(), W0());
+  iter(ks + 3, fb, fa, I0(), W0());
+
+  // epilogue: lane holds token 64rg + 32t + lq and hidden units 64hq + 32j + 8(v/4) + 4g + v%4
+  __shared__ float red[4][kSRows];   // per hidden quarter, per row
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int t = 0; t < 2; ++t) {
+    float part = 0.f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int u = 32 * (4 * hh + j) + 8 * (v >> 2) + 4 * g + (v & 3);
-      const float h = acc[j][v] + a.b1[u];
-      const float sl = h / (1.f + __expf(-h));
-      part = fmaf(sl, a.w2[u], part);
-    }
-  const float tot = pair_sum(part);
-  __shared__ float upper[kSRows];   // the second hidden half's sums, per row
-  if (hh == 1 && g == 0) upper[32 * rg + lq] = tot;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int u = 64 * hq + 32 * j + 8 * (v >> 2) + 4 * g + (v & 3);
+        const float h = acc[j][t][v] + a.b1[u];
+        const float sl = h / (1.f + __expf(-h));
+        part = fmaf(sl, a.w2[u], part);
+      }
+    const float tot = pair_sum(part);
+    if (g == 0) red[hq][64 * rg + 32 * t + lq] = tot;
+  }
   __syncthreads();
-  const int64_t row = r0 + 32 * rg + lq;
-  if (hh == 0 && g == 0 && row < a.n_rows) a.out[row] = (tot + upper[32 * rg + lq]) + a.b2;
+  if (tid < kSRows) {
+    const int64_t row = r0 + tid;
+    if (row < a.n_rows) a.out[row] = (((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid]) + a.b2;
+  }
 }
 
 // ---------------------------------------------------------------------------------------------
