@@ -185,7 +185,10 @@ int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_stride, int32
  * positions of the k_clamped largest scores in ascending position order, then art_end..seq_len-1.
  * Ties at the threshold go to the lower position; -0.0 equals +0.0; NaN ranks above +inf.
  * sumsq (optional, device fp32 per sequence) receives the sum of squared article scores.
- * max_article_len: the largest art_end - art_start (selects the LDS-resident variant). */
+ * max_article_len: the largest art_end - art_start, a speed hint only: it picks the register-
+ * resident variant for the launch, and any sequence whose article is longer than that variant
+ * holds (32768 or 65536 keys) takes the streaming path inside the same launch, so an understated
+ * value never truncates a keep list. */
 int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32_t num_seqs,
                       int32_t max_article_len, int64_t *keep, float *sumsq, hipStream_t stream);
 

@@ -158,6 +158,34 @@ def test_long_article_global_path(cuda):
     _check_select(s, seqs, cuda)
 
 
+def test_understated_max_article_len_falls_back_to_streaming(cuda):
+    """The C ABI's max_article_len only picks the kernel: a caller that understates it still gets
+    every keep list whole (sequences longer than the register capacity take the streaming path)."""
+    from tokengate_amd import _lib, gate
+    rng = np.random.default_rng(3)
+    lens = [70_000, 3000, 40_000]
+    seqs, r0 = [], 0
+    for L, K in zip(lens, [5000, 100, 20_000]):
+        seqs.append((r0, L, 64, L - 256, K))
+        r0 += L
+    sc = torch.from_numpy(rng.standard_normal(r0).astype(np.float32)).to(torch.bfloat16).float().numpy()
+    scores = torch.from_numpy(sc).to(cuda)
+    p = gate.plan([x[0] for x in seqs], [x[1] for x in seqs], [x[2] for x in seqs], [x[3] for x in seqs],
+                  [x[4] for x in seqs], cuda)
+    for hint in (1000, 32 * 1024, 64 * 1024):
+        keep = torch.full((p.total_kept,), -1, dtype=torch.int64, device=cuda)
+        sumsq = torch.empty(len(seqs), dtype=torch.float32, device=cuda)
+        _lib.call("tg_gate_topk_keep", scores.data_ptr(), p.geom.data_ptr(), len(seqs), hint, keep.data_ptr(),
+                  sumsq.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        got = keep.cpu().numpy()
+        for b, (r, L, s_, e_, K) in enumerate(seqs):
+            want = og.keep_indices(sc[r + s_:r + e_], K, s_, e_, L)
+            assert np.array_equal(got[p.cu_kept[b]:p.cu_kept[b + 1]], want), f"hint {hint} seq {b}"
+            np.testing.assert_allclose(float(sumsq[b]), float(np.sum(sc[r + s_:r + e_].astype(np.float64) ** 2)),
+                                       rtol=1e-5)
+
+
 @pytest.mark.parametrize("kind", ["few_values", "bf16_normal"])
 def test_streaming_ties_across_chunks(cuda, kind):
     """Ties at the threshold spread over several 32768-key chunks (the compaction carries the tie

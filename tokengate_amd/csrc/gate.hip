@@ -312,6 +312,9 @@ __device__ __forceinline__ void select_bin(int (*h)[256], int lane, uint32_t *se
 // t, t + 1024, ... (KPT of them), so every pass is register arithmetic plus LDS histogram
 // updates, and the index-order compaction works on 64-key blocks (block b = round r, wave w covers
 // positions 1024 r + 64 w .. +63) whose counts are scanned by one wave.
+__device__ __noinline__ void topk_stream_body(const float *scores, const int32_t *geom, int64_t *keep,
+                                                 float *sumsq);
+
 template <int KPT>
 __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float *scores, const int32_t *geom,
                                                                      int64_t *keep, float *sumsq) {
@@ -333,6 +336,12 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
   const int64_t kept0 = gm[5];
   const int n = e - s;
   const float *sc = scores + row_start + s;
+  // a sequence longer than the register capacity (the caller's max_article_len understated it)
+  // takes the streaming path: the result never depends on the hint, only the speed does
+  if (n > KPT * kTThreads) {
+    topk_stream_body(scores, geom, keep, sumsq);
+    return;
+  }
 
   // keys in registers (all loads in flight); 0 marks a position past the article
   const brsrc_t srs = make_rsrc(sc, n > 0 ? (uint32_t)n * 4u : 0u);
@@ -548,8 +557,8 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_reg_kernel(const float
 constexpr int kTChunk = 32;                 // keys per thread per chunk
 constexpr int kTChunkKeys = kTChunk * kTThreads;
 
-__global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const float *scores, const int32_t *geom,
-                                                                      int64_t *keep, float *sumsq) {
+__device__ __noinline__ void topk_stream_body(const float *scores, const int32_t *geom, int64_t *keep,
+                                                 float *sumsq) {
   constexpr int NB = kTChunk * kTWaves;   // 64-key blocks per chunk
   __shared__ int hist[2][kTWaves][256];
   __shared__ int bgt[NB], beq[NB], bkeep0[NB], beq0[NB];
@@ -726,6 +735,11 @@ __global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const fl
     }
     __syncthreads();   // the block tables are rewritten by the next chunk
   }
+}
+
+__global__ __launch_bounds__(kTThreads, 1) void gate_topk_stream_kernel(const float *scores, const int32_t *geom,
+                                                                      int64_t *keep, float *sumsq) {
+  topk_stream_body(scores, geom, keep, sumsq);
 }
 
 // ---------------------------------------------------------------------------------------------
