@@ -10,8 +10,9 @@
 //   * a workgroup owns one KV head and HP query heads of its GQA group (HP = 2 when the group
 //     size is even) over NW * 32/HP consecutive query positions; every K/V tile it streams
 //     through LDS serves all HP heads;
-//   * each wave owns 32 MFMA columns in two blocks of 16 (the HP = 2 heads, or two halves of 32
-//     query positions); the KV sequence is streamed in 64-key tiles by LDS DMA (buffer_load ...
+//   * each wave owns 32 MFMA columns in two blocks of 16: 32 consecutive query positions of one
+//     head (half the waves take each head of a pair), so a wave reads one head's key bias per
+//     tile; the KV sequence is streamed in 64-key tiles by LDS DMA (buffer_load ...
 //     lds: no staging registers, zero fill past Sk), double-buffered, one barrier per tile, the
 //     next tile in flight during compute;
 //   * scores are computed transposed, S^T = K Q^T, on v_mfma_f32_16x16x32_bf16 (on gfx950 it
@@ -43,11 +44,13 @@ constexpr int kD = 128;        // head dim
 constexpr int kBN = 64;        // keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-// A wave's 32 MFMA columns are HP heads x (32/HP) query positions; a workgroup of NW waves covers
-// NW * 32/HP positions.  NW = 8 (two waves per SIMD, one workgroup per CU) unless the grid would
-// then be too small to fill the chip, where NW = 4 (two workgroups per CU) halves the query tile.
+// A wave's 32 MFMA columns are 32 consecutive query positions of one head; a workgroup of NW waves
+// covers NW * 32/HP positions of its HP heads.  NW = 8 (two waves per SIMD, one workgroup per CU)
+// unless the grid would then be too small to fill the chip, where NW = 4 (two workgroups per CU)
+// halves the query tile.
 template <int HP> constexpr int qpw() { return 32 / HP; }
 template <int NW, int HP> constexpr int bm() { return NW * qpw<HP>(); }
+constexpr int kQW = 32;   // query positions per wave
 
 constexpr int kKRowBytes = kD * 2;      // one K or V row in LDS (256 B, 16 chunks of 16 B)
 constexpr int kKTileBytes = kBN * kKRowBytes;
@@ -113,15 +116,17 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return d;
 }
 
-// Column blocks of a wave: block cb (0, 1) is head cb of the workgroup's pair (HP = 2) or query
-// half cb (HP = 1); lane l holds column l%16 of each block.
-template <int HP> __device__ __forceinline__ int col_head(int cb) { return HP == 2 ? cb : 0; }
-template <int HP> __device__ __forceinline__ int col_query(int cb, int c16) { return HP == 2 ? c16 : 16 * cb + c16; }
+// Wave w owns head wave_head(w) of the workgroup's HP heads (waves 0 .. NW/2-1 the first of a pair,
+// the others the second) at positions wave_pos(w) .. +31 of the workgroup's query tile; its column
+// block cb (0, 1) is positions 16 cb .. 16 cb + 15 of those, lane l holding column l%16 of each.
+// One head per wave means one bias row per wave.
+template <int NW, int HP> __device__ __forceinline__ int wave_head(int w) { return HP == 2 ? w / (NW / 2) : 0; }
+template <int NW, int HP> __device__ __forceinline__ int wave_pos(int w) { return kQW * (HP == 2 ? w % (NW / 2) : w); }
+__device__ __forceinline__ int col_query(int cb, int c16) { return 16 * cb + c16; }
 
 template <int NW, int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a) {
   constexpr int kWaves = NW;
-  constexpr int QW = qpw<HP>();
   constexpr int BM = bm<NW, HP>();
   // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads only
   // across distinct objects, so the DMA of tile t+1 does not hold up the reads of tile t.
@@ -207,25 +212,26 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
       HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)(h0 + bwave) * a.bias_hs : nullptr;
   const brsrc_t brs = make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)sk * 4u : 0u);
 
-  // ---- this wave's queries and its Q fragments (B operand of S^T = K Q^T, 32 d per k-step) ----
-  const int qw0 = q0 + wave * QW;
+  // ---- this wave's head and queries, and its Q fragments (B operand of S^T = K Q^T, 32 d per
+  // k-step) ----
+  const int hw = wave_head<NW, HP>(wave);
+  const int qw0 = q0 + wave_pos<NW, HP>(wave);
   int qrow[2];
   bool qvalid[2];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    qrow[cb] = qw0 + col_query<HP>(cb, c16);
+    qrow[cb] = qw0 + col_query(cb, c16);
     qvalid[cb] = qrow[cb] < sq;
   }
   const bool wave_has_rows = qw0 < sq;
-  const int qw_hi = min(qw0 + QW, sq) - 1;
+  const int qw_hi = min(qw0 + kQW, sq) - 1;
   bf16x8 qf[2][4];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
       qf[cb][ks] = __builtin_bit_cast(
-          bf16x8, gload16(qbase + (int64_t)qrow[cb] * a.q_rs + (int64_t)col_head<HP>(cb) * a.q_hs + 32 * ks + 8 * G,
-                          qvalid[cb]));
+          bf16x8, gload16(qbase + (int64_t)qrow[cb] * a.q_rs + (int64_t)hw * a.q_hs + 32 * ks + 8 * G, qvalid[cb]));
 
   int kv_end = sk;
   if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
@@ -301,16 +307,14 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     // from the bias of their keys (raw-score units), so the bias add costs no VALU work. ----
     f32x4 sacc[2][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if constexpr (HAS_BIAS) {
-          sacc[cb][kb] = *reinterpret_cast<const f32x4 *>(
-              &bslot(buf_c)[col_head<HP>(cb)][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
-        } else {
-          sacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int kb = 0; kb < 4; ++kb) {
+      if constexpr (HAS_BIAS) {
+        // both column blocks are the wave's head: one read of its 16 keys' bias serves both
+        sacc[0][kb] = *reinterpret_cast<const f32x4 *>(&bslot(buf_c)[hw][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
+      } else {
+        sacc[0][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
+      sacc[1][kb] = sacc[0][kb];
     }
     // all 16 K fragments of the tile are read before the first MFMA, so LDS latency is paid once
     bf16x8 kfr[4][4];
@@ -461,7 +465,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
     if (!qvalid[cb]) continue;
-    const int hl = col_head<HP>(cb);
+    const int hl = hw;
     bf16_t *orow = obase + (int64_t)qrow[cb] * a.o_rs + (int64_t)hl * a.o_hs;
     const float s = inv[cb];
 #pragma unroll
@@ -492,7 +496,6 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
 constexpr int kCombineMaxGroups = 8;
 template <int NW, int HP, bool VARLEN>
 __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int CG) {
-  constexpr int QW = qpw<HP>();
   constexpr int BM = bm<NW, HP>();
   // (m, wsum, acc[8]) of groups 1..CG-1 of each piece: PP * (CG - 1) < 8 slots
   __shared__ float part[kCombineMaxGroups - 1][10][64];
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
   float (*mypart)[10][64] = part + pj * (CG - 1);
   const int c16 = lane & 15, G = lane >> 4;
   const int cb = j >> 2, p = j & 3;                        // column block, d-block pair of the piece
-  const int hl = col_head<HP>(cb);
+  const int hl = wave_head<NW, HP>(wave);
   const int per_q = a.hkv * (a.group / HP);
   const int x = (int)(hunit % per_q), r2 = (int)(hunit / per_q);
   const int kh = x % a.hkv, hg = x / a.hkv;
@@ -519,9 +522,9 @@ __global__ __launch_bounds__(512) void keybias_fwd_combine_kernel(FwdArgs a, int
     row0 = s0;
     sq = min(s1 - s0, a.sq);
   }
-  const int qw0 = qt * BM + wave * QW;
+  const int qw0 = qt * BM + wave_pos<NW, HP>(wave);
   if (qw0 >= sq) return;   // workgroup-uniform: the forward computed nothing for these rows
-  const int qrow = qw0 + col_query<HP>(cb, c16);
+  const int qrow = qw0 + col_query(cb, c16);
   const bool valid = qrow < sq;
 
   const float2 *ml = reinterpret_cast<const float2 *>(a.ws_ml);
