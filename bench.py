@@ -268,11 +268,12 @@ def bench_ttft(dev, reps=5):
 
     branch = G.random_branch_head(wts, 1, seed=5)
 
-    def decode_ms(r, head, steps=8, warmup=2):
+    def decode_ms(r, head, steps=8, warmup=2, graph=True):
         """Greedy decode after the prefill r (tokengate_amd.decode.DecodeState.step, all 28 layers,
-        attention over the pruned caches): median milliseconds per token over `steps` steps."""
+        attention over the pruned caches; graph=True: steps after the first replay one captured
+        HIP graph of the step): median milliseconds per token over `steps` steps."""
         from tokengate_amd.decode import DecodeState
-        st = DecodeState(wts, head, 1, r, steps + warmup + 1)
+        st = DecodeState(wts, head, 1, r, steps + warmup + 1, graph=graph)
         cur = r.first_tokens
         ts = []
         for i in range(steps + warmup):
@@ -299,6 +300,7 @@ def bench_ttft(dev, reps=5):
                      "phase_ms": {k: round(v, 3) for k, v in r.phase_ms.items()}}
         if decode:
             out[name]["decode_ms_per_token"] = decode_ms(r, head)
+            out[name]["decode_eager_ms_per_token"] = decode_ms(r, head, graph=False)
         if r.cu_kept[-1] <= 32768:
             # Phase 2 replayed from a captured graph (captured during the warm-up call)
             graphs = P.Phase2Graphs()

@@ -40,12 +40,14 @@ def _prompts(lens, spans, seed):
     return out
 
 
-@pytest.mark.parametrize("prune_below_gate,ssmax,branch,headroom", [
-    (False, False, False, True), (True, False, False, True), (False, True, False, True), (True, True, True, True),
-    (False, True, False, False), (True, False, False, False)])
-def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom):
+@pytest.mark.parametrize("prune_below_gate,ssmax,branch,headroom,graph", [
+    (False, False, False, True, False), (True, False, False, True, False), (False, True, False, True, False),
+    (True, True, True, True, False), (False, True, False, False, False), (True, False, False, False, False),
+    (False, False, False, True, True), (True, True, True, True, True), (True, False, False, False, True)])
+def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom, graph):
     """Greedy decode steps against the oracle, appending in place to the prefill's caches (headroom)
-    or to a copy laid out with room (a prefill without headroom)."""
+    or to a copy laid out with room (a prefill without headroom); with graph=True steps 2.. are
+    replays of one captured HIP graph of the step."""
     from tokengate_amd import inference as I
     from tokengate_amd.decode import DecodeState
     torch.set_num_threads(min(16, torch.get_num_threads()))
@@ -54,7 +56,7 @@ def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom):
     split = [I.split_state_span(p) for p in _prompts(lens, spans, 5)]
     steps = 4
     pf = m.prefill(split, Ks, prune_below_gate=prune_below_gate, decode_headroom=steps + 1 if headroom else 0)
-    st = DecodeState(m.weights, m.gate, m.gate_layer, pf, steps + 1, prune_below_gate)
+    st = DecodeState(m.weights, m.gate, m.gate_layer, pf, steps + 1, prune_below_gate, graph=graph)
     assert st.in_place == headroom
     if headroom:
         assert all(st.kv[l].k.data_ptr() == pf.kv[l].k.data_ptr() for l in range(len(st.kv)))
@@ -75,6 +77,32 @@ def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom):
             ma, rl = assert_close_grad(f"seq {b} step {i}", to_np(logits[i][b]), to_np(ref[1 + i]), rel_l2=2e-2)
             print(f"[decode] seq {b} step {i}: logits max-abs/max(1,|ref|) {ma:.2e} rel-L2 {rl:.2e}", flush=True)
             assert int(toks[i + 1][b]) == int(logits[i][b].argmax())
+    assert (st._graph is not None) == graph
+
+
+def test_decode_graph_replays_match_eager(cuda):
+    """Every replay of the captured decode step equals the eager step bit for bit (tokens and
+    logits), with eager work and host synchronisations between the replays; the two decodes
+    run over two identical prefills (each appends to its own caches)."""
+    from tokengate_amd import inference as I
+    from tokengate_amd.decode import DecodeState
+    m = _model(cuda, seed=6, ssmax=True)
+    split = [I.split_state_span(p) for p in _prompts([700, 420, 150], [(30, 640), (0, 400), (10, 140)], 8)]
+    steps = 7
+    pfs = [m.prefill(split, [40, 200, 1000], decode_headroom=steps + 1) for _ in range(2)]
+    eager = DecodeState(m.weights, m.gate, m.gate_layer, pfs[0], steps + 1)
+    graph = DecodeState(m.weights, m.gate, m.gate_layer, pfs[1], steps + 1, graph=True)
+    ce = cg = pfs[0].first_tokens
+    assert torch.equal(pfs[0].first_tokens, pfs[1].first_tokens)
+    for i in range(steps):
+        ce = eager.step(ce)
+        cg = graph.step(cg)
+        junk = torch.randn(1 << 20, device=cuda).sum()      # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(ce, cg), f"step {i}: tokens differ"
+        assert torch.equal(eager.last_logits, graph.last_logits), f"step {i}: logits differ"
+        assert bool(torch.isfinite(junk))
+    assert graph._graph is not None and eager._graph is None
 
 
 class _Tok:

@@ -14,7 +14,11 @@ place: each step's new K/V rows are written by the q/k-norm + RoPE kernel straig
 seg[b] + used[b] of each sequence's segment, and each layer's attention is ONE varlen launch
 (tg_keybias_varlen_kv_fwd) with one query row per sequence over its segment's used rows.  A
 prefill without enough headroom is re-laid out once (one copy per layer) into that layout.
-The per-step counters live on the device, so nothing in a step synchronises with the host.
+The per-step counters live on the device, so nothing in a step synchronises with the host, and
+every step launches the same kernels with the same arguments: with graph=True the second and
+later steps replay one captured HIP graph of the whole step (about 250 launches), whose inputs
+and outputs are static device buffers; the first step runs eagerly and warms every kernel and
+library handle the capture records.
 """
 import math
 from dataclasses import dataclass
@@ -51,7 +55,7 @@ def _relayout(kv: LayerKV, cu: List[int], gap: int) -> LayerKV:
 
 class DecodeState:
     def __init__(self, wts: DecoderWeights, head: ScoringHead, gate_layer: int, pf: PrefillResult,
-                 max_new_tokens: int, prune_below_gate: bool = False):
+                 max_new_tokens: int, prune_below_gate: bool = False, graph: bool = False):
         shape = wts.shape
         self.wts, self.shape = wts, shape
         dev = wts.device
@@ -96,14 +100,36 @@ class DecodeState:
         self.ssmax = pf.kept_ratio is not None
         self.n_kept_f = h2d(torch.tensor([float(x) for x in pf.n_kept], dtype=torch.float32), dev)
         self.cu_q = torch.arange(B + 1, dtype=torch.int32, device=dev)
+        self.rows_b = torch.arange(B, device=dev)
         self.steps = 0
+        self.step_f = torch.zeros((), dtype=torch.float32, device=dev)   # steps taken, on the device
         self.max_new_tokens = max_new_tokens
+        self.use_graph = graph
+        self._graph = None
+        self._tok_in = self._tok_out = None
 
     @torch.no_grad()
     def step(self, tokens: torch.Tensor) -> torch.Tensor:
         """Appends one token per sequence (tokens (B,) int64) and returns the next greedy tokens."""
         if self.steps >= self.max_new_tokens:
             raise RuntimeError("DecodeState: more steps than max_new_tokens (the caches are full)")
+        if not self.use_graph or self.steps == 0:
+            out = self._body(tokens)
+        else:
+            if self._graph is None:
+                self._tok_in = tokens.clone()
+                self._graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self._graph):
+                    self._tok_out = self._body(self._tok_in)
+            self._tok_in.copy_(tokens)
+            self._graph.replay()
+            out = self._tok_out.clone()
+        self.steps += 1
+        return out
+
+    def _body(self, tokens: torch.Tensor) -> torch.Tensor:
+        """One decode step as device work only (no host synchronisation, no host-side state), so
+        that it can be captured and replayed."""
         s, w = self.shape, self.wts
         B = self.B
         dev = tokens.device
@@ -118,7 +144,7 @@ class DecodeState:
         self.used += 1
         r_dec = None
         if self.ssmax:   # the new token's own ratio: slot n_kept + 1 + step at position next_pos
-            m = (self.n_kept_f + 1.0 + self.steps).clamp(min=2.0)
+            m = (self.n_kept_f + 1.0 + self.step_f).clamp(min=2.0)
             p = (self.next_pos.to(torch.float32) + 1.0).clamp(min=2.0)
             r_dec = (torch.log(m) / torch.log(p)).clamp(max=1.0)
         scale = 1.0 / math.sqrt(s.head_dim)
@@ -142,8 +168,8 @@ class DecodeState:
             act = silu_mul(torch.matmul(normed, lw.w_gu.t()))
             torch.matmul(act, lw.w_down.t(), out=hid)
         h = hid + res
-        self.next_pos = self.next_pos + 1
-        self.steps += 1
-        logits = logits_last(w, h, torch.arange(B, device=dev))
+        self.next_pos += 1
+        self.step_f += 1.0
+        logits = logits_last(w, h, self.rows_b)
         self.last_logits = logits
         return logits.argmax(-1)

@@ -177,7 +177,8 @@ class TokenGateModel:
             streamer.put(first.detach().cpu().view(B, 1))
         t0 = time.perf_counter()
         if max_new_tokens > 1:
-            st = DecodeState(self.weights, self.gate, self.gate_layer, pf, max_new_tokens, prune_below_gate)
+            st = DecodeState(self.weights, self.gate, self.gate_layer, pf, max_new_tokens, prune_below_gate,
+                             graph=True)
             cur = first
             done = torch.zeros(B, dtype=torch.bool, device=first.device)
             for _ in range(max_new_tokens - 1):
