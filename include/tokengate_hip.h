@@ -299,6 +299,22 @@ int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_stride, int6
 int tg_lm_head(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t vocab,
                int32_t dim, float *out, int64_t out_row_stride, hipStream_t stream);
 
+/* Decoder projections of a decode step (1 to 8 rows): out[b, v] = bf16(sum_d x[b, d] * weight[v, d]),
+ * accumulated in fp32 and stored as bf16 — F.linear(x, weight) on bf16 tensors, the nn.Linear
+ * q/k/v/o and gate/up/down projections of the Qwen3 layers the reference's decode loop calls
+ * once per step and layer (gate_decode.py:210-226, inner.layers[li](...)).  The weight is read once
+ * from HBM (the step is bound by streaming the layer weights).
+ * weight: (n_out, dim) bf16 row-major; dim a multiple of 512; out: bf16 rows of out_row_stride. */
+int tg_linear_rows(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t n_out,
+                   int32_t dim, void *out, int64_t out_row_stride, hipStream_t stream);
+
+/* Greedy next token: out[b] = argmax_v x[b, v] (int64) with torch.argmax's rules (a NaN wins, ties
+ * go to the lower index) — the reference's logits.argmax(-1) of the first-token and decode steps
+ * (gate_forward.py:1559-1562, gate_decode.py:227).  One launch and no memory clears, so a decode
+ * step captured in a graph replays it safely.  x: fp32 rows of x_row_stride (a multiple of 4). */
+int tg_argmax_rows(const float *x, int64_t x_row_stride, int32_t n_rows, int64_t n_cols, int64_t *out,
+                   hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

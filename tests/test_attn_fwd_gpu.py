@@ -50,6 +50,28 @@ def test_reference_grad_test_shapes(cuda, S):
     _check(q, k, v, bias_raw, scale, True, rows=rows, tag=f"S={S}")
 
 
+@pytest.mark.parametrize("key", [1, 10, 21, 45, 60, 70, 300])
+@pytest.mark.parametrize("causal", [True, False])
+def test_dominant_key_anywhere_in_its_tile(cuda, key, causal):
+    """One key whose biased logit exceeds every other key by about 250 log2 units: the running max
+    must be the true max over all 64 keys of a tile (a max over a subset of the tile's keys lets
+    2^(s - m) overflow to inf).  The key sits in each of the positions that different lanes of a
+    tile hold; 384 and 1000 tokens run the 4-wave tiling (1000 with the key-range split), 8192 the
+    8-wave one (checked on sampled rows)."""
+    g = torch.Generator(device=cuda).manual_seed(key + 1000 * causal)
+    for S, H, Hkv in [(384, 16, 8), (1000, 4, 2), (8192, 16, 8)]:
+        q, k, v = qkv(1, S, S, H, Hkv, g, cuda)
+        scale = 128 ** -0.5
+        bias = torch.randn(1, H, S, device=cuda, generator=g) * 2.0
+        bias[:, :, key] = 175.0                       # natural-log units: 252 log2 units above the rest
+        bias_raw = (bias.float() / scale).contiguous()
+        out, lse = _run(q, k, v, bias_raw, scale, causal)
+        assert bool(torch.isfinite(out.float()).all()) and bool(torch.isfinite(lse).all())
+        rows = None if S < 4096 else np.unique(np.concatenate([np.arange(0, 70), np.arange(max(0, key - 5), key + 70),
+                                                               np.linspace(0, S - 1, 60).astype(int)]))
+        _check(q, k, v, bias_raw, scale, causal, rows=rows, tag=f"S={S} dominant key {key} causal={causal}")
+
+
 @pytest.mark.parametrize("S", [1, 17, 63, 64, 65, 127, 128, 129, 200, 777])
 @pytest.mark.parametrize("H,Hkv", [(16, 8), (4, 4), (6, 2), (8, 2)])
 def test_ragged_lengths_and_groups(cuda, S, H, Hkv):

@@ -101,6 +101,20 @@ def test_lm_head_rejects_bad_arguments_without_touching_the_gpu():
     for args, msg in cases:
         rc = lib.tg_lm_head(*args)
         assert rc != 0 and msg in lib.tg_last_error(), (args, lib.tg_last_error())
+        rc = lib.tg_linear_rows(*args)
+        assert rc != 0 and msg in lib.tg_last_error(), ("linear_rows", args, lib.tg_last_error())
+
+
+def test_argmax_rows_rejects_bad_arguments_without_touching_the_gpu():
+    from tokengate_amd import _lib
+    lib = _lib.load()
+    # (x, x_row_stride, n_rows, n_cols, out, stream)
+    cases = [((None, 1000, 1, 1000, 16, None), b"null"), ((16, 1000, 1, 0, 16, None), b"n_cols"),
+             ((16, 999, 1, 1000, 16, None), b"stride"), ((16, 1002, 1, 1000, 16, None), b"stride"),
+             ((8, 1000, 1, 1000, 16, None), b"aligned")]
+    for args, msg in cases:
+        rc = lib.tg_argmax_rows(*args)
+        assert rc != 0 and msg in lib.tg_last_error(), (args, lib.tg_last_error())
 
 
 def test_fwd_workspace_size_queries():

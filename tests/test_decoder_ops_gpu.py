@@ -156,6 +156,47 @@ def test_lm_head(cuda, rows, vocab, dim):
     assert torch.equal(got.argmax(-1)[clear], tl.argmax(-1)[clear])
 
 
+@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (3, 2048, 6144), (8, 12288, 2048), (2, 2048, 1024)])
+def test_linear_rows(cuda, rows, n_out, dim):
+    """The decode-step projection GEMV (tg_linear_rows, bf16 out) against the float64 product of
+    the same bf16 inputs rounded to bf16 (F.linear on bf16 tensors): within one bf16 ulp
+    (summation order), into a strided output view as the decode step writes it."""
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows * 11 + n_out)
+    x = _bf(torch.randn(rows, dim + 64, generator=g, device=cuda))[:, :dim]
+    w = _bf(torch.randn(n_out, dim, generator=g, device=cuda) * dim ** -0.5)
+    buf = torch.zeros(rows, n_out + 32, dtype=torch.bfloat16, device=cuda)
+    got = dec.linear_rows(x, w, out=buf[:, :n_out])
+    torch.cuda.synchronize()
+    assert got.dtype == torch.bfloat16 and got.data_ptr() == buf.data_ptr()
+    assert bool((buf[:, n_out:] == 0).all())
+    ref = (x.double() @ w.double().t()).to(torch.bfloat16).double()
+    ulp = torch.finfo(torch.bfloat16).eps * ref.abs().clamp(min=1e-30)
+    err = (got.double() - ref).abs()
+    assert bool((err <= ulp + 1e-6).all()), float(err.max())
+    print(f"[linear_rows] rows {rows} ({n_out}, {dim}): equal to the rounded float64 product on "
+          f"{float((err == 0).double().mean()):.4f} of entries", flush=True)
+
+
+@pytest.mark.parametrize("rows,V", [(1, 151936), (3, 1001), (8, 151936)])
+def test_argmax_rows(cuda, rows, V):
+    """tg_argmax_rows against torch.argmax: bf16-valued logits (ties at the top are common), a
+    planted tie between two maxima, a NaN row, a row of -inf and a ragged length."""
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows + V)
+    pad = 4 - V % 4                               # a padded row stride that is a multiple of 4
+    x = torch.randn(rows, V + pad, generator=g, device=cuda).to(torch.bfloat16).float()[:, :V]
+    x[0, V // 3] = x[0, V - 1] = float(x[0].max()) + 1.0                      # tie: the lower index wins
+    if rows > 1:
+        x[1, 5] = float("nan")
+        x[1, V - 2] = float("nan")
+    if rows > 2:
+        x[2] = -float("inf")
+    got = dec.argmax_rows(x)
+    assert torch.equal(got, x.argmax(-1)), (got, x.argmax(-1))
+    assert int(got[0]) == V // 3
+
+
 def test_decoder_op_errors(cuda):
     from tokengate_amd import decoder as dec
     x = torch.zeros(4, 2050, dtype=torch.bfloat16, device=cuda)

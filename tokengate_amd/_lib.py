@@ -51,6 +51,8 @@ SIGNATURES = {
     "tg_silu_mul": [vp, i64, i64, i32, vp, i64, vp],
     "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
     "tg_lm_head": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
+    "tg_linear_rows": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
+    "tg_argmax_rows": [vp, i64, i32, i64, vp, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,
             "tg_keybias_varlen_fwd_workspace_size": C.c_int64, "tg_keybias_varlen_kv_fwd_workspace_size": C.c_int64,

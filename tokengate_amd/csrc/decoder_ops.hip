@@ -4,6 +4,8 @@
 //     and k / v into the layer's KV cache rows,
 //   * SiLU(gate) * up of the fused gate/up projection.
 // The projections themselves are plain GEMMs and stay on hipBLASLt.
+#include <type_traits>
+
 #include "tg_common.h"
 #include "../../include/tokengate_hip.h"
 
@@ -208,44 +210,131 @@ __global__ __launch_bounds__(256) void branch_readout_kernel(const bf16_t *__res
   if (lane == 0) out[row] = (float)(__bf16)acc;
 }
 
-// ---- LM head on a few rows: logits[b, v] = bf16(sum_d x[b, d] * w[v, d]) as fp32 -----------------
-// The vocab projection of the rows that produce the next token (F.linear on bf16 tensors, then
-// .float()).  HBM-bound on the (vocab, dim) weight: each wave owns 4 consecutive vocab rows and
-// issues all their 16-byte loads of a 512-element column chunk before the bf16 pair dot products;
-// the NR input rows are read from L2 alongside.
+// ---- Linear layer on a few rows: y[b, v] = bf16(sum_d x[b, d] * w[v, d]) ------------------------
+// F.linear on bf16 tensors for the rows of a decode step (1..8): the vocab projection of the rows
+// that produce the next token (written as fp32, .float() of the bf16 result) and the decoder
+// layers' projections (written as bf16).  HBM-bound on the (n_out, dim) weight: each wave owns 4
+// consecutive output rows and issues the 16-byte loads of up to four 512-element column chunks
+// of them (16 KB per wave) before their bf16 pair dot products, so that enough of the weight is
+// in flight to cover HBM latency even for a 2048 x 2048 matrix; the NR input rows come from L2.
+// The input x can be formed on the fly from the previous kernel's output, removing a launch:
+//   kPreNorm:   x = bf16(w_n * s / sqrt(mean(s^2) + eps)) with s = bf16(h + res) (res optional),
+//               exactly the RMSNorm kernel's arithmetic and summation order; block 0 writes
+//               res_out = s (a buffer other than res: every block reads res);
+//   kPreSwiGLU: x = bf16(silu(g) * u) of the gate/up rows [g | u], as the silu_mul kernel.
 constexpr int kLmMaxRows = 8;
-template <int NR>
-__global__ __launch_bounds__(256) void lm_head_kernel(const bf16_t *__restrict__ x, int64_t x_rs,
-                                                      const bf16_t *__restrict__ w, int64_t vocab, int dim,
-                                                      float *__restrict__ out, int64_t out_rs) {
+constexpr int kPrePlain = 0, kPreNorm = 1, kPreSwiGLU = 2;
+struct LinIn {
+  const bf16_t *x;          // plain: input rows; norm: h; swiglu: [gate | up] rows
+  int64_t x_rs;
+  const bf16_t *res;        // norm: residual stream in (NULL: s = h)
+  int64_t res_rs;
+  bf16_t *res_out;          // norm: s out (NULL: not written)
+  int64_t ro_rs;
+  const bf16_t *nw;         // norm weight (dim)
+  float eps;
+  int inter;                // swiglu: offset of u within a row (= dim)
+};
+template <int NR, int PRE>
+__device__ __forceinline__ u32x4 lin_input(const LinIn &in, int b, int c, const float (&rinv)[NR]) {
+  if constexpr (PRE == kPrePlain) {
+    return ld16(in.x + b * in.x_rs + c);
+  } else if constexpr (PRE == kPreSwiGLU) {
+    float g[8], u[8], y[8];
+    unpack8(ld16(in.x + b * in.x_rs + c), g);
+    unpack8(ld16(in.x + b * in.x_rs + in.inter + c), u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = g[e] / (1.f + __expf(-g[e])) * u[e];
+    return pack8(y);
+  } else {
+    float v[8], wf[8], y[8];
+    unpack8(ld16(in.x + b * in.x_rs + c), v);
+    if (in.res) {
+      float r[8];
+      unpack8(ld16(in.res + b * in.res_rs + c), r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
+    }
+    unpack8(ld16(in.nw + c), wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = wf[e] * (v[e] * rinv[b]);
+    return pack8(y);
+  }
+}
+// NCH consecutive 512-column chunks of a wave's 4 output rows: every weight load first, then the
+// bf16 pair dot products against the NR input rows.
+template <int NCH, int NR, int PRE>
+__device__ __forceinline__ void lin_chunks(const LinIn &in, const bf16_t *const (&wr)[4], int cg, int lane,
+                                           const float (&rinv)[NR], float (&acc)[4][NR]) {
+  u32x4 wv[NCH][4];
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[ch][r] = ld16(wr[r] + cg + 512 * ch);
+#pragma unroll
+  for (int ch = 0; ch < NCH; ++ch) {
+    const int c = cg + 512 * ch + 8 * lane;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      const u32x4 xv = lin_input<NR, PRE>(in, b, c, rinv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t wd = wv[ch][r][e], xd = xv[e];   // scalar copies: see u32_as_f32
+          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wd), __builtin_bit_cast(bf16x2, xd),
+                                                      acc[r][b], false);
+        }
+    }
+  }
+}
+template <int NR, typename OutT, int PRE>
+__global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t *__restrict__ w, int64_t vocab,
+                                                          int dim, OutT *__restrict__ out, int64_t out_rs) {
   const int lane = threadIdx.x & 63;
   const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
   if (v0 >= vocab) return;
+  float rinv[NR];
+  if constexpr (PRE == kPreNorm) {
+    // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ... element
+    // by element, then the wave butterfly
+    const bool writer = blockIdx.x == 0 && wave_id() == 0 && in.res_out != nullptr;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      float ss = 0.f;
+      for (int c = 8 * lane; c < dim; c += 512) {
+        float v[8];
+        unpack8(ld16(in.x + b * in.x_rs + c), v);
+        if (in.res) {
+          float r[8];
+          unpack8(ld16(in.res + b * in.res_rs + c), r);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
+        }
+        if (writer) st16(in.res_out + b * in.ro_rs + c, pack8(v));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+      }
+      ss = wave_sum(ss);
+      rinv[b] = rsqrtf(ss / (float)dim + in.eps);
+    }
+  }
   float acc[4][NR];
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int b = 0; b < NR; ++b) acc[r][b] = 0.f;
-  for (int c = 0; c < dim; c += 512) {
-    u32x4 wv[4], xv[NR];
+  // rows past the end read the last row (in bounds; their sums are not stored)
+  const bf16_t *wr[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      wv[r] = u32x4{0u, 0u, 0u, 0u};
-      if (v0 + r < vocab) wv[r] = *reinterpret_cast<const u32x4 *>(w + (v0 + r) * dim + c + 8 * lane);
-    }
-#pragma unroll
-    for (int b = 0; b < NR; ++b) xv[b] = *reinterpret_cast<const u32x4 *>(x + b * x_rs + c + 8 * lane);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int b = 0; b < NR; ++b)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t wd = wv[r][e], xd = xv[b][e];
-          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wd), __builtin_bit_cast(bf16x2, xd),
-                                                      acc[r][b], false);
-        }
+  for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
+  int cg = 0;
+  for (; cg + 2048 <= dim; cg += 2048) lin_chunks<4, NR, PRE>(in, wr, cg, lane, rinv, acc);
+  if (dim - cg >= 1024) {
+    lin_chunks<2, NR, PRE>(in, wr, cg, lane, rinv, acc);
+    cg += 1024;
   }
+  if (dim - cg >= 512) lin_chunks<1, NR, PRE>(in, wr, cg, lane, rinv, acc);
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -255,7 +344,55 @@ __global__ __launch_bounds__(256) void lm_head_kernel(const bf16_t *__restrict__
     for (int r = 0; r < 4; ++r)
       if (v0 + r < vocab)
 #pragma unroll
-        for (int b = 0; b < NR; ++b) out[b * out_rs + v0 + r] = (float)(__bf16)acc[r][b];
+        for (int b = 0; b < NR; ++b) {
+          const __bf16 y = (__bf16)acc[r][b];
+          if constexpr (std::is_same<OutT, float>::value)
+            out[b * out_rs + v0 + r] = (float)y;
+          else
+            out[b * out_rs + v0 + r] = __builtin_bit_cast(bf16_t, y);
+        }
+  }
+}
+
+// ---- Greedy token: the index of each row's largest logit -----------------------------------------
+// torch.argmax semantics: a NaN beats every number, and equal values go to the lower index.  One
+// 1024-thread workgroup per row: each thread scans its strided 16-byte pieces, then the (value,
+// index) pairs are folded across the wave and, through LDS, across the 16 waves.
+__device__ __forceinline__ bool amax_better(float a, int64_t ia, float b, int64_t ib) {
+  const bool na = a != a, nb = b != b;
+  if (na) return nb ? ia < ib : true;
+  if (nb) return false;
+  return a == b ? ia < ib : a > b;
+}
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restrict__ x, int64_t rs, int64_t n,
+                                                           int64_t *__restrict__ out) {
+  const float *row = x + (int64_t)blockIdx.x * rs;
+  float best = -INFINITY;
+  int64_t bi = n;   // no element yet: loses every comparison with a real one
+  const int64_t n4 = n / 4;
+  for (int64_t j = threadIdx.x; j < n4; j += 1024) {
+    const f32x4 v = *reinterpret_cast<const f32x4 *>(row + 4 * j);
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (amax_better(v[e], 4 * j + e, best, bi)) { best = v[e]; bi = 4 * j + e; }
+  }
+  for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += 1024)
+    if (amax_better(row[j], j, best, bi)) { best = row[j]; bi = j; }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ob = __shfl_xor(best, o);
+    const int64_t oi = __shfl_xor(bi, o);
+    if (amax_better(ob, oi, best, bi)) { best = ob; bi = oi; }
+  }
+  __shared__ float sb[16];
+  __shared__ int64_t si[16];
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { sb[w] = best; si[w] = bi; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 16; ++k)
+      if (amax_better(sb[k], si[k], best, bi)) { best = sb[k]; bi = si[k]; }
+    out[blockIdx.x] = bi;
   }
 }
 
@@ -384,25 +521,118 @@ extern "C" int tg_gate_branch_readout(const void *gate_up, int64_t gate_up_row_s
   return 0;
 }
 
+namespace tg {
+namespace {
+
+template <typename OutT, int PRE>
+int launch_linear_rows(const LinIn &in, int32_t n_rows, const void *weight, int64_t n_out, int32_t dim, OutT *out,
+                       int64_t out_row_stride, hipStream_t stream) {
+  const int64_t blocks = (n_out + 15) / 16;
+  const bf16_t *wp = static_cast<const bf16_t *>(weight);
+#define TG_LR(NR)                                                                                          \
+  if (n_rows == NR)                                                                                        \
+    hipLaunchKernelGGL((linear_rows_kernel<NR, OutT, PRE>), dim3((unsigned)blocks), dim3(256), 0, stream, in, wp, \
+                       n_out, dim, out, out_row_stride);
+  TG_LR(1) TG_LR(2) TG_LR(3) TG_LR(4) TG_LR(5) TG_LR(6) TG_LR(7) TG_LR(8)
+#undef TG_LR
+  TG_HIP_CHECK(hipGetLastError());
+  return 0;
+}
+int check_linear_rows(const char *what, const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight,
+                      int64_t n_out, int32_t dim, const void *out, int64_t out_row_stride) {
+  TG_CHECK(x && weight && out, "%s: null pointer", what);
+  TG_CHECK(n_rows >= 1 && n_rows <= kLmMaxRows, "%s: 1 to %d rows (got %d)", what, kLmMaxRows, n_rows);
+  TG_CHECK(dim > 0 && dim % 512 == 0, "%s: dim must be a positive multiple of 512 (got %d)", what, dim);
+  TG_CHECK(n_out > 0 && x_row_stride % 8 == 0 && x_row_stride >= dim && out_row_stride >= n_out,
+           "%s: bad output size or row strides", what);
+  TG_CHECK(aligned16(x) && aligned16(weight), "%s: x and weight must be 16-byte aligned", what);
+  TG_CHECK((n_out + 15) / 16 < (1ll << 31), "%s: too many output features", what);
+  return 0;
+}
+
+}  // namespace
+}  // namespace tg
+
+using namespace tg;
+
 extern "C" int tg_lm_head(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t vocab,
                           int32_t dim, float *out, int64_t out_row_stride, hipStream_t stream) {
   clear_error();
-  TG_CHECK(x && weight && out, "lm_head: null pointer");
-  TG_CHECK(n_rows >= 1 && n_rows <= kLmMaxRows, "lm_head: 1 to %d rows (got %d)", kLmMaxRows, n_rows);
-  TG_CHECK(dim > 0 && dim % 512 == 0, "lm_head: dim must be a positive multiple of 512 (got %d)", dim);
-  TG_CHECK(vocab > 0 && x_row_stride % 8 == 0 && x_row_stride >= dim && out_row_stride >= vocab,
-           "lm_head: bad vocab or row strides");
-  TG_CHECK(aligned16(x) && aligned16(weight), "lm_head: x and weight must be 16-byte aligned");
-  const int64_t blocks = (vocab + 15) / 16;
-  TG_CHECK(blocks < (1ll << 31), "lm_head: vocab too large");
-  const bf16_t *xp = static_cast<const bf16_t *>(x);
-  const bf16_t *wp = static_cast<const bf16_t *>(weight);
-#define TG_LM(NR)                                                                                          \
-  if (n_rows == NR)                                                                                        \
-    hipLaunchKernelGGL(lm_head_kernel<NR>, dim3((unsigned)blocks), dim3(256), 0, stream, xp, x_row_stride, wp, \
-                       vocab, dim, out, out_row_stride);
-  TG_LM(1) TG_LM(2) TG_LM(3) TG_LM(4) TG_LM(5) TG_LM(6) TG_LM(7) TG_LM(8)
-#undef TG_LM
+  if (int e = check_linear_rows("lm_head", x, x_row_stride, n_rows, weight, vocab, dim, out, out_row_stride)) return e;
+  LinIn in{};
+  in.x = static_cast<const bf16_t *>(x);
+  in.x_rs = x_row_stride;
+  return launch_linear_rows<float, kPrePlain>(in, n_rows, weight, vocab, dim, out, out_row_stride, stream);
+}
+
+extern "C" int tg_linear_rows(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight,
+                              int64_t n_out, int32_t dim, void *out, int64_t out_row_stride, hipStream_t stream) {
+  clear_error();
+  if (int e = check_linear_rows("linear_rows", x, x_row_stride, n_rows, weight, n_out, dim, out, out_row_stride))
+    return e;
+  LinIn in{};
+  in.x = static_cast<const bf16_t *>(x);
+  in.x_rs = x_row_stride;
+  return launch_linear_rows<bf16_t, kPrePlain>(in, n_rows, weight, n_out, dim, static_cast<bf16_t *>(out),
+                                               out_row_stride, stream);
+}
+
+extern "C" int tg_linear_rows_norm(const void *h, int64_t h_row_stride, const void *residual,
+                                   int64_t residual_row_stride, void *residual_out, int64_t residual_out_row_stride,
+                                   const void *norm_weight, float eps, int32_t n_rows, const void *weight,
+                                   int64_t n_out, int32_t dim, void *out, int64_t out_row_stride, int32_t out_fp32,
+                                   hipStream_t stream) {
+  clear_error();
+  if (int e = check_linear_rows("linear_rows_norm", h, h_row_stride, n_rows, weight, n_out, dim, out, out_row_stride))
+    return e;
+  TG_CHECK(norm_weight && aligned16(norm_weight), "linear_rows_norm: norm weight must be non-null and 16-byte aligned");
+  TG_CHECK(!residual || (aligned16(residual) && residual_row_stride % 8 == 0 && residual_row_stride >= dim),
+           "linear_rows_norm: bad residual");
+  TG_CHECK(!residual_out || (aligned16(residual_out) && residual_out_row_stride % 8 == 0 &&
+                             residual_out_row_stride >= dim && residual_out != residual),
+           "linear_rows_norm: bad residual_out (it must not be the residual input)");
+  TG_CHECK(eps >= 0.f, "linear_rows_norm: eps must be non-negative");
+  LinIn in{};
+  in.x = static_cast<const bf16_t *>(h);
+  in.x_rs = h_row_stride;
+  in.res = static_cast<const bf16_t *>(residual);
+  in.res_rs = residual_row_stride;
+  in.res_out = static_cast<bf16_t *>(residual_out);
+  in.ro_rs = residual_out_row_stride;
+  in.nw = static_cast<const bf16_t *>(norm_weight);
+  in.eps = eps;
+  if (out_fp32)
+    return launch_linear_rows<float, kPreNorm>(in, n_rows, weight, n_out, dim, static_cast<float *>(out),
+                                               out_row_stride, stream);
+  return launch_linear_rows<bf16_t, kPreNorm>(in, n_rows, weight, n_out, dim, static_cast<bf16_t *>(out),
+                                              out_row_stride, stream);
+}
+
+extern "C" int tg_linear_rows_swiglu(const void *gate_up, int64_t gate_up_row_stride, int32_t n_rows, int32_t inter,
+                                     const void *weight, int64_t n_out, void *out, int64_t out_row_stride,
+                                     hipStream_t stream) {
+  clear_error();
+  if (int e = check_linear_rows("linear_rows_swiglu", gate_up, gate_up_row_stride, n_rows, weight, n_out, inter, out,
+                                out_row_stride))
+    return e;
+  TG_CHECK(gate_up_row_stride >= 2 * (int64_t)inter, "linear_rows_swiglu: gate/up rows hold 2 * inter values");
+  LinIn in{};
+  in.x = static_cast<const bf16_t *>(gate_up);
+  in.x_rs = gate_up_row_stride;
+  in.inter = inter;
+  return launch_linear_rows<bf16_t, kPreSwiGLU>(in, n_rows, weight, n_out, inter, static_cast<bf16_t *>(out),
+                                                out_row_stride, stream);
+}
+
+extern "C" int tg_argmax_rows(const float *x, int64_t x_row_stride, int32_t n_rows, int64_t n_cols, int64_t *out,
+                              hipStream_t stream) {
+  clear_error();
+  TG_CHECK(x && out, "argmax_rows: null pointer");
+  TG_CHECK(n_rows >= 0 && n_cols > 0, "argmax_rows: need n_rows >= 0 and n_cols > 0");
+  TG_CHECK(x_row_stride >= n_cols && x_row_stride % 4 == 0, "argmax_rows: row stride must be >= n_cols and a multiple of 4");
+  TG_CHECK(aligned16(x), "argmax_rows: x must be 16-byte aligned");
+  if (n_rows == 0) return 0;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)n_rows), dim3(1024), 0, stream, x, x_row_stride, n_cols, out);
   TG_HIP_CHECK(hipGetLastError());
   return 0;
 }

@@ -63,21 +63,28 @@ __device__ __forceinline__ u32x4 gload16(const bf16_t *p, bool valid) {
 
 // Combine a value held by lane l and lane l^32 (the two halves of a wave64).
 __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(x, 32)); }
+// Reinterpret a 32-bit value as float.  Use this (or a copy into a scalar) instead of applying
+// __builtin_bit_cast to an element of a vector or of a builtin's result pair directly: this
+// compiler lowers __builtin_bit_cast(float, v[i]) to element 0 whatever i is.
+__device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
+// max of the two values a permlane swap returns
+template <typename Pair> __device__ __forceinline__ float swap_pair_max(const Pair &sw) {
+  const uint32_t lo = sw[0], hi = sw[1];
+  return fmaxf(u32_as_f32(lo), u32_as_f32(hi));
+}
 // Same as pair_max without the LDS crossbar: v_permlane32_swap(x, x) returns (lower half in both
 // halves, upper half in both halves), so the max of the two is max(x[l], x[l^32]) in every lane.
 __device__ __forceinline__ float half_swap_max(float x) {
-  const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                   false, false);
-  return fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1]));
+  return swap_pair_max(__builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                        __builtin_bit_cast(uint32_t, x), false, false));
 }
 __device__ __forceinline__ float pair_sum(float x) { return x + __shfl_xor(x, 32); }
 // Max over the four 16-lane groups (lanes l, l^16, l^32, l^48): v_permlane16_swap(x, x) returns
 // (rows 0 and 2 in both rows of each pair, rows 1 and 3 likewise), whose max is max(x[l], x[l^16]);
 // then the same across the two halves.
 __device__ __forceinline__ float quad_swap_max(float x) {
-  const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x), __builtin_bit_cast(uint32_t, x),
-                                                   false, false);
-  return half_swap_max(fmaxf(__builtin_bit_cast(float, sw[0]), __builtin_bit_cast(float, sw[1])));
+  return half_swap_max(swap_pair_max(__builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                                      __builtin_bit_cast(uint32_t, x), false, false)));
 }
 __device__ __forceinline__ float quad_sum(float x) {
   x += __shfl_xor(x, 16);

@@ -26,8 +26,8 @@ from typing import List, Optional
 
 import torch
 
-from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, h2d, logits_last, qk_norm_rope, rmsnorm,
-                                   silu_mul, varlen_kv_attention)
+from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, argmax_rows, h2d, linear_rows, logits_last,
+                                   qk_norm_rope, rmsnorm, silu_mul, varlen_kv_attention)
 from tokengate_amd.gate import ScoringHead
 from tokengate_amd.prefill import PrefillResult
 
@@ -156,20 +156,20 @@ class DecodeState:
                 rmsnorm(res, lw.ln1, s.rms_eps, out=normed)
             else:
                 rmsnorm(hid, lw.ln1, s.rms_eps, residual=res, residual_out=res, out=normed)
-            torch.matmul(normed, lw.w_qkv.t(), out=qkv)
+            linear_rows(normed, lw.w_qkv, out=qkv)
             kv = self.kv[l]
             q = qk_norm_rope(qkv, self.next_pos, lw, s, w.inv_freq, kv.k, kv.v,
                              self.qscale[j] if (g and self.qscale is not None) else None,
                              r_dec if (r_dec is not None and g) else None, kv_rows=rows[g])
             varlen_kv_attention(q, kv.k, kv.v, self.cu_q, self.seg_dev[g], self.used[g], 1, self.cap_k[g], scale,
                                 self.bias[j] if g else None, out=att, lse=lse)
-            torch.matmul(att.view(B, -1), lw.w_o.t(), out=hid)
+            linear_rows(att.view(B, -1), lw.w_o, out=hid)
             rmsnorm(hid, lw.ln2, s.rms_eps, residual=res, residual_out=res, out=normed)
-            act = silu_mul(torch.matmul(normed, lw.w_gu.t()))
-            torch.matmul(act, lw.w_down.t(), out=hid)
+            act = silu_mul(linear_rows(normed, lw.w_gu))
+            linear_rows(act, lw.w_down, out=hid)
         h = hid + res
         self.next_pos += 1
         self.step_f += 1.0
         logits = logits_last(w, h, self.rows_b)
         self.last_logits = logits
-        return logits.argmax(-1)
+        return argmax_rows(logits)

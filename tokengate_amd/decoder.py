@@ -413,6 +413,32 @@ def lm_head(normed: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """F.linear(x, weight) on bf16 tensors for the rows of a decode step: tg_linear_rows (a GEMV
+    that streams the weight once) for up to 8 rows, torch's GEMM otherwise."""
+    n, d = x.shape
+    if n > 8 or d % 512 != 0 or x.stride(1) != 1 or weight.stride(1) != 1 or weight.stride(0) != d \
+            or (out is not None and out.stride(1) != 1):
+        return torch.matmul(x, weight.t(), out=out)
+    N = weight.shape[0]
+    out = torch.empty(n, N, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _lib.call("tg_linear_rows", x.data_ptr(), x.stride(0), n, weight.data_ptr(), N, d, out.data_ptr(), out.stride(0),
+              _stream(x))
+    return out
+
+
+def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
+    """logits.argmax(-1) (int64) of fp32 rows with torch's rules (NaN wins, ties to the lower
+    index) in one launch that clears no memory (tg_argmax_rows)."""
+    n, V = logits.shape
+    if logits.dtype != torch.float32 or logits.stride(1) != 1 or logits.stride(0) % 4 != 0 \
+            or logits.data_ptr() % 16 != 0:
+        raise RuntimeError("argmax_rows: fp32 rows, contiguous, 16-byte aligned, row stride a multiple of 4")
+    out = torch.empty(n, dtype=torch.int64, device=logits.device)
+    _lib.call("tg_argmax_rows", logits.data_ptr(), logits.stride(0), n, V, out.data_ptr(), _stream(logits))
+    return out
+
+
 def logits_last(wts: DecoderWeights, h: torch.Tensor, last_rows: torch.Tensor) -> torch.Tensor:
     """Final norm + LM head on the given rows only (the rows that produce the next token)."""
     rows = h.index_select(0, last_rows)

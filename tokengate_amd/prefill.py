@@ -30,8 +30,8 @@ from typing import Dict, List, Optional, Sequence
 import torch
 
 from tokengate_amd import gate as G
-from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, h2d, logits_last,
-                                   mlp_sublayer, run_layers)
+from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, Ragged, Workspace, alloc_kv, argmax_rows, h2d,
+                                   logits_last, mlp_sublayer, run_layers)
 
 
 @dataclass
@@ -286,7 +286,7 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     mark("head")
     last = h2d(torch.tensor(p.cu_kept[1:], dtype=torch.int64).sub_(1), dev)
     logits = logits_last(wts, h2, last)
-    first = logits.argmax(-1)
+    first = argmax_rows(logits)
     mark("end")
     phase_ms = {}
     if ev is not None:
