@@ -308,6 +308,25 @@ int tg_lm_head(const void *x, int64_t x_row_stride, int32_t n_rows, const void *
 int tg_linear_rows(const void *x, int64_t x_row_stride, int32_t n_rows, const void *weight, int64_t n_out,
                    int32_t dim, void *out, int64_t out_row_stride, hipStream_t stream);
 
+/* tg_linear_rows with the input formed from the previous sublayer's output, one launch instead of
+ * two: x = RMSNorm(s) = bf16(norm_weight * s / sqrt(mean(s^2) + eps)) with s = bf16(h + residual)
+ * (residual NULL: s = h), the same arithmetic and summation order as tg_rmsnorm; s is also written
+ * to residual_out (NULL: not written), which must not be the residual input (every workgroup reads
+ * it).  The decode step's input_layernorm -> q/k/v projection, post_attention_layernorm -> gate/up
+ * projection and final norm -> LM head (Qwen3DecoderLayer / Qwen3Model.norm / lm_head as the
+ * reference's decode loop calls them, gate_decode.py:210-227).  out_fp32: write the bf16 result
+ * as fp32 (the logits), else as bf16. */
+int tg_linear_rows_norm(const void *h, int64_t h_row_stride, const void *residual, int64_t residual_row_stride,
+                        void *residual_out, int64_t residual_out_row_stride, const void *norm_weight, float eps,
+                        int32_t n_rows, const void *weight, int64_t n_out, int32_t dim, void *out,
+                        int64_t out_row_stride, int32_t out_fp32, hipStream_t stream);
+
+/* tg_linear_rows of the SwiGLU product: x = bf16(silu(g) * u) of the gate/up rows [g | u] (inter
+ * values each), as tg_silu_mul computes it — Qwen3MLP's down_proj(act_fn(gate_proj(x)) *
+ * up_proj(x)) in the decode step (gate_decode.py:210-226). */
+int tg_linear_rows_swiglu(const void *gate_up, int64_t gate_up_row_stride, int32_t n_rows, int32_t inter,
+                          const void *weight, int64_t n_out, void *out, int64_t out_row_stride, hipStream_t stream);
+
 /* Greedy next token: out[b] = argmax_v x[b, v] (int64) with torch.argmax's rules (a NaN wins, ties
  * go to the lower index) — the reference's logits.argmax(-1) of the first-token and decode steps
  * (gate_forward.py:1559-1562, gate_decode.py:227).  One launch and no memory clears, so a decode

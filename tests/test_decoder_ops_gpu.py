@@ -178,6 +178,35 @@ def test_linear_rows(cuda, rows, n_out, dim):
           f"{float((err == 0).double().mean()):.4f} of entries", flush=True)
 
 
+@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (5, 2048, 1024), (8, 12288, 2048)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_linear_rows_norm_and_swiglu(cuda, rows, n_out, dim, with_res):
+    """The fused-input projections equal their two-launch forms bit for bit: RMSNorm (tg_rmsnorm,
+    residual add and residual write-back) then tg_linear_rows, and silu_mul then tg_linear_rows;
+    the fp32-output form equals the bf16 one converted."""
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows * 7 + n_out + with_res)
+    h = _bf(torch.randn(rows, dim, generator=g, device=cuda))
+    res = _bf(torch.randn(rows, dim, generator=g, device=cuda)) if with_res else None
+    nw = _bf(1.0 + 0.1 * torch.randn(dim, generator=g, device=cuda))
+    w = _bf(torch.randn(n_out, dim, generator=g, device=cuda) * dim ** -0.5)
+    ro = torch.empty_like(h)
+    got = dec.linear_rows_norm(h, nw, 1e-6, w, residual=res, residual_out=ro)
+    got32 = dec.linear_rows_norm(h, nw, 1e-6, w, residual=res, out_fp32=True)
+    r2 = res.clone() if with_res else None
+    normed = dec.rmsnorm(h, nw, 1e-6, residual=r2, residual_out=r2)
+    ref = dec.linear_rows(normed, w)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref) and torch.equal(got32, ref.float())
+    assert torch.equal(ro, r2 if with_res else h)
+    gu = _bf(torch.randn(rows, 2 * dim, generator=g, device=cuda))
+    wd = _bf(torch.randn(n_out, dim, generator=g, device=cuda) * dim ** -0.5)
+    got = dec.linear_rows_swiglu(gu, wd)
+    ref = dec.linear_rows(dec.silu_mul(gu), wd)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("rows,V", [(1, 151936), (3, 1001), (8, 151936)])
 def test_argmax_rows(cuda, rows, V):
     """tg_argmax_rows against torch.argmax: bf16-valued logits (ties at the top are common), a

@@ -80,6 +80,27 @@ def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom, 
     assert (st._graph is not None) == graph
 
 
+def test_decode_fused_projections_match_unfused(cuda):
+    """The decode step with each RMSNorm folded into the projection after it, the SwiGLU product
+    into the down projection and the final norm into the LM head (one launch each) gives the same
+    tokens and logits, bit for bit, as the step with separate norm / silu_mul launches."""
+    from tokengate_amd import inference as I
+    from tokengate_amd.decode import DecodeState
+    m = _model(cuda, seed=11, ssmax=True)
+    split = [I.split_state_span(p) for p in _prompts([520, 300], [(12, 500), (0, 280)], 4)]
+    steps = 5
+    pfs = [m.prefill(split, [30, 400], decode_headroom=steps + 1) for _ in range(2)]
+    plain = DecodeState(m.weights, m.gate, m.gate_layer, pfs[0], steps + 1, fused=False)
+    fused = DecodeState(m.weights, m.gate, m.gate_layer, pfs[1], steps + 1, fused=True)
+    cp = cf = pfs[0].first_tokens
+    for i in range(steps):
+        cp = plain.step(cp)
+        cf = fused.step(cf)
+        torch.cuda.synchronize()
+        assert torch.equal(cp, cf), f"step {i}: tokens differ"
+        assert torch.equal(plain.last_logits, fused.last_logits), f"step {i}: logits differ"
+
+
 def test_decode_graph_replays_match_eager(cuda):
     """Every replay of the captured decode step equals the eager step bit for bit (tokens and
     logits), with eager work and host synchronisations between the replays; the two decodes

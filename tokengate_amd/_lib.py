@@ -52,6 +52,8 @@ SIGNATURES = {
     "tg_gate_branch_readout": [vp, i64, i64, i32, vp, vp, vp],
     "tg_lm_head": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
     "tg_linear_rows": [vp, i64, i32, vp, i64, i32, vp, i64, vp],
+    "tg_linear_rows_norm": [vp, i64, vp, i64, vp, i64, vp, f32, i32, vp, i64, i32, vp, i64, i32, vp],
+    "tg_linear_rows_swiglu": [vp, i64, i32, i32, vp, i64, vp, i64, vp],
     "tg_argmax_rows": [vp, i64, i32, i64, vp, vp],
 }
 RESTYPES = {"tg_last_error": C.c_char_p, "tg_keybias_fwd_workspace_size": C.c_int64,

@@ -261,16 +261,18 @@ __device__ __forceinline__ u32x4 lin_input(const LinIn &in, int b, int c, const 
     return pack8(y);
   }
 }
-// NCH consecutive 512-column chunks of a wave's 4 output rows: every weight load first, then the
-// bf16 pair dot products against the NR input rows.
-template <int NCH, int NR, int PRE>
-__device__ __forceinline__ void lin_chunks(const LinIn &in, const bf16_t *const (&wr)[4], int cg, int lane,
-                                           const float (&rinv)[NR], float (&acc)[4][NR]) {
-  u32x4 wv[NCH][4];
+// NCH consecutive 512-column chunks of a wave's 4 output rows: every weight load first
+// (lin_load), then the bf16 pair dot products against the NR input rows (lin_dot).
+template <int NCH>
+__device__ __forceinline__ void lin_load(const bf16_t *const (&wr)[4], int cg, u32x4 (&wv)[NCH][4]) {
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch)
 #pragma unroll
     for (int r = 0; r < 4; ++r) wv[ch][r] = ld16(wr[r] + cg + 512 * ch);
+}
+template <int NCH, int NR, int PRE>
+__device__ __forceinline__ void lin_dot(const LinIn &in, const u32x4 (&wv)[NCH][4], int cg, int lane,
+                                        const float (&rinv)[NR], float (&acc)[4][NR]) {
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     const int c = cg + 512 * ch + 8 * lane;
@@ -294,6 +296,14 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   const int lane = threadIdx.x & 63;
   const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
   if (v0 >= vocab) return;
+  // rows past the end read the last row (in bounds; their sums are not stored)
+  const bf16_t *wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
+  // the first 2048 columns of the weight are requested before the input is formed
+  u32x4 wfirst[4][4];
+  const bool first = dim >= 2048;
+  if (first) lin_load<4>(wr, 0, wfirst);
   float rinv[NR];
   if constexpr (PRE == kPreNorm) {
     // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ... element
@@ -324,17 +334,27 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   for (int r = 0; r < 4; ++r)
 #pragma unroll
     for (int b = 0; b < NR; ++b) acc[r][b] = 0.f;
-  // rows past the end read the last row (in bounds; their sums are not stored)
-  const bf16_t *wr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
   int cg = 0;
-  for (; cg + 2048 <= dim; cg += 2048) lin_chunks<4, NR, PRE>(in, wr, cg, lane, rinv, acc);
+  if (first) {
+    lin_dot<4, NR, PRE>(in, wfirst, 0, lane, rinv, acc);
+    cg = 2048;
+  }
+  for (; cg + 2048 <= dim; cg += 2048) {
+    u32x4 wv[4][4];
+    lin_load<4>(wr, cg, wv);
+    lin_dot<4, NR, PRE>(in, wv, cg, lane, rinv, acc);
+  }
   if (dim - cg >= 1024) {
-    lin_chunks<2, NR, PRE>(in, wr, cg, lane, rinv, acc);
+    u32x4 wv[2][4];
+    lin_load<2>(wr, cg, wv);
+    lin_dot<2, NR, PRE>(in, wv, cg, lane, rinv, acc);
     cg += 1024;
   }
-  if (dim - cg >= 512) lin_chunks<1, NR, PRE>(in, wr, cg, lane, rinv, acc);
+  if (dim - cg >= 512) {
+    u32x4 wv[1][4];
+    lin_load<1>(wr, cg, wv);
+    lin_dot<1, NR, PRE>(in, wv, cg, lane, rinv, acc);
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -370,11 +390,27 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float *__restri
   float best = -INFINITY;
   int64_t bi = n;   // no element yet: loses every comparison with a real one
   const int64_t n4 = n / 4;
-  for (int64_t j = threadIdx.x; j < n4; j += 1024) {
+  int64_t j = threadIdx.x;
+  for (; j + 3 * 1024 < n4; j += 4 * 1024) {   // four independent loads in flight per thread
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const f32x4 *>(row + 4 * (j + u * 1024));
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = v[u][e];
+        const int64_t ix = 4 * (j + u * 1024) + e;
+        if (amax_better(x, ix, best, bi)) { best = x; bi = ix; }
+      }
+  }
+  for (; j < n4; j += 1024) {
     const f32x4 v = *reinterpret_cast<const f32x4 *>(row + 4 * j);
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      if (amax_better(v[e], 4 * j + e, best, bi)) { best = v[e]; bi = 4 * j + e; }
+    for (int e = 0; e < 4; ++e) {
+      const float x = v[e];
+      if (amax_better(x, 4 * j + e, best, bi)) { best = x; bi = 4 * j + e; }
+    }
   }
   for (int64_t j = 4 * n4 + threadIdx.x; j < n; j += 1024)
     if (amax_better(row[j], j, best, bi)) { best = row[j]; bi = j; }

@@ -26,8 +26,9 @@ from typing import List, Optional
 
 import torch
 
-from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, argmax_rows, h2d, linear_rows, logits_last,
-                                   qk_norm_rope, rmsnorm, silu_mul, varlen_kv_attention)
+from tokengate_amd.decoder import (CacheGap, DecoderWeights, LayerKV, argmax_rows, h2d, linear_rows, linear_rows_norm,
+                                   linear_rows_swiglu, logits_last, qk_norm_rope, rmsnorm, silu_mul,
+                                   varlen_kv_attention)
 from tokengate_amd.gate import ScoringHead
 from tokengate_amd.prefill import PrefillResult
 
@@ -55,7 +56,7 @@ def _relayout(kv: LayerKV, cu: List[int], gap: int) -> LayerKV:
 
 class DecodeState:
     def __init__(self, wts: DecoderWeights, head: ScoringHead, gate_layer: int, pf: PrefillResult,
-                 max_new_tokens: int, prune_below_gate: bool = False, graph: bool = False):
+                 max_new_tokens: int, prune_below_gate: bool = False, graph: bool = False, fused: bool = True):
         shape = wts.shape
         self.wts, self.shape = wts, shape
         dev = wts.device
@@ -105,6 +106,7 @@ class DecodeState:
         self.step_f = torch.zeros((), dtype=torch.float32, device=dev)   # steps taken, on the device
         self.max_new_tokens = max_new_tokens
         self.use_graph = graph
+        self.fused = fused
         self._graph = None
         self._tok_in = self._tok_out = None
 
@@ -134,7 +136,8 @@ class DecodeState:
         B = self.B
         dev = tokens.device
         x = torch.nn.functional.embedding(tokens, w.embed)
-        res = x.clone()
+        fused = self.fused and B <= 8 and s.d_model % 512 == 0 and s.d_ff % 512 == 0
+        res = None if fused else x.clone()
         normed = torch.empty_like(x)
         hid = torch.empty_like(x)
         qkv = torch.empty(B, s.qkv_dim, dtype=x.dtype, device=dev)
@@ -148,15 +151,26 @@ class DecodeState:
             p = (self.next_pos.to(torch.float32) + 1.0).clamp(min=2.0)
             r_dec = (torch.log(m) / torch.log(p)).clamp(max=1.0)
         scale = 1.0 / math.sqrt(s.head_dim)
+        if fused:
+            # each norm is folded into the projection after it, and the SwiGLU product into the down
+            # projection; the residual stream alternates between two buffers (a fused norm reads one
+            # and writes the other)
+            rbuf = [torch.empty_like(x), torch.empty_like(x)]
+            cur = 0
         for l in range(s.n_layers):
             lw = w.layers[l]
             g = 0 if l <= self.gate_layer else 1
             j = l - self.gate_layer - 1
-            if l == 0:
+            if fused:
+                linear_rows_norm(x if l == 0 else hid, lw.ln1, s.rms_eps, lw.w_qkv, residual=None if l == 0 else rbuf[cur],
+                                 residual_out=rbuf[1 - cur], out=qkv)
+                cur = 1 - cur
+            elif l == 0:
                 rmsnorm(res, lw.ln1, s.rms_eps, out=normed)
             else:
                 rmsnorm(hid, lw.ln1, s.rms_eps, residual=res, residual_out=res, out=normed)
-            linear_rows(normed, lw.w_qkv, out=qkv)
+            if not fused:
+                linear_rows(normed, lw.w_qkv, out=qkv)
             kv = self.kv[l]
             q = qk_norm_rope(qkv, self.next_pos, lw, s, w.inv_freq, kv.k, kv.v,
                              self.qscale[j] if (g and self.qscale is not None) else None,
@@ -164,12 +178,19 @@ class DecodeState:
             varlen_kv_attention(q, kv.k, kv.v, self.cu_q, self.seg_dev[g], self.used[g], 1, self.cap_k[g], scale,
                                 self.bias[j] if g else None, out=att, lse=lse)
             linear_rows(att.view(B, -1), lw.w_o, out=hid)
-            rmsnorm(hid, lw.ln2, s.rms_eps, residual=res, residual_out=res, out=normed)
-            act = silu_mul(linear_rows(normed, lw.w_gu))
-            linear_rows(act, lw.w_down, out=hid)
-        h = hid + res
+            if fused:
+                gu = linear_rows_norm(hid, lw.ln2, s.rms_eps, lw.w_gu, residual=rbuf[cur], residual_out=rbuf[1 - cur])
+                cur = 1 - cur
+                linear_rows_swiglu(gu, lw.w_down, out=hid)
+            else:
+                rmsnorm(hid, lw.ln2, s.rms_eps, residual=res, residual_out=res, out=normed)
+                act = silu_mul(linear_rows(normed, lw.w_gu))
+                linear_rows(act, lw.w_down, out=hid)
         self.next_pos += 1
         self.step_f += 1.0
-        logits = logits_last(w, h, self.rows_b)
+        if fused:   # every row produces a token: the final norm folds into the LM head
+            logits = linear_rows_norm(hid, w.final_norm, s.rms_eps, w.lm_head, residual=rbuf[cur], out_fp32=True)
+        else:
+            logits = logits_last(w, hid + res, self.rows_b)
         self.last_logits = logits
         return argmax_rows(logits)

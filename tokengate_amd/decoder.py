@@ -427,6 +427,45 @@ def linear_rows(x: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tenso
     return out
 
 
+def _rows_ok(*ts) -> bool:
+    return all(t is None or (t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0) for t in ts)
+
+
+def linear_rows_norm(h: torch.Tensor, norm_w: torch.Tensor, eps: float, weight: torch.Tensor,
+                     residual: Optional[torch.Tensor] = None, residual_out: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None, out_fp32: bool = False) -> torch.Tensor:
+    """F.linear(RMSNorm(h + residual), weight) for up to 8 rows in one launch (tg_linear_rows_norm);
+    residual_out <- bf16(h + residual) when given (a buffer other than residual)."""
+    n, d = h.shape
+    N = weight.shape[0]
+    if not (1 <= n <= 8 and d % 512 == 0 and _rows_ok(h, residual, residual_out) and weight.stride(1) == 1
+            and weight.stride(0) == d):
+        raise RuntimeError("linear_rows_norm: 1..8 contiguous 16-byte aligned rows, dim a multiple of 512")
+    if out is None:
+        out = torch.empty(n, N, dtype=torch.float32 if out_fp32 else torch.bfloat16, device=h.device)
+    _lib.call("tg_linear_rows_norm", h.data_ptr(), h.stride(0),
+              residual.data_ptr() if residual is not None else None, residual.stride(0) if residual is not None else 0,
+              residual_out.data_ptr() if residual_out is not None else None,
+              residual_out.stride(0) if residual_out is not None else 0,
+              norm_w.data_ptr(), float(eps), n, weight.data_ptr(), N, d, out.data_ptr(), out.stride(0),
+              int(out_fp32), _stream(h))
+    return out
+
+
+def linear_rows_swiglu(gate_up: torch.Tensor, weight: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """F.linear(silu(g) * u, weight) of gate/up rows [g | u] for up to 8 rows in one launch."""
+    n, two_i = gate_up.shape
+    inter = two_i // 2
+    N = weight.shape[0]
+    if not (1 <= n <= 8 and inter % 512 == 0 and _rows_ok(gate_up) and weight.stride(1) == 1
+            and weight.stride(0) == inter):
+        raise RuntimeError("linear_rows_swiglu: 1..8 contiguous 16-byte aligned rows, inter a multiple of 512")
+    out = torch.empty(n, N, dtype=torch.bfloat16, device=gate_up.device) if out is None else out
+    _lib.call("tg_linear_rows_swiglu", gate_up.data_ptr(), gate_up.stride(0), n, inter, weight.data_ptr(), N,
+              out.data_ptr(), out.stride(0), _stream(gate_up))
+    return out
+
+
 def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     """logits.argmax(-1) (int64) of fp32 rows with torch's rules (NaN wins, ties to the lower
     index) in one launch that clears no memory (tg_argmax_rows)."""
