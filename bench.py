@@ -524,6 +524,8 @@ def main():
                     help="also run three plain 1 GiB device copies (counter calibration for HBM bytes)")
     ap.add_argument("--gate-counters", action="store_true",
                     help="only run eager launches of the gate kernels (for a per-dispatch counter profile)")
+    ap.add_argument("--bwd-only", action="store_true",
+                    help="only run the B4 x 8192 backward (for a per-dispatch counter profile)")
     ap.add_argument("--ttft-only", action="store_true",
                     help="only run 8 back-to-back gated prefills at 32k / K=2000 (for a kernel trace)")
     args = ap.parse_args()
@@ -543,6 +545,9 @@ def main():
         return
     if args.gate_counters:
         gate_counter_run(dev)
+        return
+    if args.bwd_only:
+        print(json.dumps({"bwd_8k_b4": bench_bwd(dev, iters=3)}), flush=True)
         return
 
     S, H, Hkv = 32768, 16, 8

@@ -113,14 +113,20 @@ template <int HP> constexpr int dq_bm() { return kQWaves * (32 / HP); }
 // dQ kernel tile layouts (16x16x32 MFMAs).  LDS row lr of a 64-key tile holds key dq_perm(lr):
 // within each 32-key step, S^T block kb' row m carries key 8(m/4) + 4kb' + m%4, so that lane group
 // G of a step's S^T / dP^T accumulators holds keys 8G .. 8G+7 — the k range of the B operand
-// (dS^T) of dQ^T += K^T dS^T.  K's chunk swizzle dq_kswz is a bijection of the row's low four bits
-// (conflict-free row reads: 16 rows, one chunk each) that also puts the 8 rows of half a wave's
-// transposing read (rows 4G + r/4) on 8 different 32-byte bank groups.
+// (dS^T) of dQ^T += K^T dS^T.  K's chunk swizzle dq_kswz (physical chunk = logical chunk ^
+// dq_kswz(row), a function of the row's low four bits) makes both reads conflict free whether the
+// LDS serves a 16-byte read to 8 lanes per cycle over 32 banks or to 16 lanes over 64 banks (the
+// rocprofv3 bank-conflict counter of the earlier swizzle, 2 (row & 7) + bit 3, matched the first
+// model): each 8 consecutive rows of a row read get 8 distinct chunks mod 8 (and 16 rows 16
+// distinct chunks), and the 4 (or 8) rows of a transposing read get distinct 32-byte blocks mod 4
+// (mod 8).
 __device__ __forceinline__ int dq_perm(int lr) {
   const int m = lr & 15;
   return 32 * (lr >> 5) + 8 * (m >> 2) + 4 * ((lr >> 4) & 1) + (m & 3);
 }
-__device__ __forceinline__ uint32_t dq_kswz(int row) { return (uint32_t)(2 * (row & 7) + ((row >> 3) & 1)); }
+__device__ __forceinline__ uint32_t dq_kswz(int row) {
+  return (uint32_t)(((row >> 2) & 1) | ((row & 3) << 1) | ((((row >> 2) ^ (row >> 3)) & 1) << 3));
+}
 
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
@@ -351,12 +357,13 @@ constexpr int kQTileBytes = kQT * kRow; // 8 KiB
 // S / dP 2 x 8, so that eight waves (two per SIMD) fit where the 32-key form holds one per SIMD.
 // Tile rows are read through the row map pi_rb(m) = 8(m/4) + 4rb + m%4, so that the S^T / dP^T
 // accumulators of lane group g hold queries 8g .. 8g+7 — the B operand layout of dV^T += dO^T P
-// and dK^T += Q^T dS — and the Q / dO tiles use the swizzle k16_swz, conflict-free for both the
-// row reads (16 rows x one 16-byte chunk per 16 lanes) and the transposing reads (8 rows x 32 B
-// per 32 lanes).
+// and dK^T += Q^T dS — and the Q / dO tiles use the swizzle k16_swz (physical chunk = logical
+// chunk ^ k16_swz(row)), conflict free for the row reads (rows 8(m/4) + 4rb + m%4: each 8-lane
+// group gets 8 distinct chunks mod 8, each 16-lane group 16 distinct chunks) and the transposing
+// reads (rows 8g + 0..3 / 4..7: distinct 32-byte blocks mod 4 per 16 lanes, mod 8 per 32 lanes),
+// under either LDS model (8 lanes x 16 B over 32 banks per cycle, or 16 lanes over 64 banks).
 __device__ __forceinline__ uint32_t k16_swz(int row) {
-  const int a = row >> 3, b = row & 3;
-  return (uint32_t)(8 * (a & 1) + 2 * b + (a >> 1));
+  return (uint32_t)(((row >> 3) & 1) | ((row & 3) << 1) | ((((row >> 3) ^ (row >> 4)) & 1) << 3));
 }
 constexpr int kK16Waves = 8;
 constexpr int kK16Threads = 64 * kK16Waves;
