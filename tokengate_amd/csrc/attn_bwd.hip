@@ -130,7 +130,7 @@ __device__ __forceinline__ uint32_t dq_kswz(int row) {
 
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
-  constexpr int QW = 32 / HP;
+  constexpr int QW = 32;   // query positions per wave (all of one head)
   constexpr int BM = dq_bm<HP>();
   // K: rows in dq_perm order, chunk ^ dq_kswz(row) (read row-major and transposed);
   // V: rows in dq_perm order, chunk ^ (row % 16) (read row-major only)
@@ -165,15 +165,17 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   const brsrc_t brs =
       make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
 
-  // this wave's 32 columns: block cb (0, 1) = head cb (HP = 2) or query half cb (HP = 1), lane l
-  // holding column l % 16 of each block
-  const int qw0 = q0 + wave * QW;
+  // this wave's 32 columns: 32 query positions of one head (HP = 2: waves 0-3 the first head of the
+  // pair, 4-7 the second), block cb (0, 1) = positions 16 cb .. 16 cb + 15, lane l holding column
+  // l % 16 of each block; one head per wave means one bias row per wave
+  const int hw = HP == 2 ? wave / (kQWaves / 2) : 0;
+  const int qw0 = q0 + QW * (HP == 2 ? wave % (kQWaves / 2) : wave);
   int qrow[2], hh[2];
   bool qvalid[2];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    qrow[cb] = qw0 + (HP == 2 ? c16 : 16 * cb + c16);
-    hh[cb] = h0 + (HP == 2 ? cb : 0);
+    qrow[cb] = qw0 + 16 * cb + c16;
+    hh[cb] = h0 + hw;
     qvalid[cb] = qrow[cb] < sq;
   }
   const bool wave_has_rows = qw0 < sq;
@@ -256,16 +258,13 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     // blocks x 4 d-steps each
     f32x4 sacc[2][4], pacc[2][4];
 #pragma unroll
-    for (int cb = 0; cb < 2; ++cb) {
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        if constexpr (HAS_BIAS)
-          sacc[cb][kb] = *reinterpret_cast<const f32x4 *>(
-              &bs[buf][HP == 2 ? cb : 0][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
-        else
-          sacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        pacc[cb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+    for (int kb = 0; kb < 4; ++kb) {
+      if constexpr (HAS_BIAS)   // both column blocks are the wave's head: one read serves both
+        sacc[0][kb] = *reinterpret_cast<const f32x4 *>(&bs[buf][hw][32 * (kb >> 1) + 8 * G + 4 * (kb & 1)]);
+      else
+        sacc[0][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sacc[1][kb] = sacc[0][kb];
+      pacc[0][kb] = pacc[1][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
     for (int ks4 = 0; ks4 < 4; ++ks4) {
