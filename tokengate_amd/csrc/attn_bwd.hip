@@ -347,10 +347,12 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
 // ---- 3. dK / dV / dBias kernel -----------------------------------------------------------
 constexpr int kKBlock = 128;            // keys per workgroup
 constexpr int kQT = 32;                 // queries per tile
+constexpr int kQSub = 2;                // query tiles per LDS ring slot (per workgroup barrier)
 constexpr int kQTileBytes = kQT * kRow; // 8 KiB
 
 // Eight waves; each owns 16 keys of one KV head and loops over every query head of its GQA group
-// and every 32-query tile, on v_mfma_f32_16x16x32_bf16
+// and every 32-query tile (two tiles per LDS ring slot, so one workgroup barrier per 64 queries),
+// on v_mfma_f32_16x16x32_bf16
 // (lane l: A row l%16 with k = 8(l/16)+j, B column l%16 with the same k, C rows 4(l/16)+i at
 // column l%16).  Per wave: K^T / V^T fragments 2 x 16 VGPRs, dK^T / dV^T accumulators 2 x 32,
 // S / dP 2 x 8, so that eight waves (two per SIMD) fit where the 32-key form holds one per SIMD.
@@ -370,10 +372,11 @@ static_assert(16 * kK16Waves == kKBlock, "eight waves of 16 keys");
 
 template <bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(1024))) char qs0[kQTileBytes], qs1[kQTileBytes];
-  __shared__ __attribute__((aligned(1024))) char dos0[kQTileBytes], dos1[kQTileBytes];
-  __shared__ __attribute__((aligned(128))) float ls0[kQT], ls1[kQT];
-  __shared__ __attribute__((aligned(128))) float dsh0[kQT], dsh1[kQT];
+  // each ring slot holds kQSub query tiles of kQT rows: one barrier per kQSub tiles
+  __shared__ __attribute__((aligned(1024))) char qs0[kQSub * kQTileBytes], qs1[kQSub * kQTileBytes];
+  __shared__ __attribute__((aligned(1024))) char dos0[kQSub * kQTileBytes], dos1[kQSub * kQTileBytes];
+  __shared__ __attribute__((aligned(256))) float ls0[kQSub * kQT], ls1[kQSub * kQT];
+  __shared__ __attribute__((aligned(256))) float dsh0[kQSub * kQT], dsh1[kQSub * kQT];
   auto qslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return qs0; else return qs1; };
   auto doslot = [&](auto b) -> char * { if constexpr (decltype(b)::value == 0) return dos0; else return dos1; };
   auto lslot = [&](auto b) -> float * { if constexpr (decltype(b)::value == 0) return ls0; else return ls1; };
@@ -406,7 +409,8 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
 
   int m_start = 0;
   if constexpr (CAUSAL) m_start = max(0, n0 - off) / kQT * kQT;
-  const int n_qt = sq > m_start ? (sq - m_start + kQT - 1) / kQT : 0;
+  constexpr int kQSlot = kQSub * kQT;   // query rows per ring slot
+  const int n_qt = sq > m_start ? (sq - m_start + kQSlot - 1) / kQSlot : 0;
 
   // LDS DMA: wave w fills rows 4w .. 4w+3 of the Q and dO tiles (one 1 KB load each)
   const int drow = 4 * wave + (lane >> 4);
@@ -444,19 +448,34 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
     float dbacc = 0.f;
 
     auto issue_tile = [&](int m0, auto buf_c) {
-      dma16(qrs, qslot(buf_c) + wave * 1024, (uint32_t)((int64_t)m0 * a.q_rs * 2) + qoff);
-      dma16(dors, doslot(buf_c) + wave * 1024, (uint32_t)((int64_t)m0 * a.do_rs * 2) + dooff);
-      if (wave == 0 && lane < kQT) dma4(lrs, lslot(buf_c), (uint32_t)(m0 + lane) * 4);
-      if (wave == 1 && lane < kQT) dma4(drs, dslot(buf_c), (uint32_t)(m0 + lane) * 4);
+#pragma unroll
+      for (int sub = 0; sub < kQSub; ++sub) {
+        dma16(qrs, qslot(buf_c) + sub * kQTileBytes + wave * 1024,
+              (uint32_t)((int64_t)(m0 + sub * kQT) * a.q_rs * 2) + qoff);
+        dma16(dors, doslot(buf_c) + sub * kQTileBytes + wave * 1024,
+              (uint32_t)((int64_t)(m0 + sub * kQT) * a.do_rs * 2) + dooff);
+      }
+      // lse / D of the slot: 64 rows per 4-byte DMA, waves 0 .. kLD-1 and kLD .. 2 kLD-1
+      constexpr int kLD = kQSub * kQT / 64;
+      static_assert(kLD * 64 == kQSub * kQT && 2 * kLD <= kK16Waves, "lse / D rows in 64-row DMAs");
+      if (wave < kLD) dma4(lrs, lslot(buf_c) + 64 * wave, (uint32_t)(m0 + 64 * wave + lane) * 4);
+      else if (wave < 2 * kLD) dma4(drs, dslot(buf_c) + 64 * (wave - kLD), (uint32_t)(m0 + 64 * (wave - kLD) + lane) * 4);
     };
 
     auto tile_step = [&](int t, auto buf_c) {
       constexpr int BUF = decltype(buf_c)::value;
-      const int m0 = m_start + t * kQT;
+      const int m00 = m_start + t * kQSlot;
       wait_vm<0>();
       ring_barrier();
-      if (t + 1 < n_qt) issue_tile(m0 + kQT, std::integral_constant<int, 1 - BUF>());
-      if (!wave_has_keys || (CAUSAL && m0 + kQT - 1 + off < kw0)) return;
+      if (t + 1 < n_qt) issue_tile(m00 + kQSlot, std::integral_constant<int, 1 - BUF>());
+#pragma unroll
+      for (int sub = 0; sub < kQSub; ++sub) {
+      const int m0 = m00 + sub * kQT;
+      if (!wave_has_keys || m0 >= sq || (CAUSAL && m0 + kQT - 1 + off < kw0)) continue;
+      char *const qsl = qslot(buf_c) + sub * kQTileBytes;
+      char *const dosl = doslot(buf_c) + sub * kQTileBytes;
+      const float *const lsl = lslot(buf_c) + sub * kQT;
+      const float *const dsl = dslot(buf_c) + sub * kQT;
 
       // S = Q K^T and dP = dO V^T for queries m0 + pi_rb(row), this lane's key
       f32x4 sacc[2], pacc[2];
@@ -472,8 +491,8 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) {
             const uint32_t o16 = ra[rb] * kRow + (((uint32_t)(4 * (k2 + e) + g) ^ k16_swz((int)ra[rb])) << 4);
-            qa[e][rb] = lds_load16(qslot(buf_c), o16);
-            da[e][rb] = lds_load16(doslot(buf_c), o16);
+            qa[e][rb] = lds_load16(qsl, o16);
+            da[e][rb] = lds_load16(dosl, o16);
           }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -489,8 +508,8 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       uint32_t pk[4], dk4[4];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lslot(buf_c) + 8 * g + 4 * rb);
-        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dslot(buf_c) + 8 * g + 4 * rb);
+        const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lsl + 8 * g + 4 * rb);
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dsl + 8 * g + 4 * rb);
         float p[4], ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -525,11 +544,11 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
           const uint32_t hb = (uint32_t)((tm & 1) * 8);
           const uint32_t o0 = trow0 * kRow + (((uint32_t)c ^ k16_swz(trow0)) << 4) + hb;
           const uint32_t o1 = trow1 * kRow + (((uint32_t)c ^ k16_swz(trow1)) << 4) + hb;
-          dot_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(doslot(buf_c) + o0),
-                                                                       lds_read_tr16(doslot(buf_c) + o1),
+          dot_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(dosl + o0),
+                                                                       lds_read_tr16(dosl + o1),
                                                                        0, 1, 2, 3, 4, 5, 6, 7));
-          qt_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qslot(buf_c) + o0),
-                                                                      lds_read_tr16(qslot(buf_c) + o1),
+          qt_[e] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lds_read_tr16(qsl + o0),
+                                                                      lds_read_tr16(qsl + o1),
                                                                       0, 1, 2, 3, 4, 5, 6, 7));
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -539,6 +558,7 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
           dkacc[d4 + e] = mfma16(qt_[e], dop, dkacc[d4 + e]);
         }
       }
+      }   // sub-tiles
     };
     ring_barrier();   // previous head's last tile fully consumed before its slots are reused
     if (n_qt > 0) issue_tile(m_start, std::integral_constant<int, 0>());
