@@ -347,6 +347,34 @@ def prefill_trace_run(dev, runs=8):
         print(f"prefill {i + 1}/{runs} done", flush=True)
 
 
+def decode_trace_run(dev, steps=30):
+    """Greedy decode after the 32k / K=2000 gated prefill of prefill_trace_run (graph replay of the
+    whole step after the first), for a per-kernel trace of the decode step; prints ms per token."""
+    import statistics
+    import torch
+    from tokengate_amd import decoder as dec
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    from tokengate_amd.decode import DecodeState
+    shape = dec.QWEN3_1P7B
+    wts = dec.random_decoder(shape, seed=0, device=dev)
+    head = G.random_head(shape.n_layers - 2, shape.n_heads, seed=5, device=dev)
+    g = torch.Generator().manual_seed(7)
+    ids = [torch.randint(0, shape.vocab, (32768,), generator=g).to(dev)]
+    r = P.prefill_batch(wts, head, ids, [64], [32768 - 256], 1, [2000], decode_headroom=steps + 4)
+    st = DecodeState(wts, head, 1, r, steps + 3, graph=True)
+    cur = r.first_tokens
+    ts = []
+    for i in range(steps + 2):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        cur = st.step(cur)
+        torch.cuda.synchronize()
+        if i >= 2:
+            ts.append((time.perf_counter() - t0) * 1e3)
+    print(json.dumps({"decode_ms_per_token": round(statistics.median(ts), 3), "steps": steps}), flush=True)
+
+
 def cpu_model() -> str:
     """The host CPU's model name (from /proc/cpuinfo), or 'unknown'."""
     try:
@@ -526,6 +554,8 @@ def main():
                     help="only run eager launches of the gate kernels (for a per-dispatch counter profile)")
     ap.add_argument("--bwd-only", action="store_true",
                     help="only run the B4 x 8192 backward (for a per-dispatch counter profile)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only run greedy decode steps after one 32k / K=2000 prefill (for a kernel trace)")
     ap.add_argument("--ttft-only", action="store_true",
                     help="only run 8 back-to-back gated prefills at 32k / K=2000 (for a kernel trace)")
     args = ap.parse_args()
@@ -545,6 +575,9 @@ def main():
         return
     if args.gate_counters:
         gate_counter_run(dev)
+        return
+    if args.decode_only:
+        decode_trace_run(dev)
         return
     if args.bwd_only:
         print(json.dumps({"bwd_8k_b4": bench_bwd(dev, iters=3)}), flush=True)
