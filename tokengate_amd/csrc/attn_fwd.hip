@@ -632,19 +632,6 @@ void dispatch_fwd(const FwdArgs &a, int nw, int hp, bool causal, bool has_bias, 
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Compute units of the current device (cached per device id).
-int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev] = n;
-  }
-  return cache[dev];
-}
-
 // Waves per workgroup and query tiles for a launch over `rows` query positions x `units` (sequence,
 // head group) pairs: 8-wave workgroups when that still gives at least two per CU, else 4-wave ones.
 void pick_tiling(int hp, int rows, int64_t units, int &nw, int &n_qtiles) {

@@ -13,7 +13,7 @@
 //
 // Kernels:
 //   gate_score_kernel  — s = w2 . silu(W1 x + b1) + b2 for every row of a packed (rows, 2048)
-//                        bf16 matrix (128 rows per workgroup; W1 x on bf16 MFMA, fp32 epilogue);
+//                        bf16 matrix (256 rows per workgroup; W1 x on bf16 MFMA, fp32 epilogue);
 //   gate_topk_*kernel  — one workgroup per sequence: order-preserving uint32 keys, 4-pass 8-bit
 //                        radix select of the K_c-th largest key (keys held in registers for
 //                        articles up to 65536 tokens, else re-read from global memory), then an
@@ -23,7 +23,9 @@
 //   gate_pack_kernel   — one launch gathers every kept row for any number of row streams (hidden
 //                        states, per-layer K and V, head-chunked rows) in 16-byte units, plus the
 //                        kept positions and the kept rows' gate bias.
+#include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "tg_common.h"
 #include "../../include/tokengate_hip.h"
@@ -33,27 +35,34 @@ namespace {
 
 // ---------------------------------------------------------------------------------------------
 // Scoring head: s = w2 . silu(W1 x + b1) + b2, x in R^2048 (bf16), W1 (256 x 2048) bf16.
-// Workgroup: 8 waves, 128 rows; wave w owns rows 64(w%2)..+63 and hidden units 64(w/2)..+63
-// (2 x 2 blocks of 32 x 32): the shape that reads the fewest LDS bytes per MFMA (8 KiB of X and W
-// fragments per wave per k step).  K loop over the 2048 inputs in steps of 32 through a 6-deep
-// LDS ring filled by DMA (X tile 128 x 32 = 8 KiB, W1 tile 256 x 32 = 16 KiB per stage; 144 KiB),
-// unrolled so that every ring slot index is a compile-time constant, and software-pipelined: a
+// Workgroup: 8 waves, 256 rows; wave w owns rows 128(w%2)..+127 and hidden units 64(w/2)..+63
+// (4 x 2 blocks of 32 x 32; 12 KiB of X and W fragments per wave per k step for 16 MFMAs).  Every
+// workgroup streams all of W1 (1 MiB, L2-resident) through LDS once, so the rows per workgroup set
+// how many W1 bytes each X byte costs: 256 rows make it 2 MiB of X per 1 MiB of W1.  K loop over
+// the 2048 inputs in steps of 32 through a 5-deep LDS ring filled by DMA (X tile 256 x 32 and W1
+// tile 256 x 32, 16 KiB each per stage: the whole 160 KiB of LDS, the epilogue's row sums reusing
+// the first slot; three steps of X stay in flight), unrolled so that every ring slot index is a
+// compile-time constant, and software-pipelined: a
 // wave reads step k+1's fragments from LDS while its MFMAs of step k run, so the LDS reads and the
 // matrix cores overlap instead of alternating between the per-step barriers.  Accumulators are
 // C^T blocks (hidden unit = MFMA row, token = column): each lane ends with one token's hidden
 // units of each block, the SiLU . w2 reduction is in-lane plus one cross-half exchange, and the four
 // hidden quarters of a row are added through LDS in a fixed order.
-// Measured limiter: every 128-row tile re-streams all of W1 (1 MiB, L2-resident) through the LDS
-// DMA path next to its 512 KiB of X, and that path moves about 11-12 TB/s over the whole chip: with
-// the matrix work alone a launch takes 0.33x, with X alone 0.49x, with W1 alone 0.54x of the full
-// kernel's time at 710k rows.
+// With 128-row workgroups the W1 stream through the LDS DMA path (about 11-12 TB/s over the whole
+// chip) bounded the kernel: with the matrix work alone a launch took 0.33x, with X alone 0.49x,
+// with W1 alone 0.54x of the full kernel's time at 710k rows.
 // ---------------------------------------------------------------------------------------------
+// f(integral_constant<int, J>) for J = 0, 1, ... in order
+template <typename F, int... J>
+__device__ __forceinline__ void for_each_c(F &&f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>()), ...);
+}
+
 constexpr int kDin = 2048;
 constexpr int kDh = 256;
-constexpr int kSRows = 128;
+constexpr int kSRowsMax = 256;
 constexpr int kSK = 32;
 constexpr int kSThreads = 512;
-constexpr int kSStages = 6;
 
 struct ScoreArgs {
   const bf16_t *x;
@@ -65,15 +74,23 @@ struct ScoreArgs {
   float *out;
 };
 
+// ROWS rows per workgroup (128 or 256: wave w owns rows (ROWS/2)(w%2) .. +ROWS/2-1, in ROWS/64
+// blocks of 32, and hidden units 64(w/2) .. +63), S-deep LDS ring.
+template <int ROWS, int S>
 __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
-  // X tile: 128 rows x 64 B, W tile: 256 rows x 64 B; 16-byte chunks, 4 per row, XOR-swizzled.
+  constexpr int RB = ROWS / 64;            // 32-row blocks per wave
+  constexpr int XI = ROWS / 128;           // 1 KiB X DMA issues per wave per step
+  constexpr int kXBytes = ROWS * kSK * 2, kWBytes = kDh * kSK * 2;
+  static_assert(S >= 4 && S <= 6 && S * (kXBytes + kWBytes) <= 160 * 1024, "ring fits the LDS");
+  // X tile: ROWS rows x 64 B, W tile: 256 rows x 64 B; 16-byte chunks, 4 per row, XOR-swizzled.
   // One __shared__ object per ring slot: the compiler separates LDS-DMA writes from LDS reads
   // only across distinct objects, so a slot's DMA does not hold up the reads of the others.
-  __shared__ __attribute__((aligned(1024))) char xs0[kSRows * kSK * 2], xs1[kSRows * kSK * 2],
-      xs2[kSRows * kSK * 2], xs3[kSRows * kSK * 2], xs4[kSRows * kSK * 2], xs5[kSRows * kSK * 2];
-  __shared__ __attribute__((aligned(1024))) char ws0[kDh * kSK * 2], ws1[kDh * kSK * 2], ws2[kDh * kSK * 2],
-      ws3[kDh * kSK * 2], ws4[kDh * kSK * 2], ws5[kDh * kSK * 2];
-  static_assert(kSStages == 6, "one named LDS object per ring slot");
+  constexpr int kX5 = S > 4 ? kXBytes : 16, kW5 = S > 4 ? kWBytes : 16;   // unused slots: minimal
+  constexpr int kX6 = S > 5 ? kXBytes : 16, kW6 = S > 5 ? kWBytes : 16;
+  __shared__ __attribute__((aligned(1024))) char xs0[kXBytes], xs1[kXBytes], xs2[kXBytes], xs3[kXBytes],
+      xs4[kX5], xs5[kX6];
+  __shared__ __attribute__((aligned(1024))) char ws0[kWBytes], ws1[kWBytes], ws2[kWBytes], ws3[kWBytes],
+      ws4[kW5], ws5[kW6];
   auto xsl = [&](auto b) -> char * {
     constexpr int B = decltype(b)::value;
     if constexpr (B == 0) return xs0; else if constexpr (B == 1) return xs1; else if constexpr (B == 2) return xs2;
@@ -86,43 +103,43 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
   };
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63, lq = lane & 31, g = lane >> 5;
   const int rg = wave & 1, hq = wave >> 1;   // row half, hidden quarter
-  const int64_t r0 = (int64_t)blockIdx.x * kSRows;
+  const int64_t r0 = (int64_t)blockIdx.x * ROWS;
 
-  const int64_t rows_here = min((int64_t)kSRows, a.n_rows - r0);
+  const int64_t rows_here = min((int64_t)ROWS, a.n_rows - r0);
   const brsrc_t xrs = make_rsrc(a.x + r0 * a.x_rs, (uint32_t)(((rows_here - 1) * a.x_rs + kDin) * 2));
   const brsrc_t wrs = make_rsrc(a.w1, (uint32_t)(kDh * kDin * 2));
-  // DMA slots: X tile = 512 chunks (one 1 KiB issue per wave), W tile = 1024 chunks (two);
+  // DMA slots: X tile = 4 ROWS chunks (XI 1 KiB issues per wave), W tile = 1024 chunks (two);
   // LDS row r (64 B), physical chunk p holds logical chunk p ^ ((r>>2)&3): the 16 rows that 16
   // lanes read with one chunk index then land on 16 distinct 16-byte bank groups of the 64-bank
   // LDS (rows r and r+1..3 share a 256-byte bank line at different quarters; rows 4 apart get
   // different chunks).  Per-lane source offsets (bytes) within a k step; the step's byte offset is
   // added per issue.
-  uint32_t xoff, woff[2];
-  {
-    const int slot = wave * 64 + lane;                   // 0..511
+  uint32_t xoff[XI], woff[2];
+#pragma unroll
+  for (int it = 0; it < XI; ++it) {
+    const int slot = (wave * XI + it) * 64 + lane;
     const int r = slot >> 2, p = slot & 3;
-    const int c = p ^ ((r >> 2) & 3);
-    xoff = (uint32_t)((r * a.x_rs + 8 * c) * 2);
+    xoff[it] = (uint32_t)((r * a.x_rs + 8 * (p ^ ((r >> 2) & 3))) * 2);
   }
 #pragma unroll
   for (int it = 0; it < 2; ++it) {
     const int slot = (wave * 2 + it) * 64 + lane;        // 0..1023
     const int r = slot >> 2, p = slot & 3;
-    const int c = p ^ ((r >> 2) & 3);
-    woff[it] = (uint32_t)((r * kDin + 8 * c) * 2);
+    woff[it] = (uint32_t)((r * kDin + 8 * (p ^ ((r >> 2) & 3))) * 2);
   }
   auto issue = [&](int kstep, auto buf_c) {
     const uint32_t k0b = (uint32_t)(kstep * kSK * 2);
     char *xd = xsl(buf_c), *wd = wsl(buf_c);
-    dma16(xrs, xd + wave * 1024, xoff + k0b);
+#pragma unroll
+    for (int it = 0; it < XI; ++it) dma16(xrs, xd + (wave * XI + it) * 1024, xoff[it] + k0b);
 #pragma unroll
     for (int it = 0; it < 2; ++it) dma16(wrs, wd + (wave * 2 + it) * 1024, woff[it] + k0b);
   };
 
-  // fragments of one k step: [substep s][block]: X^T columns (B operand, token 64rg + 32t + lq) and
-  // W1 rows (A operand, hidden unit 64hq + 32j + lq), k = 16s + 8g .. +7
+  // fragments of one k step: [substep s][block]: X^T columns (B operand, token (ROWS/2)rg + 32t +
+  // lq) and W1 rows (A operand, hidden unit 64hq + 32j + lq), k = 16s + 8g .. +7
   struct Frags {
-    bf16x8 x[2][2], w[2][2];
+    bf16x8 x[2][RB], w[2][2];
   };
   auto read = [&](auto buf_c, Frags &f) {
     const char *xb_lds = xsl(buf_c), *wb_lds = wsl(buf_c);
@@ -130,20 +147,23 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
     for (int s2 = 0; s2 < 2; ++s2) {
       const uint32_t c = (uint32_t)(2 * s2 + g);
 #pragma unroll
-      for (int b = 0; b < 2; ++b) {
-        const int xr = 64 * rg + 32 * b + lq;
-        const int wr = 64 * hq + 32 * b + lq;
+      for (int b = 0; b < RB; ++b) {
+        const int xr = (ROWS / 2) * rg + 32 * b + lq;
         f.x[s2][b] = lds_load16(xb_lds, xr * 64 + ((c ^ ((xr >> 2) & 3)) << 4));
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int wr = 64 * hq + 32 * b + lq;
         f.w[s2][b] = lds_load16(wb_lds, wr * 64 + ((c ^ ((wr >> 2) & 3)) << 4));
       }
     }
   };
 
-  f32x16 acc[2][2];
+  f32x16 acc[2][RB];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < RB; ++t)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[j][t][v] = 0.f;
   auto mma = [&](const Frags &f) {
@@ -152,65 +172,55 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc[j][t] = mfma32(f.w[s2][j], f.x[s2][t], acc[j][t]);
+        for (int t = 0; t < RB; ++t) acc[j][t] = mfma32(f.w[s2][j], f.x[s2][t], acc[j][t]);
   };
 
   constexpr int nk = kDin / kSK;
-  constexpr int kOps = 3;   // DMA ops per thread per step (1 X + 2 W)
-  static_assert(nk % kSStages == 4, "the k loop is unrolled by the ring depth, with a four-step tail");
+  constexpr int kOps = XI + 2;   // DMA ops per thread per step
+  constexpr int L = S % 2 == 0 ? S : 2 * S;   // unroll: ring slots and the two fragment sets cycle
+  static_assert((nk - 4) % L == 0, "the k loop is unrolled L steps at a time, with a four-step tail");
   // Iteration ks (compile-time ring slots): cur holds step ks's fragments (read in the previous
-  // iteration).  Wait until step ks+1's DMA of this wave is done (WAITN = DMA ops of later steps
-  // this wave may leave in flight), barrier (step ks+1 resident for every wave; the slot of step
-  // ks-1 is free), refill that slot with step ks+S-1, read step ks+1's fragments into nxt, then run
-  // step ks's MFMAs while those reads are in flight.
+  // iteration).  Wait until step ks+1's DMA of this wave is done (the DMA ops of steps issued after
+  // it may stay in flight), barrier (step ks+1 resident for every wave; the slot of step ks-1 is
+  // free), refill that slot with step ks+S-1, read step ks+1's fragments into nxt, then run step
+  // ks's MFMAs while those reads are in flight.  Steps ks+2 .. ks+S-2 are in flight at the wait.
   auto iter = [&](int ks, Frags &cur, Frags &nxt, auto next_c, auto waitn_c) {
     constexpr int NX = decltype(next_c)::value;                   // slot of step ks+1
-    constexpr int FREE = (NX + kSStages - 2) % kSStages;          // slot of step ks-1
+    constexpr int FREE = (NX + S - 2) % S;                        // slot of step ks-1
     if (ks + 1 < nk) wait_vm<decltype(waitn_c)::value>();
     ring_barrier();
-    if (ks + kSStages - 1 < nk) issue(ks + kSStages - 1, std::integral_constant<int, FREE>());
+    if (ks + S - 1 < nk) issue(ks + S - 1, std::integral_constant<int, FREE>());
     if (ks + 1 < nk) read(std::integral_constant<int, NX>(), nxt);
     mma(cur);
   };
-  using I0 = std::integral_constant<int, 0>;
-  using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
-  using I4 = std::integral_constant<int, 4>;
-  using I5 = std::integral_constant<int, 5>;
-  using W3 = std::integral_constant<int, 3 * kOps>;
-  using W2 = std::integral_constant<int, 2 * kOps>;
-  using W1 = std::integral_constant<int, kOps>;
-  using W0 = std::integral_constant<int, 0>;
+  // step j of an unrolled group (j known at compile time; the group starts at a multiple of L)
+  auto step = [&](int ks, auto j_c, Frags &fa, Frags &fb, auto waitn_c) {
+    constexpr int J = decltype(j_c)::value;
+    if constexpr (J % 2 == 0) iter(ks, fa, fb, std::integral_constant<int, (J + 1) % S>(), waitn_c);
+    else iter(ks, fb, fa, std::integral_constant<int, (J + 1) % S>(), waitn_c);
+  };
   Frags fa, fb;
-  issue(0, I0());
-  issue(1, I1());
-  issue(2, I2());
-  issue(3, I3());
-  issue(4, I4());
-  wait_vm<4 * kOps>();   // step 0 resident for this wave
+  for_each_c([&](auto k_c) { issue(decltype(k_c)::value, k_c); }, std::make_integer_sequence<int, S - 1>());
+  wait_vm<(S - 2) * kOps>();   // step 0 resident for this wave
   ring_barrier();
-  read(I0(), fa);
+  read(std::integral_constant<int, 0>(), fa);
+  using Wsteady = std::integral_constant<int, (S - 3) * kOps>;
   int ks = 0;
-  // steady state: at iteration ks, steps ks+2 .. ks+4 may stay in flight while waiting for ks+1
-  for (; ks + kSStages <= nk - 4; ks += kSStages) {
-    iter(ks, fa, fb, I1(), W3());
-    iter(ks + 1, fb, fa, I2(), W3());
-    iter(ks + 2, fa, fb, I3(), W3());
-    iter(ks + 3, fb, fa, I4(), W3());
-    iter(ks + 4, fa, fb, I5(), W3());
-    iter(ks + 5, fb, fa, I0(), W3());
-  }
-  // the last four steps (60..63, slots 0..3); nothing more is issued after step 63's DMA
-  iter(ks, fa, fb, I1(), W2());
-  iter(ks + 1, fb, fa, I2(), W1());
-  iter(ks + 2, fa, fb, I3(), W0());
-  iter(ks + 3, fb, fa, I0(), W0());
+  for (; ks + L <= nk - 4; ks += L)
+    for_each_c([&](auto j_c) { step(ks + decltype(j_c)::value, j_c, fa, fb, Wsteady()); },
+               std::make_integer_sequence<int, L>());
+  // the last four steps (nk-4 .. nk-1, steps 0..3 of a group): at step ks the steps after ks+1
+  // up to min(ks+S-2, nk-1) are in flight, none after the last DMA
+  for_each_c([&](auto j_c) {
+    constexpr int J = decltype(j_c)::value;
+    constexpr int kInFlight = std::max(0, std::min(nk - 4 + J + S - 2, nk - 1) - (nk - 4 + J + 1));
+    step(ks + J, j_c, fa, fb, std::integral_constant<int, kInFlight * kOps>());
+  }, std::make_integer_sequence<int, 4>());
 
-  // epilogue: lane holds token 64rg + 32t + lq and hidden units 64hq + 32j + 8(v/4) + 4g + v%4
-  __shared__ float red[4][kSRows];   // per hidden quarter, per row
+  // epilogue: lane holds token (ROWS/2)rg + 32t + lq and hidden units 64hq + 32j + 8(v/4) + 4g + v%4
+  __shared__ float red[4][ROWS];   // per hidden quarter, per row
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < RB; ++t) {
     float part = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -222,10 +232,10 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
         part = fmaf(sl, a.w2[u], part);
       }
     const float tot = pair_sum(part);
-    if (g == 0) red[hq][64 * rg + 32 * t + lq] = tot;
+    if (g == 0) red[hq][(ROWS / 2) * rg + 32 * t + lq] = tot;
   }
   __syncthreads();
-  if (tid < kSRows) {
+  if (tid < ROWS) {
     const int64_t row = r0 + tid;
     if (row < a.n_rows) a.out[row] = (((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid]) + a.b2;
   }
@@ -877,13 +887,21 @@ extern "C" int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_st
            "x and w1 must be 16-byte aligned with a row stride that is a multiple of 8");
   TG_CHECK(n_rows >= 0, "negative size");
   if (n_rows == 0) return 0;
-  TG_CHECK((int64_t)(kSRows + 1) * x_row_stride * 2 < (1ll << 32) - 1024,
-           "a 128-row block of x must span less than 4 GiB");
+  TG_CHECK((int64_t)(kSRowsMax + 1) * x_row_stride * 2 < (1ll << 32) - 1024,
+           "a 256-row block of x must span less than 4 GiB");
   ScoreArgs a{static_cast<const bf16_t *>(x), x_row_stride, n_rows, static_cast<const bf16_t *>(w1), b1, w2, b2,
               scores};
-  const int64_t nb = (n_rows + kSRows - 1) / kSRows;
+  // 256-row workgroups (each W1 byte streamed through LDS serves twice the rows) once they still
+  // give every CU two of them; 128-row ones below that, where a grid of the larger ones would
+  // leave CUs idle
+  const bool wide = (n_rows + 255) / 256 >= 2 * (int64_t)device_cus();
+  const int rows = wide ? 256 : 128;
+  const int64_t nb = (n_rows + rows - 1) / rows;
   TG_CHECK(nb < (1ll << 31), "grid too large");
-  hipLaunchKernelGGL(gate_score_kernel, dim3((unsigned)nb), dim3(kSThreads), 0, stream, a);
+  if (wide)
+    hipLaunchKernelGGL((gate_score_kernel<256, 4>), dim3((unsigned)nb), dim3(kSThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gate_score_kernel<128, 6>), dim3((unsigned)nb), dim3(kSThreads), 0, stream, a);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
 }

@@ -67,10 +67,14 @@ __device__ __forceinline__ float pair_max(float x) { return fmaxf(x, __shfl_xor(
 // __builtin_bit_cast to an element of a vector or of a builtin's result pair directly: this
 // compiler lowers __builtin_bit_cast(float, v[i]) to element 0 whatever i is.
 __device__ __forceinline__ float u32_as_f32(uint32_t u) { return __builtin_bit_cast(float, u); }
-// max of the two values a permlane swap returns
+// max of the two values a permlane swap returns.  A bare v_max_f32: fmaxf would first
+// canonicalise both operands (two more VALU instructions), which only matters for signalling
+// NaNs, and the values reduced here are arithmetic results, never signalling NaNs.
 template <typename Pair> __device__ __forceinline__ float swap_pair_max(const Pair &sw) {
   const uint32_t lo = sw[0], hi = sw[1];
-  return fmaxf(u32_as_f32(lo), u32_as_f32(hi));
+  float d;
+  asm("v_max_f32 %0, %1, %2" : "=v"(d) : "v"(u32_as_f32(lo)), "v"(u32_as_f32(hi)));
+  return d;
 }
 // Same as pair_max without the LDS crossbar: v_permlane32_swap(x, x) returns (lower half in both
 // halves, upper half in both halves), so the max of the two is max(x[l], x[l^32]) in every lane.
@@ -179,6 +183,19 @@ __device__ __forceinline__ float sum_bf16x2(uint32_t pair, float acc) {
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t x) {
   return __builtin_bit_cast(float, (uint32_t)x << 16);
+}
+
+// Compute units of the current device (cached per device id).
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
 }
 
 }  // namespace tg
