@@ -219,6 +219,14 @@ def bench_gate_ragged8(dev):
     scores = torch.randn(R, generator=g, device=dev).to(torch.bfloat16).float()
     x = torch.randn(R, 2048, generator=g, device=dev).to(torch.bfloat16)
     kv = [torch.randn(R, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    # the scoring head over all rows of the batch (the 256-row workgroup form at this size)
+    a1 = math.sqrt(6.0 / (2048 + 256))
+    w1 = ((torch.rand(256, 2048, generator=g, device=dev) * 2 - 1) * a1).to(torch.bfloat16)
+    w2 = (torch.rand(256, generator=g, device=dev) * 2 - 1) * math.sqrt(6.0 / 257)
+    b1 = torch.zeros(256, device=dev)
+    sc_out = torch.empty(R, dtype=torch.float32, device=dev)
+    ms_score = time_graph(lambda: gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out))
+    score_bytes = R * 2048 * 2 + w1.numel() * 2 + R * 4
     p = gate.plan(row0, lens, starts, ends, Ks, dev)
     T = p.total_kept
     outs = [torch.empty(T, 2048, dtype=torch.bfloat16, device=dev)] + \
@@ -236,7 +244,9 @@ def bench_gate_ragged8(dev):
     n_art = sum(e - s for s, e in zip(starts, ends))
     byts = 2 * T * (2048 * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4) + n_art * 4
     gbs = lambda ms: byts / (ms * 1e-3) / 1e9
-    return {"kept": T, "lens": lens, "K": Ks, "bytes": byts,
+    return {"score": {"rows": R, "ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
+                      "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "kept": T, "lens": lens, "K": Ks, "bytes": byts,
             "topk_single_wg_ms": round(ms_topk, 4), "topk_pack_ms": round(ms_old, 4),
             "topk_pack_frac_hbm": round(gbs(ms_old) / PEAK_HBM_GBS, 4),
             "select_multi_wg_ms": round(ms_sel, 4), "select_pack_ms": round(ms_new, 4),
@@ -388,8 +398,9 @@ def cpu_model() -> str:
 
 
 def gate_counter_run(dev, reps=5):
-    """Eager launches of the gate kernels for a per-dispatch counter profile: scoring at 32k; at 32k
-    for K in {100, 500, 2000} and on the ragged8 batch, the single-workgroup top-K, the pack, and
+    """Eager launches of the gate kernels for a per-dispatch counter profile: scoring at 32k and over
+    the ragged8 batch's rows; at 32k for K in {100, 500, 2000} and on the ragged8 batch, the
+    single-workgroup top-K, the pack, and
     the multi-workgroup selection + pack (gate.select_pack), `reps` times each; then three plain
     1 GiB device copies (counter calibration)."""
     import torch
@@ -431,6 +442,11 @@ def gate_counter_run(dev, reps=5):
     sc8 = torch.randn(R, generator=g, device=dev).to(torch.bfloat16).float()
     x8 = torch.randn(R, 2048, generator=g, device=dev).to(torch.bfloat16)
     kv8 = [torch.randn(R, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+    sc8_head = torch.empty(R, dtype=torch.float32, device=dev)
+    for _ in range(reps):
+        gate.score_mlp(x8, w1, b1, w2, 0.0, out=sc8_head)
+    torch.cuda.synchronize()
+    print("gate counters: ragged8 scoring done", flush=True)
     p8 = gate.plan([sum(lens[:b]) for b in range(8)], lens, [64] * 8, [L - 256 for L in lens], Ks, dev)
     one(sc8, p8, [x8] + kv8, "ragged8")
     del x8, kv8

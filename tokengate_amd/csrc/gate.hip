@@ -13,7 +13,8 @@
 //
 // Kernels:
 //   gate_score_kernel  — s = w2 . silu(W1 x + b1) + b2 for every row of a packed (rows, 2048)
-//                        bf16 matrix (256 rows per workgroup; W1 x on bf16 MFMA, fp32 epilogue);
+//                        bf16 matrix (128 or 256 rows per workgroup; W1 x on bf16 MFMA, fp32
+//                        epilogue);
 //   gate_topk_*kernel  — one workgroup per sequence: order-preserving uint32 keys, 4-pass 8-bit
 //                        radix select of the K_c-th largest key (keys held in registers for
 //                        articles up to 65536 tokens, else re-read from global memory), then an
@@ -35,15 +36,15 @@ namespace {
 
 // ---------------------------------------------------------------------------------------------
 // Scoring head: s = w2 . silu(W1 x + b1) + b2, x in R^2048 (bf16), W1 (256 x 2048) bf16.
-// Workgroup: 8 waves, 256 rows; wave w owns rows 128(w%2)..+127 and hidden units 64(w/2)..+63
-// (4 x 2 blocks of 32 x 32; 12 KiB of X and W fragments per wave per k step for 16 MFMAs).  Every
+// Workgroup: 8 waves, 256 rows (128 for grids too small to give every CU two 256-row workgroups);
+// wave w owns rows 128(w%2)..+127 and hidden units 64(w/2)..+63 (4 x 2 blocks of 32 x 32; 12 KiB of
+// X and W fragments per wave per k step for 16 MFMAs; half of that with 128 rows).  Every
 // workgroup streams all of W1 (1 MiB, L2-resident) through LDS once, so the rows per workgroup set
 // how many W1 bytes each X byte costs: 256 rows make it 2 MiB of X per 1 MiB of W1.  K loop over
-// the 2048 inputs in steps of 32 through a 5-deep LDS ring filled by DMA (X tile 256 x 32 and W1
-// tile 256 x 32, 16 KiB each per stage: the whole 160 KiB of LDS, the epilogue's row sums reusing
-// the first slot; three steps of X stay in flight), unrolled so that every ring slot index is a
-// compile-time constant, and software-pipelined: a
-// wave reads step k+1's fragments from LDS while its MFMAs of step k run, so the LDS reads and the
+// the 2048 inputs in steps of 32 through an LDS ring filled by DMA (256 rows: 4 slots of X tile
+// 256 x 32 + W1 tile 256 x 32, 32 KiB per slot; 128 rows: 6 slots of 24 KiB), unrolled so that
+// every ring slot index is a compile-time constant, and software-pipelined: a wave reads step
+// k+1's fragments from LDS while its MFMAs of step k run, so the LDS reads and the
 // matrix cores overlap instead of alternating between the per-step barriers.  Accumulators are
 // C^T blocks (hidden unit = MFMA row, token = column): each lane ends with one token's hidden
 // units of each block, the SiLU . w2 reduction is in-lane plus one cross-half exchange, and the four
