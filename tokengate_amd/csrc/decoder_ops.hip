@@ -374,6 +374,120 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   }
 }
 
+// Split-K form for dim > 2048 (the down projection, 6144 inputs): the kernel above walks a long
+// row in 2048-column steps, one HBM round trip each, over only n_out / 16 workgroups.  Here a
+// workgroup (4 waves) owns 4 output rows and wave wv takes the 512-column chunks wv, wv + 4,
+// wv + 8, ... of them, so the four waves split the dot products 4 ways.  When dim is 2048 * NJ
+// (NJ = 3: 6144) every wave has exactly NJ chunks and requests all of them (NJ x 4 rows x 16 B
+// per lane) before anything else, so a workgroup's whole 4-row slice of the weight is in flight
+// at once; other multiples of 512 take them one at a time (NJ = 0).
+template <int NCH>
+__device__ __forceinline__ void lin_load_sk(const bf16_t *const (&wr)[4], int c0, u32x4 (&wv_)[NCH][4]) {
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv_[j][r] = ld16(wr[r] + c0 + 2048 * j);
+}
+template <int NCH, int NR, int PRE>
+__device__ __forceinline__ void lin_dot_sk(const LinIn &in, const u32x4 (&wv_)[NCH][4], int c0, int lane,
+                                        const float (&rinv)[NR], float (&acc)[4][NR]) {
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c = c0 + 2048 * j + 8 * lane;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      const u32x4 xv = lin_input<NR, PRE>(in, b, c, rinv);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t wd = wv_[j][r][e], xd = xv[e];   // scalar copies: see u32_as_f32
+          acc[r][b] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wd), __builtin_bit_cast(bf16x2, xd),
+                                                      acc[r][b], false);
+        }
+    }
+  }
+}
+// One workgroup (4 waves) per 4 output rows; per wave the bf16 pair dot products of its chunks,
+// a wave butterfly per (row, input row), then the four waves' partial sums added in wave order
+// through LDS.
+template <int NR, typename OutT, int PRE, int NJ>
+__global__ __launch_bounds__(256) void linear_rows_splitk_kernel(LinIn in, const bf16_t *__restrict__ w, int64_t vocab,
+                                                          int dim, OutT *__restrict__ out, int64_t out_rs) {
+  __shared__ float part[4][4][NR];
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  const int64_t v0 = (int64_t)blockIdx.x * 4;
+  // rows past the end read the last row (in bounds; their sums are not stored)
+  const bf16_t *wr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
+  // the wave's chunks of the weight are requested before the input is formed
+  u32x4 wfirst[NJ > 0 ? NJ : 1][4];
+  if constexpr (NJ > 0) lin_load_sk<NJ>(wr, 512 * wv, wfirst);
+  float rinv[NR];
+  if constexpr (PRE == kPreNorm) {
+    // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ... element
+    // by element, then the wave butterfly
+    const bool writer = blockIdx.x == 0 && wv == 0 && in.res_out != nullptr;
+#pragma unroll
+    for (int b = 0; b < NR; ++b) {
+      float ss = 0.f;
+      for (int c = 8 * lane; c < dim; c += 512) {
+        float v[8];
+        unpack8(ld16(in.x + b * in.x_rs + c), v);
+        if (in.res) {
+          float r[8];
+          unpack8(ld16(in.res + b * in.res_rs + c), r);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
+        }
+        if (writer) st16(in.res_out + b * in.ro_rs + c, pack8(v));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+      }
+      ss = wave_sum(ss);
+      rinv[b] = rsqrtf(ss / (float)dim + in.eps);
+    }
+  }
+  float acc[4][NR];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int b = 0; b < NR; ++b) acc[r][b] = 0.f;
+  if constexpr (NJ > 0) {
+    lin_dot_sk<NJ, NR, PRE>(in, wfirst, 512 * wv, lane, rinv, acc);
+  } else {
+    for (int c0 = 512 * wv; c0 < dim; c0 += 2048) {
+      u32x4 wv_[1][4];
+      lin_load_sk<1>(wr, c0, wv_);
+      lin_dot_sk<1, NR, PRE>(in, wv_, c0, lane, rinv, acc);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int b = 0; b < NR; ++b) acc[r][b] = wave_sum(acc[r][b]);
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int b = 0; b < NR; ++b) part[wv][r][b] = acc[r][b];
+  }
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t < 4 * NR) {
+    const int r = t / NR, b = t % NR;
+    if (v0 + r < vocab) {
+      const float sum = ((part[0][r][b] + part[1][r][b]) + part[2][r][b]) + part[3][r][b];
+      const __bf16 y = (__bf16)sum;
+      if constexpr (std::is_same<OutT, float>::value)
+        out[b * out_rs + v0 + r] = (float)y;
+      else
+        out[b * out_rs + v0 + r] = __builtin_bit_cast(bf16_t, y);
+    }
+  }
+}
+
 // ---- Greedy token: the index of each row's largest logit -----------------------------------------
 // torch.argmax semantics: a NaN beats every number, and equal values go to the lower index.  One
 // 1024-thread workgroup per row: each thread scans its strided 16-byte pieces, then the (value,
@@ -565,10 +679,19 @@ int launch_linear_rows(const LinIn &in, int32_t n_rows, const void *weight, int6
                        int64_t out_row_stride, hipStream_t stream) {
   const int64_t blocks = (n_out + 15) / 16;
   const bf16_t *wp = static_cast<const bf16_t *>(weight);
+  const int64_t sk_blocks = (n_out + 3) / 4;
 #define TG_LR(NR)                                                                                          \
-  if (n_rows == NR)                                                                                        \
-    hipLaunchKernelGGL((linear_rows_kernel<NR, OutT, PRE>), dim3((unsigned)blocks), dim3(256), 0, stream, in, wp, \
-                       n_out, dim, out, out_row_stride);
+  if (n_rows == NR) {                                                                                      \
+    if (dim <= 2048)                                                                                       \
+      hipLaunchKernelGGL((linear_rows_kernel<NR, OutT, PRE>), dim3((unsigned)blocks), dim3(256), 0, stream, in, wp, \
+                         n_out, dim, out, out_row_stride);                                                 \
+    else if (dim == 6144)                                                                                  \
+      hipLaunchKernelGGL((linear_rows_splitk_kernel<NR, OutT, PRE, 3>), dim3((unsigned)sk_blocks), dim3(256), 0,  \
+                         stream, in, wp, n_out, dim, out, out_row_stride);                                 \
+    else                                                                                                   \
+      hipLaunchKernelGGL((linear_rows_splitk_kernel<NR, OutT, PRE, 0>), dim3((unsigned)sk_blocks), dim3(256), 0,  \
+                         stream, in, wp, n_out, dim, out, out_row_stride);                                 \
+  }
   TG_LR(1) TG_LR(2) TG_LR(3) TG_LR(4) TG_LR(5) TG_LR(6) TG_LR(7) TG_LR(8)
 #undef TG_LR
   TG_HIP_CHECK(hipGetLastError());
