@@ -668,7 +668,9 @@ SplitPlan plan_split(int nw, int hp, int n_qtiles, int64_t units, int sq, int sk
   };
   const int tmax = tiles(n_qtiles - 1);
   int ns = (int)std::min<int64_t>(32, std::max<int64_t>(2, slots / nblocks));
-  ns = std::min(ns, tmax / 4);
+  // at least 4 key tiles per chunk; 2 for a few query rows (a decode step), whose chunks are short
+  // enough that the tile count, not the merge, sets their time (decode at 2.3k keys: -2 %)
+  ns = std::min(ns, tmax / (sq <= 16 ? 2 : 4));
   if (ns < 2) return p;
   int n_heavy = 0;
   for (int qt = n_qtiles - 1; qt >= 0 && (int64_t)tiles(qt) * ns > tmax; --qt) ++n_heavy;
