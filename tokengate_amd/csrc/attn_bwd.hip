@@ -506,27 +506,45 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       // accumulator value i of row block rb is query m0 + 8g + 4rb + i
       const bool need_mask = (m0 + kQT > sq) || (kw0 + 16 > sk) || (CAUSAL && kw0 + 15 > m0 + off);
       uint32_t pk[4], dk4[4];
+      float p[2][4];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
         const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lsl + 8 * g + 4 * rb);
-        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dsl + 8 * g + 4 * rb);
-        float p[4], ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float z = sacc[rb][i];
           if constexpr (HAS_BIAS) z += bk;
-          p[i] = fast_exp2(fmaf(z, a.scale_log2, -l4[i] * kLog2e));
-          if (need_mask) {
+          p[rb][i] = fast_exp2(fmaf(z, a.scale_log2, -l4[i] * kLog2e));
+        }
+      }
+      // one uniform branch for the whole tile, and no per-element branches inside it: P -> +0 where
+      // the query is past the sequence, the key past the keys, or (causal) the key after the query,
+      // selected by the sign of the smallest margin
+      if (need_mask) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
             const int qi = m0 + 8 * g + 4 * rb + i;
-            bool masked = qi >= sq || !kvalid;
-            if constexpr (CAUSAL) masked = masked || (key > qi + off);
-            p[i] = masked ? 0.f : p[i];
+            int lim = kvalid ? sq - 1 - qi : -1;
+            if constexpr (CAUSAL) lim = min(lim, qi + off - key);
+            int sgn;
+            asm("v_ashrrev_i32 %0, 31, %1" : "=v"(sgn) : "v"(lim));   // -1 where masked
+            const uint32_t pbits = __builtin_bit_cast(uint32_t, p[rb][i]) & ~(uint32_t)sgn;
+            p[rb][i] = __builtin_bit_cast(float, pbits);
           }
-          ds[i] = p[i] * (pacc[rb][i] - d4[i]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dsl + 8 * g + 4 * rb);
+        float ds[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ds[i] = p[rb][i] * (pacc[rb][i] - d4[i]);
           dbacc += ds[i];
         }
-        pk[2 * rb] = pack_bf16x2(p[0], p[1]);
-        pk[2 * rb + 1] = pack_bf16x2(p[2], p[3]);
+        pk[2 * rb] = pack_bf16x2(p[rb][0], p[rb][1]);
+        pk[2 * rb + 1] = pack_bf16x2(p[rb][2], p[rb][3]);
         dk4[2 * rb] = pack_bf16x2(ds[0], ds[1]);
         dk4[2 * rb + 1] = pack_bf16x2(ds[2], ds[3]);
       }
