@@ -156,7 +156,8 @@ def test_lm_head(cuda, rows, vocab, dim):
     assert torch.equal(got.argmax(-1)[clear], tl.argmax(-1)[clear])
 
 
-@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (3, 2048, 6144), (8, 12288, 2048), (2, 2048, 1024)])
+@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (3, 2048, 6144), (8, 12288, 2048), (2, 2048, 1024),
+                                          (2, 1000, 4096), (1, 517, 2560)])
 def test_linear_rows(cuda, rows, n_out, dim):
     """The decode-step projection GEMV (tg_linear_rows, bf16 out) against the float64 product of
     the same bf16 inputs rounded to bf16 (F.linear on bf16 tensors): within one bf16 ulp
@@ -201,6 +202,20 @@ def test_linear_rows_norm_and_swiglu(cuda, rows, n_out, dim, with_res):
     assert torch.equal(ro, r2 if with_res else h)
     gu = _bf(torch.randn(rows, 2 * dim, generator=g, device=cuda))
     wd = _bf(torch.randn(n_out, dim, generator=g, device=cuda) * dim ** -0.5)
+    got = dec.linear_rows_swiglu(gu, wd)
+    ref = dec.linear_rows(dec.silu_mul(gu), wd)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("rows,n_out,inter", [(1, 2048, 6144), (2, 2048, 6144), (8, 1000, 6144), (3, 998, 4096)])
+def test_linear_rows_swiglu_long_rows(cuda, rows, n_out, inter):
+    """The down projection's long rows (split-K form: four waves per 4 output rows): the SwiGLU-fused
+    input equals silu_mul then tg_linear_rows bit for bit, at the decoder's 6144 and another length."""
+    from tokengate_amd import decoder as dec
+    g = torch.Generator(device=cuda).manual_seed(rows * 13 + n_out + inter)
+    gu = _bf(torch.randn(rows, 2 * inter, generator=g, device=cuda))
+    wd = _bf(torch.randn(n_out, inter, generator=g, device=cuda) * inter ** -0.5)
     got = dec.linear_rows_swiglu(gu, wd)
     ref = dec.linear_rows(dec.silu_mul(gu), wd)
     torch.cuda.synchronize()

@@ -336,6 +336,28 @@ def test_config_scoring_and_pruning_32k(cuda, K):
     assert_close("fused bias", to_np(bias2), ref_bias, max_abs=1e-5, rel_l2=1e-6)
 
 
+def test_scoring_wide_workgroups(cuda):
+    """The scoring head's 256-row workgroup form (taken when the grid still gives every CU two of
+    them): a ragged row count that covers chips of up to 304 CUs, checked on sampled rows (every
+    97th, the first and last 300) against the float64 oracle, and row for row equal to the same
+    rows scored in small launches, which take the 128-row form."""
+    from tokengate_amd import gate
+    n = 256 * 2 * 304 + 77
+    g = torch.Generator(device=cuda).manual_seed(11)
+    x = torch.randn(n, 2048, generator=g, device=cuda).to(torch.bfloat16)
+    w1 = _xavier((256, 2048), g, cuda).to(torch.bfloat16)
+    w2 = _xavier((1, 256), g, cuda)[0].contiguous()
+    b1 = torch.randn(256, generator=g, device=cuda) * 0.1
+    scores = gate.score_mlp(x, w1, b1, w2, 0.25)
+    small = torch.cat([gate.score_mlp(x[r:r + 8192], w1, b1, w2, 0.25) for r in (0, n - 8192)])
+    torch.cuda.synchronize()
+    assert torch.equal(scores[:8192], small[:8192]) and torch.equal(scores[n - 8192:], small[8192:])
+    rows = np.unique(np.concatenate([np.arange(0, n, 97), np.arange(300), np.arange(n - 300, n)]))
+    idx = torch.from_numpy(rows).to(cuda)
+    ref = og.score_mlp(to_np(x.index_select(0, idx)), to_np(w1), to_np(b1), to_np(w2), 0.25)
+    assert_close("wide scores", to_np(scores.index_select(0, idx)), ref, max_abs=2e-3, rel_l2=1e-4)
+
+
 def test_ragged8_select_pack(cuda):
     """The ragged pruned-prefill batch at full size: 8 prompts of 16k-128k tokens (prefix 64,
     suffix 256), K from {100, 500, 2000, 4000}, bf16-valued scores (ties at every threshold), the
