@@ -270,15 +270,19 @@ __device__ __forceinline__ void lin_load(const bf16_t *const (&wr)[4], int cg, u
 #pragma unroll
     for (int r = 0; r < 4; ++r) wv[ch][r] = ld16(wr[r] + cg + 512 * ch);
 }
+// xs: the NR input rows formed once per workgroup in LDS (norm / SwiGLU stages), row stride
+// kLinXsRow; NULL for the plain stage, whose rows are read from global memory (L2).
+constexpr int kLinXsRow = 2048;
 template <int NCH, int NR, int PRE>
-__device__ __forceinline__ void lin_dot(const LinIn &in, const u32x4 (&wv)[NCH][4], int cg, int lane,
-                                        const float (&rinv)[NR], float (&acc)[4][NR]) {
+__device__ __forceinline__ void lin_dot(const LinIn &in, const bf16_t *xs, const u32x4 (&wv)[NCH][4], int cg,
+                                        int lane, float (&acc)[4][NR]) {
 #pragma unroll
   for (int ch = 0; ch < NCH; ++ch) {
     const int c = cg + 512 * ch + 8 * lane;
 #pragma unroll
     for (int b = 0; b < NR; ++b) {
-      const u32x4 xv = lin_input<NR, PRE>(in, b, c, rinv);
+      const u32x4 xv = PRE == kPrePlain ? ld16(in.x + b * in.x_rs + c)
+                                        : *reinterpret_cast<const u32x4 *>(xs + b * kLinXsRow + c);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -290,13 +294,20 @@ __device__ __forceinline__ void lin_dot(const LinIn &in, const u32x4 (&wv)[NCH][
     }
   }
 }
+// Rows of at most 2048 inputs (longer ones take the split-K form below).  The norm / SwiGLU
+// input stage is formed once per workgroup into LDS: with the norm, wave w computes the sum of
+// squares of input rows w, w + 4, ... (in the RMSNorm kernel's order), then the 256 threads
+// write the normalised (or SwiGLU) rows; every wave's dot products read them from LDS.
 template <int NR, typename OutT, int PRE>
 __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t *__restrict__ w, int64_t vocab,
                                                           int dim, OutT *__restrict__ out, int64_t out_rs) {
-  const int lane = threadIdx.x & 63;
-  const int64_t v0 = ((int64_t)blockIdx.x * 4 + wave_id()) * 4;
-  if (v0 >= vocab) return;
-  // rows past the end read the last row (in bounds; their sums are not stored)
+  constexpr bool kStage = PRE != kPrePlain;
+  __shared__ __attribute__((aligned(16))) bf16_t xs[kStage ? NR * kLinXsRow : 8];
+  __shared__ float rinv_s[NR];
+  const int lane = threadIdx.x & 63, wv = wave_id();
+  const int64_t v0 = ((int64_t)blockIdx.x * 4 + wv) * 4;
+  // rows past the end read the last row (in bounds; their sums are not stored); a wave whose rows
+  // are all past the end still takes part in the workgroup's barriers
   const bf16_t *wr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
@@ -304,30 +315,40 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   u32x4 wfirst[4][4];
   const bool first = dim >= 2048;
   if (first) lin_load<4>(wr, 0, wfirst);
-  float rinv[NR];
-  if constexpr (PRE == kPreNorm) {
-    // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ... element
-    // by element, then the wave butterfly
-    const bool writer = blockIdx.x == 0 && wave_id() == 0 && in.res_out != nullptr;
+  if constexpr (kStage) {
+    float rinv[NR] = {};
+    if constexpr (PRE == kPreNorm) {
+      // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ...
+      // element by element, then the wave butterfly
+      const bool writer = blockIdx.x == 0 && in.res_out != nullptr;
+      for (int b = wv; b < NR; b += 4) {
+        float ss = 0.f;
+        for (int c = 8 * lane; c < dim; c += 512) {
+          float v[8];
+          unpack8(ld16(in.x + b * in.x_rs + c), v);
+          if (in.res) {
+            float r[8];
+            unpack8(ld16(in.res + b * in.res_rs + c), r);
 #pragma unroll
-    for (int b = 0; b < NR; ++b) {
-      float ss = 0.f;
-      for (int c = 8 * lane; c < dim; c += 512) {
-        float v[8];
-        unpack8(ld16(in.x + b * in.x_rs + c), v);
-        if (in.res) {
-          float r[8];
-          unpack8(ld16(in.res + b * in.res_rs + c), r);
+            for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
+          }
+          if (writer) st16(in.res_out + b * in.ro_rs + c, pack8(v));
 #pragma unroll
-          for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
+          for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
         }
-        if (writer) st16(in.res_out + b * in.ro_rs + c, pack8(v));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        ss = wave_sum(ss);
+        if (lane == 0) rinv_s[b] = rsqrtf(ss / (float)dim + in.eps);
       }
-      ss = wave_sum(ss);
-      rinv[b] = rsqrtf(ss / (float)dim + in.eps);
+      __syncthreads();
+#pragma unroll
+      for (int b = 0; b < NR; ++b) rinv[b] = rinv_s[b];
     }
+    const int groups = dim / 8;
+    for (int idx = threadIdx.x; idx < NR * groups; idx += 256) {
+      const int b = idx / groups, c = 8 * (idx - b * groups);
+      *reinterpret_cast<u32x4 *>(xs + b * kLinXsRow + c) = lin_input<NR, PRE>(in, b, c, rinv);
+    }
+    __syncthreads();
   }
   float acc[4][NR];
 #pragma unroll
@@ -336,24 +357,24 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
     for (int b = 0; b < NR; ++b) acc[r][b] = 0.f;
   int cg = 0;
   if (first) {
-    lin_dot<4, NR, PRE>(in, wfirst, 0, lane, rinv, acc);
+    lin_dot<4, NR, PRE>(in, xs, wfirst, 0, lane, acc);
     cg = 2048;
   }
   for (; cg + 2048 <= dim; cg += 2048) {
-    u32x4 wv[4][4];
-    lin_load<4>(wr, cg, wv);
-    lin_dot<4, NR, PRE>(in, wv, cg, lane, rinv, acc);
+    u32x4 wv_[4][4];
+    lin_load<4>(wr, cg, wv_);
+    lin_dot<4, NR, PRE>(in, xs, wv_, cg, lane, acc);
   }
   if (dim - cg >= 1024) {
-    u32x4 wv[2][4];
-    lin_load<2>(wr, cg, wv);
-    lin_dot<2, NR, PRE>(in, wv, cg, lane, rinv, acc);
+    u32x4 wv_[2][4];
+    lin_load<2>(wr, cg, wv_);
+    lin_dot<2, NR, PRE>(in, xs, wv_, cg, lane, acc);
     cg += 1024;
   }
   if (dim - cg >= 512) {
-    u32x4 wv[1][4];
-    lin_load<1>(wr, cg, wv);
-    lin_dot<1, NR, PRE>(in, wv, cg, lane, rinv, acc);
+    u32x4 wv_[1][4];
+    lin_load<1>(wr, cg, wv_);
+    lin_dot<1, NR, PRE>(in, xs, wv_, cg, lane, acc);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r)

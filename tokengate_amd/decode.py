@@ -55,6 +55,9 @@ def _relayout(kv: LayerKV, cu: List[int], gap: int) -> LayerKV:
 
 
 class DecodeState:
+    # most rows per step for which the norms and the SwiGLU product are folded into the projections
+    max_fused_rows = 2
+
     def __init__(self, wts: DecoderWeights, head: ScoringHead, gate_layer: int, pf: PrefillResult,
                  max_new_tokens: int, prune_below_gate: bool = False, graph: bool = False, fused: bool = True):
         shape = wts.shape
@@ -136,9 +139,8 @@ class DecodeState:
         B = self.B
         dev = tokens.device
         x = torch.nn.functional.embedding(tokens, w.embed)
-        # the fused projections form their input in every wave, which pays off for one or two rows;
-        # with more rows the separate norm / SwiGLU launches are cheaper (8 rows: 4.2 against 9.9 ms)
-        fused = self.fused and B <= 2 and s.d_model % 512 == 0 and s.d_ff % 512 == 0
+        # rows beyond max_fused_rows take the separate norm / SwiGLU launches
+        fused = self.fused and B <= self.max_fused_rows and s.d_model % 512 == 0 and s.d_ff % 512 == 0
         res = None if fused else x.clone()
         normed = torch.empty_like(x)
         hid = torch.empty_like(x)
