@@ -2,8 +2,11 @@
 //   * residual add + RMSNorm (the input / post-attention norms of a Qwen3 layer and the final norm),
 //   * per-head q/k RMSNorm + rotary embedding at each token's own position, writing q in place
 //     and k / v into the layer's KV cache rows,
-//   * SiLU(gate) * up of the fused gate/up projection.
-// The projections themselves are plain GEMMs and stay on hipBLASLt.
+//   * SiLU(gate) * up of the fused gate/up projection;
+//   * for the few rows of a decode step: the projections as HBM-bound GEMVs (a row form for rows
+//     of up to 2048 inputs, a split-K form for longer ones), optionally with the RMSNorm or the
+//     SwiGLU product folded into their input, and the greedy argmax over the logits.
+// The prefill's projections (many rows) are plain GEMMs and stay on hipBLASLt.
 #include <type_traits>
 
 #include "tg_common.h"
