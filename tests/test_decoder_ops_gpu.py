@@ -179,7 +179,8 @@ def test_linear_rows(cuda, rows, n_out, dim):
           f"{float((err == 0).double().mean()):.4f} of entries", flush=True)
 
 
-@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (5, 2048, 1024), (8, 12288, 2048)])
+@pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (5, 2048, 1024), (8, 12288, 2048), (2, 1000, 4096),
+                                          (3, 517, 2560)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_linear_rows_norm_and_swiglu(cuda, rows, n_out, dim, with_res):
     """The fused-input projections equal their two-launch forms bit for bit: RMSNorm (tg_rmsnorm,
