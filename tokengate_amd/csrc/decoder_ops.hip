@@ -319,14 +319,21 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   const bool first = dim >= 2048;
   if (first) lin_load<4>(wr, 0, wfirst);
   if constexpr (kStage) {
-    float rinv[NR] = {};
+    const int groups = dim / 8;   // NR * groups <= 256 * NR: thread t owns chunks t + 256 i, i < NR
     if constexpr (PRE == kPreNorm) {
-      // sum of squares in the RMSNorm kernel's order: lane l sums its chunks l, l + 64, ...
-      // element by element, then the wave butterfly
+      // One read of the input rows: s = bf16(h + res) (exact in bf16) goes to LDS (block 0 also
+      // writes res_out) and the norm weight of the thread's chunks to registers.  The sums of
+      // squares then come from LDS in the RMSNorm kernel's order (lane l sums its chunks l,
+      // l + 64, ... element by element, then the wave butterfly), and each thread scales its own
+      // chunks in place: the same arithmetic as lin_input, one global round trip fewer.
       const bool writer = blockIdx.x == 0 && in.res_out != nullptr;
-      for (int b = wv; b < NR; b += 4) {
-        float ss = 0.f;
-        for (int c = 8 * lane; c < dim; c += 512) {
+      u32x4 nwv[NR];
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        if (idx < NR * groups) {
+          const int b = idx / groups, c = 8 * (idx - b * groups);
+          nwv[i] = ld16(in.nw + c);
           float v[8];
           unpack8(ld16(in.x + b * in.x_rs + c), v);
           if (in.res) {
@@ -335,7 +342,17 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
           }
-          if (writer) st16(in.res_out + b * in.ro_rs + c, pack8(v));
+          const u32x4 pv = pack8(v);
+          if (writer) st16(in.res_out + b * in.ro_rs + c, pv);
+          *reinterpret_cast<u32x4 *>(xs + b * kLinXsRow + c) = pv;
+        }
+      }
+      __syncthreads();
+      for (int b = wv; b < NR; b += 4) {
+        float ss = 0.f;
+        for (int c = 8 * lane; c < dim; c += 512) {
+          float v[8];
+          unpack8(*reinterpret_cast<const u32x4 *>(xs + b * kLinXsRow + c), v);
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
         }
@@ -344,12 +361,25 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
       }
       __syncthreads();
 #pragma unroll
-      for (int b = 0; b < NR; ++b) rinv[b] = rinv_s[b];
-    }
-    const int groups = dim / 8;
-    for (int idx = threadIdx.x; idx < NR * groups; idx += 256) {
-      const int b = idx / groups, c = 8 * (idx - b * groups);
-      *reinterpret_cast<u32x4 *>(xs + b * kLinXsRow + c) = lin_input<NR, PRE>(in, b, c, rinv);
+      for (int i = 0; i < NR; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        if (idx < NR * groups) {
+          const int b = idx / groups, c = 8 * (idx - b * groups);
+          float v[8], wf[8], y[8];
+          unpack8(*reinterpret_cast<const u32x4 *>(xs + b * kLinXsRow + c), v);
+          unpack8(nwv[i], wf);
+          const float ri = rinv_s[b];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[e] = wf[e] * (v[e] * ri);
+          *reinterpret_cast<u32x4 *>(xs + b * kLinXsRow + c) = pack8(y);
+        }
+      }
+    } else {
+      const float rinv[NR] = {};
+      for (int idx = threadIdx.x; idx < NR * groups; idx += 256) {
+        const int b = idx / groups, c = 8 * (idx - b * groups);
+        *reinterpret_cast<u32x4 *>(xs + b * kLinXsRow + c) = lin_input<NR, PRE>(in, b, c, rinv);
+      }
     }
     __syncthreads();
   }
