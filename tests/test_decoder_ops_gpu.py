@@ -180,7 +180,7 @@ def test_linear_rows(cuda, rows, n_out, dim):
 
 
 @pytest.mark.parametrize("rows,n_out,dim", [(1, 4096, 2048), (5, 2048, 1024), (8, 12288, 2048), (2, 1000, 4096),
-                                          (3, 517, 2560)])
+                                          (3, 517, 2560), (7, 333, 512)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_linear_rows_norm_and_swiglu(cuda, rows, n_out, dim, with_res):
     """The fused-input projections equal their two-launch forms bit for bit: RMSNorm (tg_rmsnorm,
