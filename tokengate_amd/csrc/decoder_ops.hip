@@ -314,12 +314,27 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
   const bf16_t *wr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) wr[r] = w + min(v0 + r, vocab - 1) * dim + 8 * lane;
-  // the first 2048 columns of the weight are requested before the input is formed
+  const int groups = dim / 8;   // NR * groups <= 256 * NR: thread t owns chunks t + 256 i, i < NR
+  // The norm stage's inputs are requested first, then the first 2048 columns of the weight:
+  // loads complete in issue order, so the stage can run while the weight bytes stream in.
+  constexpr int kIn = PRE == kPreNorm ? NR : 1;
+  u32x4 xin[kIn], rin[kIn], nwv[kIn];
+  if constexpr (PRE == kPreNorm) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      const int idx = threadIdx.x + 256 * i;
+      if (idx < NR * groups) {
+        const int b = idx / groups, c = 8 * (idx - b * groups);
+        nwv[i] = ld16(in.nw + c);
+        xin[i] = ld16(in.x + b * in.x_rs + c);
+        if (in.res) rin[i] = ld16(in.res + b * in.res_rs + c);
+      }
+    }
+  }
   u32x4 wfirst[4][4];
   const bool first = dim >= 2048;
   if (first) lin_load<4>(wr, 0, wfirst);
   if constexpr (kStage) {
-    const int groups = dim / 8;   // NR * groups <= 256 * NR: thread t owns chunks t + 256 i, i < NR
     if constexpr (PRE == kPreNorm) {
       // One read of the input rows: s = bf16(h + res) (exact in bf16) goes to LDS (block 0 also
       // writes res_out) and the norm weight of the thread's chunks to registers.  The sums of
@@ -327,18 +342,16 @@ __global__ __launch_bounds__(256) void linear_rows_kernel(LinIn in, const bf16_t
       // l + 64, ... element by element, then the wave butterfly), and each thread scales its own
       // chunks in place: the same arithmetic as lin_input, one global round trip fewer.
       const bool writer = blockIdx.x == 0 && in.res_out != nullptr;
-      u32x4 nwv[NR];
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
         const int idx = threadIdx.x + 256 * i;
         if (idx < NR * groups) {
           const int b = idx / groups, c = 8 * (idx - b * groups);
-          nwv[i] = ld16(in.nw + c);
           float v[8];
-          unpack8(ld16(in.x + b * in.x_rs + c), v);
+          unpack8(xin[i], v);
           if (in.res) {
             float r[8];
-            unpack8(ld16(in.res + b * in.res_rs + c), r);
+            unpack8(rin[i], r);
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = (float)(__bf16)(v[e] + r[e]);
           }
