@@ -215,7 +215,9 @@ typedef struct tg_pack_stream {
  * sequence b, every stream copies source row geom[b].row_start + keep[j] to destination row j;
  * positions_out[j] = keep[j] (int64, optional); bias_out[j] (optional) = the kept row's score
  * bias_src[row_start + keep[j]] scaled by rsqrt(sumsq[b] / n_art + rms_eps) when sumsq is given,
- * on article rows, and 0 on prefix / suffix rows.  At most 16 streams. */
+ * on article rows, and 0 on prefix / suffix rows.  A kept position outside [0, seq_len) of its
+ * sequence gathers nothing (destination row, positions_out and bias_out entries left as they
+ * were).  At most 16 streams. */
 int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep,
                  const int32_t *geom, int32_t num_seqs, int64_t total_kept, int64_t *positions_out,
                  const float *bias_src, const float *sumsq, float rms_eps, float *bias_out,
@@ -235,10 +237,13 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
  * zero-filled before its first use, for calls of at most seq_capacity sequences and
  * chunk_capacity chunks (every call on one workspace passes the same capacities: its layout
  * depends on them alone).  Every call leaves its counters zeroed again, so stream-ordered calls
- * reuse it without clearing; calls that overlap on one workspace race.  Global word 2 of the
- * workspace is an error flag no call clears (nonzero: a wait timed out or an internal count was
- * inconsistent; no row outside a sequence is ever written).  No workgroup waits for one that may
- * not have started: every call completes whatever the scheduling. */
+ * reuse it without clearing; calls that overlap on one workspace race.  The 32-bit word at byte
+ * offset 8 of the workspace is an error word that stays set until the caller clears it: 1 = a
+ * look-back wait timed out, 2 = a chunk's count overran its sequence, 3 = the gather met a kept
+ * position outside its sequence (a keep entry left unwritten) and skipped that row.  Nonzero means
+ * the keep lists and gathered rows of the calls since it was last cleared are not to be used; no
+ * row outside a sequence is ever read or written.  No workgroup waits for one that may not have
+ * started: every call completes whatever the scheduling. */
 int tg_gate_select_pack(const float *scores, const int32_t *geom, const int32_t *wg_start, int32_t num_seqs,
                         int32_t n_select_wgs, int32_t keys_per_thread, const tg_pack_stream *streams,
                         int32_t n_streams, int64_t total_kept, int64_t *keep, int64_t *positions_out,

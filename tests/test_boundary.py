@@ -137,6 +137,33 @@ def test_fwd_workspace_size_queries():
     assert lib.tg_keybias_fwd_workspace_size(1, 1, 128, 16, 8, 1) == 0
 
 
+def test_fwd_split_fits_the_resident_slots():
+    """Every split plan keeps its chunks within the resident-workgroup slots, so its partials need
+    at most CUs x 73,728 bytes (18 MiB at the 256 CUs assumed without a GPU): the bound behind the
+    static scratch of tg_keybias_fwd_noalloc.  Grids of more than half the slots (a few thousand
+    rows over a long cache) once planned 1.5x that."""
+    from tokengate_amd import _lib
+    lib = _lib.load()
+    bound = 256 * 73728
+    worst = 0
+    for sq in (1, 3, 17, 500, 1000, 1500, 2000, 2320, 2500, 2800, 3000, 3072, 3500, 4000, 4096, 6000, 8192):
+        for sk in (sq, 4096, 9000, 32768, 131072):
+            if sk < sq:
+                continue
+            for b in (1, 2, 4):
+                for causal in (0, 1):
+                    n = lib.tg_keybias_fwd_workspace_size(b, sq, sk, 16, 8, causal)
+                    worst = max(worst, n)
+                    assert 0 <= n <= bound, (b, sq, sk, causal, n)
+    for sq in (1, 700, 2320, 3000, 9000):
+        n = lib.tg_keybias_varlen_fwd_workspace_size(3, sq, 16, 8, 1)
+        assert 0 <= n <= bound, (sq, n)
+    # the shapes that exceeded the scratch before the cap still split, inside the bound
+    for args in ((1, 3072, 32768, 16, 8, 1), (1, 3072, 4096, 16, 8, 0), (1, 3000, 32768, 16, 8, 1)):
+        assert 0 < lib.tg_keybias_fwd_workspace_size(*args) <= bound, args
+    assert worst > 0
+
+
 def test_python_checks_match_reference_messages():
     from tokengate_amd.fa2bias.keybias import ext
     q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)

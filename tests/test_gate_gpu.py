@@ -414,3 +414,66 @@ def test_select_pack_workspace_reuse_across_batch_sizes(cuda):
         p = _run_select(scores, seqs, cuda)[2]
         ref, _, _ = og.select_and_pack(scores.astype(np.float64), seqs)
         _check_select_pack(scores, seqs, ref, p, cuda)
+
+
+def test_pack_skips_positions_outside_their_sequence(cuda):
+    """A kept position outside [0, seq_len) of its sequence (what an unwritten keep entry holds)
+    gathers nothing: that destination row and its position / bias entries keep their contents, the
+    other rows are gathered as usual.  The kernel's own range check turns these entries into skips;
+    no access leaves the source rows of the entry's sequence."""
+    from tokengate_amd import gate
+    seqs = [(0, 300, 10, 290, 20), (300, 500, 0, 500, 40)]
+    p = gate.plan([x[0] for x in seqs], [x[1] for x in seqs], [x[2] for x in seqs], [x[3] for x in seqs],
+                  [x[4] for x in seqs], cuda)
+    rng = np.random.default_rng(11)
+    scores = torch.from_numpy(rng.standard_normal(800).astype(np.float32)).to(cuda)
+    keep, sumsq = gate.select_keep(scores, p)
+    bad = keep.clone()
+    # sequence 0 (300 rows): -1 and 300 (its own length); sequence 1: 10^9 and -2^40
+    c0, c1 = p.cu_kept[1], p.cu_kept[2]
+    bad_rows = [0, 5, c0 + 3, c1 - 1]
+    bad[bad_rows[0]] = -1
+    bad[bad_rows[1]] = 300
+    bad[bad_rows[2]] = 10 ** 9
+    bad[bad_rows[3]] = -(2 ** 40)
+    src = torch.arange(800 * 8, dtype=torch.int32, device=cuda).view(800, 8)
+    dst = torch.full((p.total_kept, 8), -1, dtype=torch.int32, device=cuda)
+    pos = torch.full((p.total_kept,), -7, dtype=torch.int64, device=cuda)
+    bias = torch.full((p.total_kept,), 5.0, dtype=torch.float32, device=cuda)
+    gate.pack(bad, p, [(src, dst)], positions=pos, bias_src=scores, sumsq=sumsq, bias_out=bias)
+    torch.cuda.synchronize()
+    good = torch.ones(p.total_kept, dtype=torch.bool)
+    good[bad_rows] = False
+    k = keep.cpu().numpy()
+    row_of = np.concatenate([seqs[b][0] + k[p.cu_kept[b]:p.cu_kept[b + 1]] for b in range(2)])
+    d, s_ = dst.cpu(), src.cpu()
+    assert torch.equal(d[good], s_[torch.from_numpy(row_of)][good])
+    assert bool((d[~good] == -1).all()) and bool((pos.cpu()[~good] == -7).all())
+    assert bool((bias.cpu()[~good] == 5.0).all())
+    assert torch.equal(pos.cpu()[good], keep.cpu()[good])
+
+
+def test_select_pack_error_word_round_trip(cuda):
+    """The error word of tg_gate_select_pack's workspace stays set until reported: select_pack
+    (check=True) raises on it and clears it, so the next call is clean; error_out receives it."""
+    from tokengate_amd import gate
+    rng = np.random.default_rng(12)
+    seqs = [(0, 4000, 64, 3800, 100), (4000, 9000, 0, 9000, 700)]
+    scores_np = rng.standard_normal(13000).astype(np.float32)
+    scores = torch.from_numpy(scores_np).to(cuda)
+    p = gate.plan([x[0] for x in seqs], [x[1] for x in seqs], [x[2] for x in seqs], [x[3] for x in seqs],
+                  [x[4] for x in seqs], cuda)
+    ref, _, _ = og.select_and_pack(scores_np.astype(np.float64), seqs)
+    keep = gate.select_pack(scores, p, [], check=True)
+    assert np.array_equal(keep.cpu().numpy(), ref)
+    stream = torch.cuda.current_stream().cuda_stream
+    ws = gate._SEL_WS[(torch.device(cuda).index, stream)][0]
+    gate._error_word(ws).fill_(1)        # as a timed-out wait leaves it
+    err = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    with pytest.raises(RuntimeError, match="error word 1"):
+        gate.select_pack(scores, p, [], check=True, error_out=err)
+    assert int(err[0]) == 1
+    assert int(gate._error_word(ws).item()) == 0      # cleared by the report
+    keep2 = gate.select_pack(scores, p, [], check=True, error_out=err)
+    torch.cuda.synchronize()
+    assert int(err[0]) == 0 and np.array_equal(keep2.cpu().numpy(), ref)

@@ -231,6 +231,30 @@ def test_prefill_prune_below_gate(cuda):
         assert torch.equal(pruned.kv[i].k, full.kv[i].k)
 
 
+def test_prefill_raises_on_selection_error(cuda):
+    """The prefill reads the keep-list selection's error word back (asynchronously, checked once
+    every launch is queued): set from the host as a timed-out wait would leave it, the prefill
+    raises; the report clears it, and the next prefill is clean and equal to one before."""
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    lens, starts, ends, Ks = CASES["ragged3"]
+    shape, wts, head = _setup(cuda, seed=2)
+    g = torch.Generator().manual_seed(13)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    before = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
+    torch.cuda.synchronize()
+    ws = G._SEL_WS[(torch.device(cuda).index, torch.cuda.current_stream().cuda_stream)][0]
+    G._error_word(ws).fill_(2)
+    with pytest.raises(RuntimeError, match="error word 2"):
+        P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
+    assert int(G._error_word(ws).item()) == 0
+    after = P.prefill_batch(wts, head, ids, starts, ends, 1, Ks)
+    torch.cuda.synchronize()
+    assert torch.equal(after.first_tokens, before.first_tokens)
+    assert torch.equal(after.kept_positions, before.kept_positions)
+    assert torch.equal(after.logits, before.logits)
+
+
 @pytest.mark.parametrize("prune_below_gate,graphs", [(False, False), (True, False), (False, True)])
 def test_prefill_decode_headroom_layout(cuda, prune_below_gate, graphs):
     """decode_headroom lays every cache out with free rows after each sequence: the same bits as

@@ -51,12 +51,60 @@ def _both(q, k, v, b, scale, causal):
 
 def test_noalloc_matches_workspace_entry_point(cuda):
     # (B, Sq, Sk, H, Hkv, causal): a few rows over long caches, then one decode row over a shorter one
-    for i, (B, Sq, Sk, H, Hkv, causal) in enumerate([(2, 3, 9000, 16, 8, True), (1, 1, 3000, 16, 8, True)]):
+    # then grids of more than half the resident slots (a few thousand rows over a long cache, and a
+    # non-causal one), whose split plans once needed more than the static scratch
+    shapes = [(2, 3, 9000, 16, 8, True), (1, 1, 3000, 16, 8, True), (1, 3072, 32768, 16, 8, True),
+              (1, 3000, 32768, 16, 8, True), (1, 3072, 4096, 16, 8, False)]
+    for i, (B, Sq, Sk, H, Hkv, causal) in enumerate(shapes):
         print(f"[noalloc] call {i}: B{B} Sq{Sq} Sk{Sk} H{H}/{Hkv}", flush=True)
         q, k, v, b, scale = _inputs(B, Sq, Sk, H, Hkv, 40 + i, cuda)
         n, (o1, l1), (o2, l2) = _both(q, k, v, b, scale, causal)
         assert n > 0, "this launch is meant to use the key-range split (and so the scratch)"
         assert torch.equal(o1, o2) and torch.equal(l1, l2), f"call {i}: noalloc differs from tg_keybias_fwd"
+
+
+_CAPTURE_SCRIPT = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+import tests.test_zz_no_alloc as T
+from tokengate_amd import _lib
+dev = torch.device("cuda:0")
+B, Sq, Sk, H, Hkv = 1, 5, 9000, 16, 8
+q, k, v, b, scale = T._inputs(B, Sq, Sk, H, Hkv, 90, dev)
+o = torch.empty_like(q)
+l = torch.empty(B, H, Sq, dtype=torch.float32, device=dev)
+stream = torch.cuda.Stream()
+g = torch.cuda.CUDAGraph()
+torch.cuda.synchronize()
+# the first tg_keybias_fwd_noalloc call of this process (its scratch lookup) happens under capture
+with torch.cuda.graph(g, stream=stream):
+    _lib.call("tg_keybias_fwd_noalloc", *T._args(q, k, v, b, o, l), float(scale), 1,
+              torch.cuda.current_stream().cuda_stream)
+for rep in range(3):
+    q2, k2, v2, b2, _ = T._inputs(B, Sq, Sk, H, Hkv, 91 + rep, dev)
+    q.copy_(q2); k.copy_(k2); v.copy_(v2); b.copy_(b2)
+    g.replay()
+    torch.cuda.synchronize()
+    n, (o1, l1), _ = T._both(q, k, v, b, scale, True)
+    assert n > 0
+    ok = torch.equal(o, o1) and torch.equal(l, l1)
+    print(f"replay {rep}: bit-exact {ok}", flush=True)
+    assert ok, f"replay {rep} differs from tg_keybias_fwd"
+print("capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(cuda):
+    """In a fresh process, the first noalloc call (which looks up the device scratch) is made under
+    HIP graph capture; three replays over new inputs each equal tg_keybias_fwd bit for bit."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-u", "-c", _CAPTURE_SCRIPT, root], capture_output=True, text=True,
+                       timeout=300, cwd=root)
+    print(r.stdout[-2000:], r.stderr[-2000:])
+    assert r.returncode == 0 and "capture ok" in r.stdout
 
 
 def test_noalloc_unsplit_launch(cuda):

@@ -285,7 +285,18 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   for (int dblk = 0; dblk < 8; ++dblk) vch[dblk] = (v_lane + (uint32_t)(((2 * dblk) ^ vsw) << 4)) & 0x1FF8u;
 
   f32x4 oacc[2][8];
-  float mrun[2] = {-INFINITY, -INFINITY}, lrun[2] = {0.f, 0.f};
+  // Row sums on the matrix cores: lacc[cb] += ones(16x32) . P^T puts column c's sum of the step's
+  // bf16 P values (exactly the weights P V uses) in all four values of every lane of column c, so
+  // the softmax spends no VALU on it and needs no cross-lane sum at the end.
+  f32x4 lacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+  bf16x8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = (__bf16)1.0f;
+  // Per column block: the running max mrun (log2 units), -mrun as the exponent offset (0 before the
+  // first visible key), and the tile max in raw-score units above which mrun is raised; all three
+  // change only when the running max is raised.
+  float mrun[2] = {-INFINITY, -INFINITY}, mneg[2] = {0.f, 0.f}, thr[2] = {-INFINITY, -INFINITY};
+  const float inv_scale_log2 = 1.f / a.scale_log2;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -360,46 +371,58 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
         }
       }
     }
-    float mx[2];
+    float mt[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const f32x4 *s = sacc[cb];
       const float m0 = vmax3(s[0][0], s[0][1], s[0][2]), m1 = vmax3(s[0][3], s[1][0], s[1][1]);
       const float m2 = vmax3(s[1][2], s[1][3], s[2][0]), m3 = vmax3(s[2][1], s[2][2], s[2][3]);
       const float m4 = vmax3(s[3][0], s[3][1], s[3][2]);
-      const float m = vmax3(vmax3(m0, m1, m2), vmax3(m3, m4, s[3][3]), m0);
-      mx[cb] = quad_swap_max(m) * a.scale_log2;   // tile max in log2 units (-inf if fully masked)
+      mt[cb] = vmax3(vmax3(m0, m1, m2), vmax3(m3, m4, s[3][3]), m0);
     }
-    if (__builtin_amdgcn_ballot_w64(mx[0] > mrun[0] + kRescaleTau || mx[1] > mrun[1] + kRescaleTau) != 0) {
+    // Both column blocks' maxima over the four lane groups in three permlane swaps:
+    // swap16(cb0, cb1) + max leaves cb0's pair maxima (groups 0|1, 2|3) in groups 0 and 2 and cb1's
+    // in groups 1 and 3; swap32 + max folds the halves; a last swap16 of that value with itself
+    // returns (cb0's max in every lane, cb1's max in every lane).  Raw-score units, -inf if the
+    // tile is fully masked for the column.
+    float mxr[2];
+    {
+      const float x = swap_pair_max(__builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, mt[0]),
+                                                                     __builtin_bit_cast(uint32_t, mt[1]), false, false));
+      const float y = half_swap_max(x);
+      const auto sw = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, y), __builtin_bit_cast(uint32_t, y),
+                                                       false, false);
+      const uint32_t lo = sw[0], hi = sw[1];
+      mxr[0] = u32_as_f32(lo);
+      mxr[1] = u32_as_f32(hi);
+    }
+    if (__builtin_amdgcn_ballot_w64(mxr[0] > thr[0] || mxr[1] > thr[1]) != 0) {
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
-        const float m_new = fmaxf(mrun[cb], mx[cb]);
+        const float m_new = fmaxf(mrun[cb], mxr[cb] * a.scale_log2);
         // 0 on the first visible tile; columns that have seen no key yet (m_new = -inf) keep 1.
         const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(mrun[cb] - m_new);
         mrun[cb] = m_new;
-        lrun[cb] *= alpha;
+        mneg[cb] = m_new == -INFINITY ? 0.f : -m_new;
+        thr[cb] = (m_new + kRescaleTau) * inv_scale_log2;
+        lacc[cb] *= alpha;
 #pragma unroll
         for (int d = 0; d < 8; ++d) oacc[cb][d] *= alpha;
       }
     }
-    // P rounded to bf16 pairs; the row sum adds those same bf16 values (v_dot2 with 1.0, one
-    // instruction per pair), i.e. exactly the weights the P V product uses.
+    // P rounded to bf16 pairs (the B operand of P V and of the row-sum product)
     uint32_t pk[2][4][2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      const float mneg = mrun[cb] == -INFINITY ? 0.f : -mrun[cb];
-      float ps[2] = {0.f, 0.f};
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
-          const float p0 = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, mneg));
-          const float p1 = fast_exp2(fmaf(sacc[cb][kb][i + 1], a.scale_log2, mneg));
+          const float p0 = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, mneg[cb]));
+          const float p1 = fast_exp2(fmaf(sacc[cb][kb][i + 1], a.scale_log2, mneg[cb]));
           pk[cb][kb][i >> 1] = pack_bf16x2(p0, p1);
-          ps[kb & 1] = sum_bf16x2(pk[cb][kb][i >> 1], ps[kb & 1]);
         }
       }
-      lrun[cb] += ps[0] + ps[1];
     }
 
     // ---- O^T += V^T P^T: 2 key steps x 8 d-blocks x 2 column blocks ----
@@ -411,6 +434,8 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
         const u32x4 w = {pk[cb][2 * st][0], pk[cb][2 * st][1], pk[cb][2 * st + 1][0], pk[cb][2 * st + 1][1]};
         pb[cb] = __builtin_bit_cast(bf16x8, w);
       }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) lacc[cb] = mfma16(ones, pb[cb], lacc[cb]);
       const uint32_t krow = (uint32_t)(32 * st * kKRowBytes);
 #pragma unroll
       for (int dblk = 0; dblk < 8; ++dblk) {
@@ -434,7 +459,7 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
   float l[2], inv[2];
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
-    l[cb] = quad_sum(lrun[cb]);
+    l[cb] = lacc[cb][0];
     inv[cb] = l[cb] > 0.f ? 1.f / l[cb] : 0.f;
   }
   if (chunk >= 0) {
@@ -674,7 +699,13 @@ SplitPlan plan_split(int nw, int hp, int n_qtiles, int64_t units, int sq, int sk
   if (ns < 2) return p;
   int n_heavy = 0;
   for (int qt = n_qtiles - 1; qt >= 0 && (int64_t)tiles(qt) * ns > tmax; --qt) ++n_heavy;
-  if (n_heavy == 0) return p;
+  // The split grid (nblocks + heavy_units * (ns - 1) workgroups) must fit the resident slots: past
+  // that, extra chunks only queue behind the others.  ns <= slots / nblocks already ensures it
+  // unless ns was raised to 2 for a grid of more than half the slots; then only the heaviest tiles
+  // that fit are split.  Hence heavy_units * ns <= slots, and the partials take at most
+  // CUs x 8 waves x 64 lanes x kPartialBytesPerLane bytes.
+  n_heavy = (int)std::min<int64_t>(n_heavy, (slots - nblocks) / ((int64_t)(ns - 1) * units));
+  if (n_heavy <= 0) return p;
   p.ns = ns;
   p.n_heavy = n_heavy;
   p.heavy_units = (int64_t)n_heavy * units;
@@ -784,11 +815,11 @@ int64_t fwd_workspace_size(int32_t units_batch, int32_t seqlen_q, int32_t seqlen
   return plan_split(nw, hp, nq, units, seqlen_q, seqlen_k, causal != 0).bytes;
 }
 
-// Device scratch of tg_keybias_fwd_noalloc: the key-range split's partial results.  A split is
-// planned only for grids that leave a quarter of the resident-workgroup slots empty, and its
-// chunks fill at most every slot, so it needs at most CUs x 8 waves x 64 lanes x 144 B
-// (18 MiB on a 256-CU MI355X); 24 MiB covers devices of up to 341 CUs.  One copy per device,
-// held until the process ends; every call on a device shares it.
+// Device scratch of tg_keybias_fwd_noalloc: the key-range split's partial results.  plan_split
+// keeps the split chunks within the resident-workgroup slots (heavy units x ns <= slots), so a
+// split needs at most CUs x 8 waves x 64 lanes x 144 B (18 MiB on a 256-CU MI355X); 24 MiB
+// covers devices of up to 341 CUs.  One copy per device, held until the process ends; every call
+// on a device shares it.
 constexpr int64_t kScratchBytes = 24ll << 20;
 static __device__ __align__(256) char scratch[kScratchBytes];
 

@@ -772,7 +772,9 @@ struct PackArgs {
   const float *sumsq;     // optional: per-sequence article sum of squares -> RMS normalisation
   float eps;
   float *bias_out;        // optional: gate bias of kept rows (0 on prefix / suffix rows)
+  uint32_t *err;          // optional: set to kPackBadPosition when a kept position lies outside its sequence
 };
+constexpr uint32_t kPackBadPosition = 3u;
 
 // ROWS kept rows per workgroup: 4 for large packs, 1 when there are too few rows to give every CU
 // several workgroups (small K: the copy is latency-bound and wants as many rows in flight as possible)
@@ -796,7 +798,14 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
       }
       sb = lo;
       pos = a.keep[j];
-      srow = (int64_t)a.geom[6 * lo] + pos;
+      // a position outside its sequence (a keep list that was never written) gathers nothing: the
+      // row is skipped and the error word raised, instead of reading another sequence's rows or
+      // past the source
+      if (pos >= 0 && pos < (int64_t)a.geom[6 * lo + 1]) {
+        srow = (int64_t)a.geom[6 * lo] + pos;
+      } else if (a.err) {
+        __hip_atomic_store(a.err, kPackBadPosition, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
     src_row[tid] = srow;
     s_pos[tid] = pos;
@@ -924,11 +933,11 @@ extern "C" int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32
   return 0;
 }
 
-extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep,
-                            const int32_t *geom, int32_t num_seqs, int64_t total_kept, int64_t *positions_out,
-                            const float *bias_src, const float *sumsq, float rms_eps, float *bias_out,
-                            hipStream_t stream) {
-  clear_error();
+namespace tg {
+// The pack behind tg_gate_pack and tg_gate_select_pack (err: the selection's error word, or NULL).
+int gate_pack_launch(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep, const int32_t *geom,
+                     int32_t num_seqs, int64_t total_kept, int64_t *positions_out, const float *bias_src,
+                     const float *sumsq, float rms_eps, float *bias_out, uint32_t *err, hipStream_t stream) {
   TG_CHECK(n_streams >= 0 && n_streams <= kMaxStreams, "at most %d streams", kMaxStreams);
   TG_CHECK(n_streams == 0 || streams != nullptr, "null streams");
   TG_CHECK(keep && geom, "null pointer");
@@ -957,6 +966,7 @@ extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, co
   a.sumsq = sumsq;
   a.eps = rms_eps;
   a.bias_out = bias_out;
+  a.err = err;
   TG_CHECK(total_kept < (1ll << 31), "grid too large");
   if (total_kept < 16 * 256)
     hipLaunchKernelGGL(gate_pack_kernel<1>, dim3((unsigned)total_kept), dim3(kPThreads), 0, stream, a);
@@ -964,4 +974,14 @@ extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, co
     hipLaunchKernelGGL(gate_pack_kernel<4>, dim3((unsigned)((total_kept + 3) / 4)), dim3(kPThreads), 0, stream, a);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
+}
+}  // namespace tg
+
+extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep,
+                            const int32_t *geom, int32_t num_seqs, int64_t total_kept, int64_t *positions_out,
+                            const float *bias_src, const float *sumsq, float rms_eps, float *bias_out,
+                            hipStream_t stream) {
+  clear_error();
+  return gate_pack_launch(streams, n_streams, keep, geom, num_seqs, total_kept, positions_out, bias_src, sumsq,
+                          rms_eps, bias_out, nullptr, stream);
 }

@@ -37,6 +37,11 @@
 #include "../../include/tokengate_hip.h"
 
 namespace tg {
+// gate.hip: the row gather, here with this workspace's error word (a kept position outside its
+// sequence, i.e. a keep list left unwritten after a failed wait, is skipped and reported)
+int gate_pack_launch(const tg_pack_stream *streams, int32_t n_streams, const int64_t *keep, const int32_t *geom,
+                     int32_t num_seqs, int64_t total_kept, int64_t *positions_out, const float *bias_src,
+                     const float *sumsq, float rms_eps, float *bias_out, uint32_t *err, hipStream_t stream);
 namespace {
 
 constexpr int kQThreads = 512;
@@ -625,7 +630,7 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   TG_HIP_CHECK(hipPeekAtLastError());
   // the rows themselves: the pack over the keep lists just written (positions and bias are done)
   if (n_streams > 0)
-    return tg_gate_pack(streams, n_streams, keep, geom, num_seqs, total_kept, nullptr, nullptr, nullptr, rms_eps,
-                        nullptr, stream);
+    return gate_pack_launch(streams, n_streams, keep, geom, num_seqs, total_kept, nullptr, nullptr, nullptr, rms_eps,
+                            nullptr, a.glob + GL_ERROR, stream);
   return 0;
 }

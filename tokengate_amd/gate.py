@@ -147,12 +147,16 @@ def _sel_workspace(device, stream: int, nseq: int, n_chunks: int):
 def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple] = (),
                 positions: Optional[torch.Tensor] = None, bias_out: Optional[torch.Tensor] = None,
                 keep_out: Optional[torch.Tensor] = None, rms_eps: float = RMS_EPS,
-                check: bool = False) -> torch.Tensor:
+                check: bool = False, error_out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """select_keep and pack with the keep lists selected by many workgroups per state span
     (tg_gate_select_pack): the keep lists of every sequence (returned, int64, packed), the rows of
     every (src, dst) pair gathered at them, the kept positions and the kept rows' RMS-normalised
     gate bias.  Spans beyond its limits (more than 64 x 16384 scores) run select_keep then pack.
-    check: read back the wait-timeout flag (a host synchronisation) and raise if it is set."""
+    The launches' error word (a failed look-back wait, an overrun count, or a kept position outside
+    its sequence) stays set in the stream's workspace until reported:
+    check: read it back (a host synchronisation), and if set clear it and raise;
+    error_out: a (1,) int32 pinned host tensor that receives it by an asynchronous copy after the
+    launches (0 when these launches use no workspace); see raise_select_error."""
     if scores.dtype != torch.float32 or scores.dim() != 1 or not scores.is_contiguous():
         raise RuntimeError("scores must be a contiguous 1-D float32 tensor")
     keep = keep_out if keep_out is not None else torch.empty(p.total_kept, dtype=torch.int64, device=scores.device)
@@ -164,6 +168,10 @@ def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple] = (),
         if t is not None and (t.dtype != dt or not t.is_contiguous()):
             raise RuntimeError("select_pack: positions must be contiguous int64, bias_out contiguous float32")
     arr = _streams(pairs, p)
+    if error_out is not None:
+        if error_out.dtype != torch.int32 or error_out.device.type != "cpu" or error_out.numel() != 1:
+            raise RuntimeError("select_pack: error_out must be a (1,) int32 host tensor")
+        error_out.zero_()
     if p.total_kept == 0:
         return keep
     if not p.sel_kpt:
@@ -179,11 +187,34 @@ def select_pack(scores: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple] = (),
               positions.data_ptr() if positions is not None else None,
               bias_out.data_ptr() if bias_out is not None else None, float(rms_eps), ws.data_ptr(), seq_cap, chunk_cap,
               stream)
+    flag = _error_word(ws)
+    if error_out is not None:
+        error_out.copy_(flag, non_blocking=True)
     if check:
-        off = _lib.SELECT_PACK_ERROR_OFFSET
-        if int(ws[off:off + 4].view(torch.int32).item()):
-            raise RuntimeError("tg_gate_select_pack: error flag set (a wait timed out or a count was inconsistent)")
+        raise_select_error(int(flag.item()), scores.device, stream)
     return keep
+
+
+_SELECT_ERRORS = {1: "a look-back wait timed out", 2: "a chunk's kept count overran its sequence",
+                  3: "the gather met a kept position outside its sequence"}
+
+
+def _error_word(ws: torch.Tensor) -> torch.Tensor:
+    off = _lib.SELECT_PACK_ERROR_OFFSET
+    return ws[off:off + 4].view(torch.int32)
+
+
+def raise_select_error(code: int, device, stream: int) -> None:
+    """If `code` (the error word select_pack reported) is nonzero, clear the word in the workspace of
+    (device, stream), so that the next call starts clean, and raise RuntimeError: the keep lists and
+    packed rows of the calls since it was last cleared are not valid."""
+    if not code:
+        return
+    ent = _SEL_WS.get((torch.device(device).index, stream))
+    if ent is not None:
+        _error_word(ent[0]).zero_()
+    raise RuntimeError(f"tg_gate_select_pack: error word {code} "
+                       f"({_SELECT_ERRORS.get(code, 'unknown')}); the keep lists are not valid")
 
 
 def _streams(pairs, p: KeepPlan):

@@ -176,7 +176,9 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     from captured graphs (captured on first use per geometry); the Phase-2 KV caches are then views
     of the graph's buffers, valid until its next replay.  decode_headroom: every layer's KV cache
     is laid out with that many free rows after each sequence (written there by the prefill's own
-    launches and the pack), so that decode appends in place."""
+    launches and the pack), so that decode appends in place.  Raises RuntimeError (after queueing
+    every launch, when the selection's launches have finished) if the keep-list selection reported
+    an error: the result would be built on invalid keep lists."""
     shape = wts.shape
     dev = wts.device
     B = len(ids_list)
@@ -238,7 +240,13 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
             nk = alloc_kv(shape, T2 + B_ * gap, dev)
             pairs += [(kv[i].k, nk.k, gap), (kv[i].v, nk.v, gap)]
             kv[i] = nk
-    keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias)
+    # the selection's error word comes back with an asynchronous copy; it is checked once every
+    # launch of the prefill is queued (the GPU then never waits for the host)
+    err_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias, error_out=err_host)
+    err_ev = torch.cuda.Event()
+    err_ev.record()
+    sel_stream = torch.cuda.current_stream().cuda_stream
     if cap is not None:
         cap["h1"] = h
     del h, ws1, pairs
@@ -288,6 +296,8 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     logits = logits_last(wts, h2, last)
     first = argmax_rows(logits)
     mark("end")
+    err_ev.synchronize()
+    G.raise_select_error(int(err_host[0]), dev, sel_stream)
     phase_ms = {}
     if ev is not None:
         torch.cuda.synchronize()
