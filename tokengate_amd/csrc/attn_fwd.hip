@@ -24,7 +24,8 @@
 //     then directly the B operand of O^T = V^T P^T, whose A operand (8 consecutive keys at one d
 //     per lane) comes from row-major V through the transposing LDS read ds_read_b64_tr_b16;
 //   * O^T accumulates per lane for one column per block, so the per-query rescale is a scalar per
-//     lane, and it is applied lazily (only when the running max grows by more than 2^8);
+//     lane, and it is applied lazily (only when the running max grows by more than 2^8); the row
+//     sums run on the matrix cores too (ones . P^T, the same bf16 weights P V uses);
 //   * two waves per SIMD let one wave's softmax (VALU) run under the other's matrix-core work;
 //     all NW waves share every K/V tile and each issues 1/NW of its LDS DMA.
 // Workgroups are issued heaviest-first (largest query tile first) with the KV head varying
@@ -261,10 +262,13 @@ __global__ __launch_bounds__(64 * NW, 8 / NW) void keybias_fwd_kernel(FwdArgs a)
     const uint32_t kb0 = (uint32_t)((int64_t)tile * kBN * a.k_rs * 2);
     const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
     char *kd = kslot(buf_c), *vd = vslot(buf_c);
+    // the LDS destination goes to M0: with the wave index in a scalar register it is scalar
+    // arithmetic instead of a per-lane add and a readfirstlane per DMA (+0.5 % at 32k)
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int it = 0; it < kLoads; ++it) {
-      dma16(krs, kd + (wave + it * kWaves) * 1024, kb0 + koff[it]);
-      dma16(vrs, vd + (wave + it * kWaves) * 1024, vb0 + voff[it]);
+      dma16(krs, kd + (wv + it * kWaves) * 1024, kb0 + koff[it]);
+      dma16(vrs, vd + (wv + it * kWaves) * 1024, vb0 + voff[it]);
     }
     if constexpr (HAS_BIAS) {
       if (wave < HP)
