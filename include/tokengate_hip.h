@@ -253,6 +253,25 @@ int tg_gate_select_pack(const float *scores, const int32_t *geom, const int32_t 
 /* Workspace bytes of tg_gate_select_pack for these capacities. */
 int64_t tg_gate_select_pack_workspace_size(int32_t seq_capacity, int32_t chunk_capacity);
 
+/* Threshold selection (_select_threshold with aggregate, gate_forward.py:102-143,
+ * e2e_gate_module.py:387-399: keep the state tokens with sigmoid(agg) >= tau, or the single argmax
+ * when none passes; the kept count is sample-dependent).  For the state span of every sequence
+ * (geom as for tg_gate_select_pack; its k_clamped / kept_start columns are ignored), with
+ * raw = scores[row_start + art_start + j]: inv = fp32(1 / sqrt(fp32(m + rms_eps))), m the span's
+ * mean of raw^2 rounded once to fp32; bn = fp32(gain * fp32(raw * inv)); agg = the sum over h in
+ * order of fp32(fp32(bn * head_scale[h]) * fp32(1 / n_heads)) (bn * head_scale[0] for one head),
+ * every operation a separately rounded fp32 one; head_scale (n_heads <= 64 floats, HOST memory) is
+ * softplus(gate_scale) of the first Phase-2 layer.  A token passes when agg >= b_star (the exact
+ * fp32 form of sigmoid(agg) >= tau: the least fp32 value whose sigmoid reaches tau; NaN to pass
+ * nothing); NaN never passes.  Outputs, at the span's rows of the packed row layout: agg_out and
+ * select_out (rows fp32) with select = passing ? 1 : 0 when the sequence has a passing token, else
+ * agg; counts[b] = passing tokens (int32); sumsq[b] (optional) = the span's sum of squares.  Top-K
+ * of select_out with K_b = max(counts[b], 1) (tg_gate_select_pack) is then exactly the reference's
+ * selection. */
+int tg_gate_threshold_select(const float *scores, const int32_t *geom, int32_t num_seqs, const float *head_scale,
+                             int32_t n_heads, float gain, float rms_eps, float b_star, float *agg_out,
+                             float *select_out, int32_t *counts, float *sumsq, hipStream_t stream);
+
 /* ---- decoder ops of the gated prefill (Qwen3 layer, transformers 5.x modeling_qwen3.py) ------
  * Called by this library's prefill around the attention; the reference runs them as eager torch
  * modules inside each decoder layer (qwen3_flex_attention.py:533-544 for q/k norm + RoPE). */

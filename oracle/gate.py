@@ -18,7 +18,9 @@ rounding points (the model runs in bf16, the gate's parameters are fp32):
     in fp32: transformers' Qwen3RMSNorm(1, eps) over the sequence axis (E2EGate._seq_rms_norm_qwen,
     e2e_gate_module.py:299, :342-344, forward :363-385); raw is the branch's bf16 score in fp32
     (gate_forward.py:1399-1405)
-  * selection key agg_j = sum_h b[j, 0, h] * (1/H) (aggregate :387-399)
+  * selection key agg_j = sum_h b[j, 0, h] * (1/H) (aggregate :387-399); the threshold mode keeps
+    the tokens with sigmoid(agg_j) >= tau, or the argmax when none passes (_select_threshold,
+    gate_forward.py:102-125)
   * stored bias gb = bf16(b) on kept article rows, 0 on prefix / suffix rows
     (build_gate_bias_vectorized, per_layer_gate branch, gate_forward.py:995-1008; model dtype
     :1450, :1462-1466)
@@ -165,6 +167,40 @@ def phase2_query(q, s):
 def decode_query_scale(temp, r):
     """The decode token's query multiplier bf16(fp32(gamma_h * r)) (H,) (FormDecodeState.step)."""
     return bf16((np.asarray(temp, dtype=np.float32) * np.float32(r)).astype(np.float32))
+
+
+def selection_values(scores_art, gate_scale, eps=RMS_EPS, gain=1.0):
+    """The selection value agg_j of every state token (aggregate of E2EGate.forward's bias,
+    e2e_gate_module.py:363-399): the value _select_indices compares (gate_forward.py:1411-1412)."""
+    return aggregate(gate_bias_layers(scores_art, gate_scale, eps, gain))
+
+
+def argmax_first(x):
+    """torch.argmax of a 1-D float tensor: the first maximal entry, a NaN counting as maximal."""
+    x = np.asarray(x, dtype=np.float32)
+    nan = np.isnan(x)
+    if nan.any():
+        return int(np.argmax(nan))
+    return int(np.argmax(x))
+
+
+def select_threshold(agg, b_star):
+    """_select_threshold (gate_forward.py:102-125): article-relative indices, ascending, of the
+    tokens with sigmoid(agg) >= tau, written as agg >= b_star (b_star: the least fp32 value whose
+    sigmoid reaches tau; NaN when none does, -inf when all do); NaN never passes; when nothing
+    passes, the single argmax."""
+    agg = np.asarray(agg, dtype=np.float32)
+    with np.errstate(invalid="ignore"):
+        idx = np.nonzero(agg >= np.float32(b_star))[0]
+    if len(idx) == 0 and len(agg) > 0:
+        return np.array([argmax_first(agg)], dtype=np.int64)
+    return idx.astype(np.int64)
+
+
+def threshold_keep_indices(agg, b_star, art_start, art_end, seq_len):
+    """keep = [0, s) + s + select_threshold + [e, seq_len) (gate_forward.py:1412-1421)."""
+    sel = select_threshold(agg, b_star)
+    return np.concatenate([np.arange(art_start), art_start + sel, np.arange(art_end, seq_len)]).astype(np.int64)
 
 
 def select_and_pack(scores, seqs):

@@ -78,13 +78,29 @@ def test_load_gate_holds_bf16_images(tmp_path):
 @pytest.mark.parametrize("over,match", [
     (dict(readout_residual=True), "readout_residual"), (dict(absorbed_readout=False), "absorbed_readout"),
     (dict(tanh_gate=True), "tanh_gate"), (dict(head_agg="learned"), "head_agg"),
-    (dict(gate_cond="film"), "gate_cond"), (dict(selection_mode="threshold"), "selection_mode"),
+    (dict(gate_cond="film"), "gate_cond"), (dict(selection_mode="adaptive"), "selection_mode"),
 ])
 def test_load_gate_rejects_variants(tmp_path, over, match):
     p = str(tmp_path / "gate_final.pt")
     torch.save(_gate_obj(**over), p)
     with pytest.raises(ValueError, match=match):
         C.load_gate(p, device="cpu")
+
+
+def test_load_gate_selection_mode(tmp_path):
+    """selection_mode / tau are restored as E2EGate keeps them (load_gate, e2e_gate_module.py:482-488):
+    top-K by default, the threshold mode with its tau."""
+    p = str(tmp_path / "gate_final.pt")
+    torch.save(_gate_obj(), p)
+    head, _ = C.load_gate(p, device="cpu")
+    assert head.selection_mode == "topk"
+    torch.save(_gate_obj(selection_mode="threshold", tau=0.625), p)
+    head, _ = C.load_gate(p, device="cpu")
+    assert head.selection_mode == "threshold" and head.tau == 0.625
+    obj = _gate_obj(selection_mode="threshold")
+    del obj["tau"]
+    torch.save(obj, p)
+    assert C.load_gate(p, device="cpu")[0].tau == 0.5
 
 
 def test_load_gate_rejects_missing_branch_and_post_proj(tmp_path):

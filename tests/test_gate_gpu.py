@@ -477,3 +477,85 @@ def test_select_pack_error_word_round_trip(cuda):
     keep2 = gate.select_pack(scores, p, [], check=True, error_out=err)
     torch.cuda.synchronize()
     assert int(err[0]) == 0 and np.array_equal(keep2.cpu().numpy(), ref)
+
+
+def _threshold_batch(rng):
+    """A ragged batch for the threshold mode: (scores, seqs) with seqs (row_start, len, s, e)."""
+    parts, seqs, r0 = [], [], 0
+    specs = [(3000, 64, 2744, "normal"), (5000, 0, 5000, "bf16"), (900, 10, 890, "zeros"), (1200, 100, 1100, "nan"),
+             (700, 700, 700, "empty"), (70000, 64, 69744, "normal"), (2500, 5, 2495, "few"), (40, 3, 37, "normal")]
+    for L, s, e, kind in specs:
+        x = rng.standard_normal(L).astype(np.float32)
+        if kind == "bf16":
+            x = og.bf16(x)
+        elif kind == "zeros":
+            x[:] = 0.0
+        elif kind == "nan":
+            x[s + 17] = np.nan
+        elif kind == "few":
+            x = np.round(x * 2).astype(np.float32) / 2
+        parts.append(x)
+        seqs.append((r0, L, s, e))
+        r0 += L
+    return np.concatenate(parts), seqs
+
+
+@pytest.mark.parametrize("tau", [0.5, 0.62, 0.4, 0.995])
+def test_threshold_selection_matches_oracle(cuda, tau):
+    """tg_gate_threshold_select + the top-K selection over its derived scores (gate.threshold_plan,
+    then select_pack and the bias pack): the selection values bit-exact against the oracle's fp32
+    chain (aggregate of the per-head bias), kept counts, keep lists bit-exact against the oracle's
+    _select_threshold restatement (non-strict sigmoid(agg) >= tau; the argmax when nothing passes;
+    NaN never passes), packed rows against index_select, kept positions and gate bias.  The batch
+    holds the init case (every score 0: everything kept at tau 0.5), a span with a NaN (all of its
+    values NaN: the argmax fallback takes the first), ties, an empty span and a 70k span."""
+    from tokengate_amd import gate
+    rng = np.random.default_rng(21)
+    scores_np, seqs = _threshold_batch(rng)
+    g = torch.Generator(device=cuda).manual_seed(3)
+    head = gate.random_head(3, 16, seed=7, device=cuda)
+    head.gate_scale = head.gate_scale + 0.5 * torch.randn(head.gate_scale.shape, generator=g, device=cuda)
+    head.selection_mode, head.tau, head.bias_gain = "threshold", tau, 1.25
+    scores = torch.from_numpy(scores_np).to(cuda)
+    rs, lens, ss, es = ([x[i] for x in seqs] for i in range(4))
+    p, sel, agg, sumsq, counts = gate.threshold_plan(scores, rs, lens, ss, es, head, cuda)
+    b_star = gate.sigmoid_threshold(tau, cuda)
+    # b_star is the device torch.sigmoid's own boundary: the two predicates agree around it
+    if np.isfinite(b_star):
+        u = int(np.float32(b_star).view(np.uint32))
+        key = ((~u) & 0xFFFFFFFF) if u & 0x80000000 else (u | 0x80000000)
+        near = torch.from_numpy(gate._f32_of_keys(key + np.arange(-512, 513)).copy()).to(cuda)
+        assert torch.equal(torch.sigmoid(near) >= tau, near >= b_star)
+    sp = np.asarray(head.selection_head_scale(), np.float32)
+    gs = head.gate_scale.float().cpu().numpy()
+    assert np.array_equal(sp, og.softplus32(gs[0])) or np.abs(sp - og.softplus32(gs[0])).max() <= 1.2e-7
+    agg_np = agg.cpu().numpy()
+    src = torch.arange(len(scores_np) * 8, dtype=torch.int32, device=cuda).view(-1, 8)
+    dst = torch.full((p.total_kept, 8), -1, dtype=torch.int32, device=cuda)
+    pos = torch.full((p.total_kept,), -7, dtype=torch.int64, device=cuda)
+    bias = torch.full((p.total_kept,), float("nan"), dtype=torch.float32, device=cuda)
+    keep = gate.select_pack(sel, p, [(src, dst)], positions=pos, check=True)
+    gate.pack(keep, p, [], bias_src=scores, sumsq=sumsq, bias_out=bias)
+    torch.cuda.synchronize()
+    keep_np, pos_np, bias_np, dst_np = keep.cpu().numpy(), pos.cpu().numpy(), bias.cpu().numpy(), dst.cpu().numpy()
+    src_np = src.cpu().numpy()
+    for b, (r0, L, s, e) in enumerate(seqs):
+        raw = scores_np[r0 + s:r0 + e]
+        # the oracle's chain (gate_bias_layers then aggregate) with the product's softplus values
+        b0 = (og.seq_rms_norm(raw, gain=1.25)[:, None] * sp[None, :]).astype(np.float32)[:, None, :]
+        want_agg = og.aggregate(b0)
+        got_agg = agg_np[r0 + s:r0 + e]
+        assert np.array_equal(got_agg, want_agg, equal_nan=True), f"seq {b}: selection values differ"
+        with np.errstate(invalid="ignore"):
+            assert counts[b] == int(np.sum(want_agg >= np.float32(b_star))), f"seq {b}: count"
+        want = og.threshold_keep_indices(want_agg, b_star, s, e, L)
+        c0, c1 = p.cu_kept[b], p.cu_kept[b + 1]
+        assert np.array_equal(keep_np[c0:c1], want), f"seq {b}: keep list differs (tau {tau})"
+        assert np.array_equal(pos_np[c0:c1], want)
+        assert np.array_equal(dst_np[c0:c1], src_np[r0 + want])
+        if np.isfinite(raw).all():
+            np.testing.assert_allclose(bias_np[c0:c1], og.gate_bias(raw, want, s, e), rtol=2e-6, atol=1e-30)
+    if tau == 0.5:
+        assert counts[2] == 900 - 20         # every score 0: the whole span passes
+    assert counts[4] == 0 and p.n_kept[4] == 700   # empty span: prefix and suffix only
+    assert counts[3] == 0                    # a NaN makes the span's values NaN: the argmax fallback

@@ -231,6 +231,45 @@ def test_prefill_prune_below_gate(cuda):
         assert torch.equal(pruned.kv[i].k, full.kv[i].k)
 
 
+@pytest.mark.parametrize("tau", [0.62, 0.999])
+def test_prefill_threshold_mode(cuda, tau):
+    """A gate in the threshold selection mode (E2EGate(selection_mode='threshold', tau)): each
+    prompt keeps the state tokens with sigmoid(agg) >= tau (tau 0.999: none, so the argmax alone),
+    K unused.  The keep lists equal the oracle's _select_threshold on the kernel's own scores, and
+    the rest of the prefill equals a top-K prefill with K = the kept counts (the same kept rows):
+    positions exactly, gate bias to float32 rounding, logits within the layer bound."""
+    from tokengate_amd import gate as G
+    from tokengate_amd import prefill as P
+    lens, starts, ends, Ks = CASES["ragged3"]
+    shape, wts, head = _setup(cuda, seed=3)
+    g = torch.Generator().manual_seed(14)
+    ids = [torch.randint(0, shape.vocab, (n,), generator=g).tolist() for n in lens]
+    head.selection_mode, head.tau = "threshold", tau
+    r = P.prefill_batch(wts, head, ids, starts, ends, 1, [1] * len(lens), capture=True)
+    torch.cuda.synchronize()
+    scores = r.capture["scores"].cpu().numpy()
+    b_star = G.sigmoid_threshold(tau, cuda)
+    sp = np.asarray(head.selection_head_scale(), np.float32)
+    n_art = []
+    for b in range(len(lens)):
+        raw = scores[r.cu_prompt[b] + starts[b]:r.cu_prompt[b] + ends[b]]
+        agg = og.aggregate((og.seq_rms_norm(raw)[:, None] * sp[None, :]).astype(np.float32)[:, None, :])
+        want = og.threshold_keep_indices(agg, b_star, starts[b], ends[b], lens[b])
+        got = r.kept_positions[r.cu_kept[b]:r.cu_kept[b + 1]].cpu().numpy()
+        assert np.array_equal(got, want), f"seq {b}: threshold keep list differs"
+        n_art.append(len(want) - starts[b] - (lens[b] - ends[b]))
+    if tau == 0.999:
+        assert n_art == [1, 1, 1]
+    else:
+        assert len(set(n_art)) > 1 and min(n_art) > 1
+    head.selection_mode = "topk"
+    t = P.prefill_batch(wts, head, ids, starts, ends, 1, n_art)
+    torch.cuda.synchronize()
+    assert torch.equal(t.kept_positions, r.kept_positions)
+    np.testing.assert_allclose(r.kept_bias.cpu().numpy(), t.kept_bias.cpu().numpy(), rtol=2e-6, atol=1e-30)
+    assert_close_grad("threshold vs top-K logits", to_np(r.logits.float()), to_np(t.logits.float()))
+
+
 def test_prefill_raises_on_selection_error(cuda):
     """The prefill reads the keep-list selection's error word back (asynchronously, checked once
     every launch is queued): set from the host as a timed-out wait would leave it, the prefill

@@ -45,6 +45,7 @@ SIGNATURES = {
     "tg_gate_pack": [vp, i32, vp, vp, i32, i64, vp, vp, vp, f32, vp, vp],
     "tg_gate_select_pack": [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, vp, vp, f32, vp, i32, i32, vp],
     "tg_gate_select_pack_workspace_size": [i32, i32],
+    "tg_gate_threshold_select": [vp, vp, i32, vp, i32, f32, f32, f32, vp, vp, vp, vp, vp],
     "tg_rmsnorm": [vp, i64, vp, i64, vp, i64, vp, vp, i64, i64, i32, f32, vp],
     "tg_qk_norm_rope": [vp, i64, vp, i64, i32, i32, i32, vp, vp, f32, vp, vp, vp, vp, i64, vp, i64, vp, i64, vp,
                         vp],

@@ -76,9 +76,9 @@ def load_gate(path: str, device="cuda") -> Tuple[G.BranchHead, Dict]:
     gc = obj.get("gate_cond", "none")
     if gc not in ("none", None) or obj.get("use_boundary_cond", False):
         raise ValueError(f"Checkpoint {path} uses removed gate_cond={gc!r}; only gate_cond='none' gates are supported")
-    if obj.get("selection_mode", "topk") != "topk":
-        raise ValueError(f"Checkpoint {path}: selection_mode={obj.get('selection_mode')!r}; only 'topk' "
-                         "(fixed K) selection is implemented")
+    mode = obj.get("selection_mode", "topk")
+    if mode not in ("topk", "threshold"):
+        raise ValueError(f"selection_mode must be 'topk' or 'threshold', got {mode!r}")
     sd = obj["state_dict"]
     if "post_proj.weight" in sd:
         raise ValueError(f"checkpoint {path!r} carries post_proj.weight (removed post-top-K projection)")
@@ -108,6 +108,9 @@ def load_gate(path: str, device="cuda") -> Tuple[G.BranchHead, Dict]:
     head = G.BranchHead(torch.cat([gp, up]).to(device=device, dtype=bf).contiguous(),
                         dp[0].to(device=device, dtype=bf).contiguous(), gs.to(device), at.to(device), True,
                         float(gain.reshape(-1)[0]) if gain is not None else 1.0)
+    # E2EGate(selection_mode=..., tau=...) as load_gate restores them (e2e_gate_module.py:482-488)
+    head.selection_mode = mode
+    head.tau = float(obj.get("tau", 0.5))
     return head, dict(obj.get("metadata", {}) or {})
 
 

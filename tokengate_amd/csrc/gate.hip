@@ -880,6 +880,83 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Threshold selection (the reference's _select_threshold, gate_forward.py:102-125, on the selection
+// value of aggregate, e2e_gate_module.py:387-399).  One workgroup per sequence:
+//   1. the state span's mean square in fp64, rounded once to fp32 (the correctly rounded mean),
+//      inv = fp32(1 / sqrt(fp32(mean + eps))) (fp64 square root and division, rounded once);
+//   2. agg_j = sum over heads, in head order, of fp32(fp32(bn_j * sp_h) * w) with
+//      bn_j = fp32(gain * fp32(raw_j * inv)), w = fp32(1 / H) (agg_j = bn_j * sp_0 when H = 1):
+//      every step a separately rounded fp32 operation, as the reference's tensor ops are;
+//      a token passes when agg_j >= b_star (the caller's exact fp32 form of sigmoid(agg_j) >= tau,
+//      NaN never passes); count = passing tokens;
+//   3. sel_j = passing ? 1 : 0 when count > 0, else agg_j: the top-count (top-1) selection over sel
+//      is then exactly the passing set (the argmax fallback, ties and NaN ranked as top-K ranks them).
+// ---------------------------------------------------------------------------------------------
+constexpr int kThThreads = 512;
+constexpr int kThMaxHeads = 64;
+
+struct ThArgs {
+  const float *scores;
+  const int32_t *geom;
+  float sp[kThMaxHeads];   // softplus(gate_scale[0, h]) of the first Phase-2 layer
+  int n_heads;
+  float gain, eps, b_star;
+  float *agg, *sel;
+  int32_t *counts;
+  float *sumsq;
+};
+
+__device__ __forceinline__ float th_agg(const ThArgs &a, float raw, float inv, float w) {
+  const float bn = __fmul_rn(a.gain, __fmul_rn(raw, inv));
+  if (a.n_heads == 1) return __fmul_rn(bn, a.sp[0]);
+  float acc = 0.f;
+  for (int h = 0; h < a.n_heads; ++h) acc = __fadd_rn(acc, __fmul_rn(__fmul_rn(bn, a.sp[h]), w));
+  return acc;
+}
+
+__global__ __launch_bounds__(kThThreads) void gate_threshold_kernel(ThArgs a) {
+  __shared__ double s_d[kThThreads / 64];
+  __shared__ int s_c[kThThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int *gm = a.geom + 6 * blockIdx.x;
+  const int64_t r0 = (int64_t)gm[0] + gm[2];
+  const int n = gm[3] - gm[2];
+  const float *x = a.scores + r0;
+  double ss = 0.0;
+  for (int i = tid; i < n; i += kThThreads) {
+    const double v = x[i];
+    ss += v * v;
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if (lane == 0) s_d[wv] = ss;
+  __syncthreads();
+  double tot = 0.0;
+  for (int w = 0; w < kThThreads / 64; ++w) tot += s_d[w];
+  const float mean = n > 0 ? (float)(tot / (double)n) : 0.f;
+  const float inv = (float)(1.0 / sqrt((double)__fadd_rn(mean, a.eps)));
+  const float w = (float)(1.0 / (double)a.n_heads);
+  int cnt = 0;
+  for (int i = tid; i < n; i += kThThreads) {
+    const float g = th_agg(a, x[i], inv, w);
+    a.agg[r0 + i] = g;
+    cnt += g >= a.b_star ? 1 : 0;
+  }
+  for (int o = 32; o > 0; o >>= 1) cnt += __shfl_xor(cnt, o);
+  if (lane == 0) s_c[wv] = cnt;
+  __syncthreads();
+  int count = 0;
+  for (int k = 0; k < kThThreads / 64; ++k) count += s_c[k];
+  for (int i = tid; i < n; i += kThThreads) {
+    const float g = th_agg(a, x[i], inv, w);
+    a.sel[r0 + i] = count > 0 ? (g >= a.b_star ? 1.f : 0.f) : g;
+  }
+  if (tid == 0) {
+    a.counts[blockIdx.x] = count;
+    if (a.sumsq) a.sumsq[blockIdx.x] = (float)tot;
+  }
+}
+
 }  // namespace
 }  // namespace tg
 
@@ -984,4 +1061,30 @@ extern "C" int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, co
   clear_error();
   return gate_pack_launch(streams, n_streams, keep, geom, num_seqs, total_kept, positions_out, bias_src, sumsq,
                           rms_eps, bias_out, nullptr, stream);
+}
+
+extern "C" int tg_gate_threshold_select(const float *scores, const int32_t *geom, int32_t num_seqs,
+                                        const float *head_scale, int32_t n_heads, float gain, float rms_eps,
+                                        float b_star, float *agg_out, float *select_out, int32_t *counts,
+                                        float *sumsq, hipStream_t stream) {
+  clear_error();
+  TG_CHECK(scores && geom && head_scale && agg_out && select_out && counts, "null pointer");
+  TG_CHECK(num_seqs >= 0, "negative size");
+  TG_CHECK(n_heads >= 1 && n_heads <= kThMaxHeads, "n_heads must be 1 .. %d (got %d)", kThMaxHeads, n_heads);
+  if (num_seqs == 0) return 0;
+  ThArgs a{};
+  a.scores = scores;
+  a.geom = geom;
+  for (int h = 0; h < n_heads; ++h) a.sp[h] = head_scale[h];
+  a.n_heads = n_heads;
+  a.gain = gain;
+  a.eps = rms_eps;
+  a.b_star = b_star;
+  a.agg = agg_out;
+  a.sel = select_out;
+  a.counts = counts;
+  a.sumsq = sumsq;
+  hipLaunchKernelGGL(gate_threshold_kernel, dim3(num_seqs), dim3(kThThreads), 0, stream, a);
+  TG_HIP_CHECK(hipPeekAtLastError());
+  return 0;
 }

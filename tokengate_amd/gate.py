@@ -9,12 +9,15 @@ gate bias (build_gate_bias_vectorized :968-1036) — on the gfx950 kernels of cs
 Differences from the reference, by design: kept rows of all sequences are packed back to back
 (cu_seqlens layout) rather than right-padded to the longest; score ties go to the lower position
 (torch.topk leaves the order unspecified).  The per-sequence Python loop of the reference becomes
-one launch per step for the whole batch.
+one launch per step for the whole batch.  The threshold selection mode (_select_threshold
+:102-125) runs as a count launch, one host synchronisation for the sample-dependent kept counts,
+then the same top-K selection over a derived score (threshold_plan).
 """
 import ctypes
 from dataclasses import dataclass
 from typing import ClassVar, List, Optional, Sequence, Tuple
 
+import numpy as np
 import torch
 
 from tokengate_amd import _lib
@@ -217,6 +220,77 @@ def raise_select_error(code: int, device, stream: int) -> None:
                        f"({_SELECT_ERRORS.get(code, 'unknown')}); the keep lists are not valid")
 
 
+_BSTAR: dict = {}
+
+
+def _f32_of_keys(keys: np.ndarray) -> np.ndarray:
+    """fp32 values of ordered keys (the order-preserving uint32 map of non-NaN floats)."""
+    k = keys.astype(np.uint64)
+    u = np.where(k >= 0x80000000, k - 0x80000000, (~k) & 0xFFFFFFFF).astype(np.uint32)
+    return u.view(np.float32)
+
+
+def sigmoid_threshold(tau: float, device) -> float:
+    """b_star: the least fp32 value x with torch.sigmoid(x) >= tau on `device` -- the exact form of
+    _select_threshold's `torch.sigmoid(b) >= tau` (gate_forward.py:102-125) that a kernel evaluates
+    without a transcendental: b >= b_star.  -inf when every non-NaN value passes, NaN when none does.
+    Found over the ordered fp32 values by grid refinement (65537 sigmoid evaluations per step, three
+    steps), which relies on torch.sigmoid being non-decreasing; cached per (tau, device)."""
+    dev = torch.device(device)
+    ck = (float(tau), dev.type, dev.index)
+    if ck in _BSTAR:
+        return _BSTAR[ck]
+
+    def passes(keys):
+        x = torch.from_numpy(_f32_of_keys(keys).copy()).to(dev)
+        return (torch.sigmoid(x) >= tau).cpu().numpy()
+
+    lo, hi = 0x007FFFFF, 0xFF800000          # the keys of -inf and +inf
+    if passes(np.array([lo]))[0]:
+        out = float("-inf")
+    elif not passes(np.array([hi]))[0]:
+        out = float("nan")
+    else:
+        while hi - lo > 1:                   # passes(lo) is False, passes(hi) is True
+            step = -(-(hi - lo) // 65536)
+            grid = np.minimum(lo + step * np.arange(65537, dtype=np.int64), hi)
+            j = int(np.argmax(passes(grid)))
+            lo, hi = int(grid[j - 1]), int(grid[j])
+        out = float(_f32_of_keys(np.array([hi]))[0])
+    _BSTAR[ck] = out
+    return out
+
+
+def threshold_plan(scores: torch.Tensor, row_starts: Sequence[int], seq_lens: Sequence[int],
+                   art_starts: Sequence[int], art_ends: Sequence[int], head, device,
+                   rms_eps: float = RMS_EPS):
+    """The threshold mode's selection (_select_threshold via _select_indices, gate_forward.py:102-143)
+    for a batch: tg_gate_threshold_select computes every state token's selection value agg
+    (aggregate of E2EGate.forward's bias, e2e_gate_module.py:363-399) and the per-sequence count of
+    tokens with sigmoid(agg) >= head.tau; one host synchronisation reads the counts.  Returns
+    (plan with K_b = max(count_b, 1) -- the argmax fallback when nothing passes --, sel: the scores
+    whose top-K_b are exactly the kept tokens, agg, sumsq (per sequence, for the kept rows' gate
+    bias), counts).  K is the reference's sample-dependent kept count; the caller's K is unused,
+    as in the reference."""
+    if scores.dtype != torch.float32 or scores.dim() != 1 or not scores.is_contiguous():
+        raise RuntimeError("scores must be a contiguous 1-D float32 tensor")
+    n = len(seq_lens)
+    p0 = plan(row_starts, seq_lens, art_starts, art_ends, [1] * n, device)
+    hs = head.selection_head_scale()
+    b_star = sigmoid_threshold(float(head.tau), scores.device)
+    agg = torch.empty_like(scores)
+    sel = torch.empty_like(scores)
+    counts = torch.empty(n, dtype=torch.int32, device=scores.device)
+    sumsq = torch.empty(n, dtype=torch.float32, device=scores.device)
+    hs_arr = (ctypes.c_float * len(hs))(*hs)
+    _lib.call("tg_gate_threshold_select", scores.data_ptr(), p0.geom.data_ptr(), n, ctypes.cast(hs_arr, ctypes.c_void_p),
+              len(hs), float(getattr(head, "bias_gain", 1.0)), float(rms_eps), float(b_star), agg.data_ptr(),
+              sel.data_ptr(), counts.data_ptr(), sumsq.data_ptr(), _stream(scores))
+    ch = counts.cpu().tolist()
+    p = plan(row_starts, seq_lens, art_starts, art_ends, [max(1, c) for c in ch], device)
+    return p, sel, agg, sumsq, ch
+
+
 def _streams(pairs, p: KeepPlan):
     """PackStream array of (src, dst) or (src, dst, gap) entries: with a gap, kept row j of
     sequence b goes to dst row j + b * gap (a cache with `gap` free rows after each sequence)."""
@@ -327,8 +401,17 @@ def branch_readout(gu: torch.Tensor, w_row: torch.Tensor, out: Optional[torch.Te
 class _BiasScales:
     """Per-(Phase-2 layer, head) bias magnitude and temperature shared by the scoring heads:
     gate_scale (L2, H) and attn_scale (L2, H) or None, both pre-softplus, scaled_softmax flag and
-    the normalisation gain bias_gain."""
+    the normalisation gain bias_gain.  selection_mode / tau: E2EGate's selection (e2e_gate_module.py
+    :216-266): "topk" keeps K state tokens, "threshold" keeps those with sigmoid(agg) >= tau
+    (threshold_plan)."""
     bias_gain: float = 1.0
+    selection_mode: str = "topk"
+    tau: float = 0.5
+
+    def selection_head_scale(self) -> List[float]:
+        """softplus(gate_scale) of the first Phase-2 layer, fp32, as host floats: the per-head factors
+        of the selection value agg (aggregate, e2e_gate_module.py:387-399)."""
+        return torch.nn.functional.softplus(self.gate_scale[0].float()).cpu().tolist()
 
     @property
     def ssmax(self) -> bool:

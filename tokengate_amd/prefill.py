@@ -228,7 +228,13 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
         scores = head.scores(h)
 
     mark("select+pack")
-    p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
+    threshold = getattr(head, "selection_mode", "topk") == "threshold"
+    if threshold:
+        # sample-dependent kept counts (one host synchronisation); K is unused, as in the reference
+        p, sel_scores, _, sel_sumsq, _ = G.threshold_plan(scores, geo1.cu[:-1], lens, art_starts, art_ends, head,
+                                                           dev)
+    else:
+        p = G.plan(geo1.cu[:-1], lens, art_starts, art_ends, K, dev)
     T2 = p.total_kept
     hs = torch.empty(T2, shape.d_model, dtype=h.dtype, device=dev)
     kept_pos = torch.empty(T2, dtype=torch.int64, device=dev)
@@ -243,7 +249,11 @@ def prefill_batch(wts: DecoderWeights, head, ids_list: Sequence, art_starts: Seq
     # the selection's error word comes back with an asynchronous copy; it is checked once every
     # launch of the prefill is queued (the GPU then never waits for the host)
     err_host = torch.zeros(1, dtype=torch.int32, pin_memory=True)
-    keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias, error_out=err_host)
+    if threshold:
+        keep = G.select_pack(sel_scores, p, pairs, positions=kept_pos, error_out=err_host)
+        G.pack(keep, p, [], bias_src=scores, sumsq=sel_sumsq, bias_out=kept_bias)
+    else:
+        keep = G.select_pack(scores, p, pairs, positions=kept_pos, bias_out=kept_bias, error_out=err_host)
     err_ev = torch.cuda.Event()
     err_ev.record()
     sel_stream = torch.cuda.current_stream().cuda_stream
