@@ -6,13 +6,20 @@ head_dim 128, bf16, causal; Q/K/V ~ N(0,1)/sqrt(128); per-key bias log(sigmoid(z
 forced to 0 on positions [0,64) and [32512,32768), broadcast over heads.  Inputs are generated
 on the device before timing (synthetic data).
 
+Before the W warmup steps the forward runs untimed for about 0.15 s (`clock_warmup_launches`): a
+per-dispatch clock profile (profiles/prefill_32k_phase1_clock.txt) shows the part's clock ramping
+over the first ~10 launches from idle, so without it the timed steps would measure the ramp.
+
 Prints ONE JSON line with the bench contract fields plus:
   roofline     — the attention kernel's algorithmic TFLOP/s (2*B*H*D*S*(S+1) per launch over
                  the mean launch time from HIP events on the launch stream) against the bf16
                  dense MFMA peak; traffic = HBM bytes per launch from the committed rocprofv3
                  counter summary when present;
-  cpu_baseline — the oracle (float32 numpy, all host cores through BLAS) on a bounded sample of
-                 the same workload: the last query rows of every head, full causal key range;
+  cpu_baseline — the reference's CPU attention path (its SDPA compatibility prefill: chunks of 128
+                 query rows, an additive float mask, GQA by repeating K/V) restated in float32 torch
+                 on the host's threads, timed on a bounded sample of the same workload (the last
+                 query chunks, each over every key it sees); `cores` is the thread count used and
+                 `affinity_cores` the cores this process may run on;
   extra        — secondary measurements: the 4k forward, the B4 x 8192 backward (TFLOP/s of
                  5*B*H*D*S*(S+1)), the 32k gate path (scoring, top-K, pack; the short gate
                  launches are timed as replays of a captured HIP graph), and the pruned-prefill
@@ -58,10 +65,16 @@ def make_inputs(S, H, Hkv, sigma, seed, device, prefix=64, suffix=256, qkv_scale
     return q, k, v, bias_raw, scale
 
 
-def time_fwd(q, k, v, bias_raw, scale, steps, warmup):
-    """Returns (ms_per_step from the bracketing host clock, mean kernel ms from HIP events)."""
+CLOCK_WARMUP_LAUNCHES = 40
+
+
+def time_fwd(q, k, v, bias_raw, scale, steps, warmup, clock_warmup=0):
+    """Returns (ms_per_step from the bracketing host clock, mean kernel ms from HIP events).
+    clock_warmup: untimed launches before the warmup steps (the clock's ramp from idle)."""
     import torch
     op = torch.ops.recursive_kvs.fa2_keybias_fwd
+    for _ in range(clock_warmup):
+        op(q, k, v, bias_raw, scale, True)
     for _ in range(warmup):
         op(q, k, v, bias_raw, scale, True)
     torch.cuda.synchronize()
@@ -357,6 +370,26 @@ def prefill_trace_run(dev, runs=8):
         print(f"prefill {i + 1}/{runs} done", flush=True)
 
 
+def clock_study_run(dev, runs=3):
+    """The 32k key-bias forward alone (10 launches, the benchmark's inputs), then `runs` gated
+    prefills at 32k / K=2000 (prefill_trace_run's), then the forward alone again (5 launches): a
+    per-dispatch GRBM_GUI_ACTIVE / duration profile compares the clock of the forward with that of
+    the prefill's own Phase-1 attention launches."""
+    import torch
+    S, H, Hkv = 32768, 16, 8
+    q, k, v, bias_raw, scale = make_inputs(S, H, Hkv, 3.0, 2, dev, qkv_scale=1.0 / math.sqrt(128))
+    op = torch.ops.recursive_kvs.fa2_keybias_fwd
+    for _ in range(10):
+        op(q, k, v, bias_raw, scale, True)
+    torch.cuda.synchronize()
+    print("clock study: forward alone x10 done", flush=True)
+    prefill_trace_run(dev, runs=runs)
+    for _ in range(5):
+        op(q, k, v, bias_raw, scale, True)
+    torch.cuda.synchronize()
+    print("clock study: forward alone x5 done", flush=True)
+
+
 def decode_trace_run(dev, steps=30):
     """Greedy decode after the 32k / K=2000 gated prefill of prefill_trace_run (graph replay of the
     whole step after the first), for a per-kernel trace of the decode step; prints ms per token."""
@@ -460,7 +493,8 @@ def gate_counter_run(dev, reps=5):
 
 def cpu_threads() -> int:
     """Host threads for the CPU legs: the job's CPU share (OMP_NUM_THREADS when the environment
-    sets it), else every core this process may run on."""
+    sets it, as on a GPU box shared by several jobs), else every core this process may run on
+    (len(os.sched_getaffinity(0))); the report gives both counts."""
     env = os.environ.get("OMP_NUM_THREADS", "")
     n = len(os.sched_getaffinity(0))
     return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
@@ -496,7 +530,8 @@ def cpu_prune_baseline():
     for K in (100, 500, 2000):
         t = _median_s(lambda: cp.prune(sc, K, s, e, S, [hid] + kvs))
         res[f"K{K}_ms"] = round(t * 1e3, 3)
-    res.update({"cores": threads, "kind": "port", "cpu_model": cpu_model(),
+    res.update({"cores": threads, "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
+                "cpu_model": cpu_model(),
                 "sample": "reference CPU pruning path restated in torch (topk, sort, cat, index_select of "
                           "hidden + 2 layers' K/V), 32k / K in {100, 500, 2000}, median of 3"})
     return res
@@ -536,7 +571,8 @@ def cpu_baseline(seconds):
         flop += 4.0 * H * D * sum(r + 1 for r in range(hi - chunk, hi))
         done += chunk
     dt = time.perf_counter() - t0
-    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+            "affinity_cores": len(os.sched_getaffinity(0)), "kind": "port",
             "cpu_model": cpu_model(),
             "sample": f"reference CPU attention path restated in torch (chunked SDPA, float mask, GQA by "
                       f"repeat), float32: the last {done} query rows of the 32k causal workload in "
@@ -574,6 +610,9 @@ def main():
                     help="only run greedy decode steps after one 32k / K=2000 prefill (for a kernel trace)")
     ap.add_argument("--ttft-only", action="store_true",
                     help="only run 8 back-to-back gated prefills at 32k / K=2000 (for a kernel trace)")
+    ap.add_argument("--clock-study", action="store_true",
+                    help="only run the 32k forward alone, 3 gated prefills at 32k / K=2000, then the forward "
+                         "alone again (for a per-dispatch clock profile)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the path is timed on one GPU's share of the work, with no "
@@ -589,6 +628,9 @@ def main():
     if args.ttft_only:
         prefill_trace_run(dev)
         return
+    if args.clock_study:
+        clock_study_run(dev)
+        return
     if args.gate_counters:
         gate_counter_run(dev)
         return
@@ -602,11 +644,12 @@ def main():
     S, H, Hkv = 32768, 16, 8
     q, k, v, bias_raw, scale = make_inputs(S, H, Hkv, 3.0, 2, dev, qkv_scale=1.0 / math.sqrt(128))
     flops = causal_flops(1, H, S)
-    ms_step, kern_ms = time_fwd(q, k, v, bias_raw, scale, args.steps, args.warmup)
+    ms_step, kern_ms = time_fwd(q, k, v, bias_raw, scale, args.steps, args.warmup,
+                                clock_warmup=CLOCK_WARMUP_LAUNCHES)
     value = flops / (ms_step * 1e-3) / 1e12
     achieved = flops / (kern_ms * 1e-3) / 1e12
 
-    extra = {"kernel_ms_32k": round(kern_ms, 4)}
+    extra = {"kernel_ms_32k": round(kern_ms, 4), "clock_warmup_launches": CLOCK_WARMUP_LAUNCHES}
     if not args.no_extra:
         q1, k1, v1, b1, s1 = make_inputs(4096, H, Hkv, 2.0, 0, dev, prefix=0, suffix=0)
         _, k1ms = time_fwd(q1, k1, v1, b1, s1, 20, 5)
