@@ -21,7 +21,8 @@ Prints ONE JSON line with the bench contract fields plus:
                  query chunks, each over every key it sees); `cores` is the thread count used and
                  `affinity_cores` the cores this process may run on;
   extra        — secondary measurements: the 4k forward, the B4 x 8192 backward (TFLOP/s of
-                 5*B*H*D*S*(S+1)), the 32k gate path (scoring, top-K, pack; the short gate
+                 5*B*H*D*S*(S+1)), the 32k and ragged 8 x 16k-128k gate paths (scoring, top-K,
+                 pack, and the whole score -> select -> pack chain in one graph; the short gate
                  launches are timed as replays of a captured HIP graph), and the pruned-prefill
                  time to first token of a Qwen3-1.7B-shaped decoder at 32k (K = 100, 2000, all)
                  and on 8 ragged prompts of 16k-128k tokens.
@@ -202,6 +203,11 @@ def bench_gate(dev, iters=50):
         ms_sel = time_graph(lambda: gate.select_pack(scores, p, [], positions=pos, bias_out=bias, keep_out=keep))
         ms_sp = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
         sp = (pack_bytes + topk_bytes) / (ms_sp * 1e-3) / 1e9
+        # the whole chain from the hidden states: scoring head, selection, pack (one graph)
+        ms_chain = time_graph(lambda: (gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e]),
+                                       gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias,
+                                                        keep_out=keep)))
+        chain = (score_bytes + pack_bytes + topk_bytes) / (ms_chain * 1e-3) / 1e9
         res[f"K{K}"] = {"kept": T, "topk_ms": round(ms_topk, 4), "pack_ms": round(ms_pack, 4),
                         "pack_gbs": round(pack_bytes / (ms_pack * 1e-3) / 1e9, 1),
                         "pack_frac_hbm": round(pack_bytes / (ms_pack * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -212,6 +218,8 @@ def bench_gate(dev, iters=50):
                         "select_multi_wg_ms": round(ms_sel, 4),
                         "select_pack_ms": round(ms_sp, 4), "select_pack_gbs": round(sp, 1),
                         "select_pack_frac_hbm": round(sp / PEAK_HBM_GBS, 4),
+                        "score_select_pack_ms": round(ms_chain, 4),
+                        "score_select_pack_frac_hbm": round(chain / PEAK_HBM_GBS, 4),
                         "bytes": pack_bytes + topk_bytes}
     return res
 
@@ -254,6 +262,9 @@ def bench_gate_ragged8(dev):
     ms_topk = time_graph(lambda: gate.select_keep(scores, p, keep_out=keep, sumsq_out=ss))
     ms_sel = time_graph(lambda: gate.select_pack(scores, p, [], positions=pos, bias_out=bias, keep_out=keep))
     ms_new = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
+    # the whole chain from the hidden states: scoring head over every row, selection, pack (one graph)
+    ms_chain = time_graph(lambda: (gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out),
+                                   gate.select_pack(sc_out, p, pairs, positions=pos, bias_out=bias, keep_out=keep)))
     n_art = sum(e - s for s, e in zip(starts, ends))
     byts = 2 * T * (2048 * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4) + n_art * 4
     gbs = lambda ms: byts / (ms * 1e-3) / 1e9
@@ -263,7 +274,9 @@ def bench_gate_ragged8(dev):
             "topk_single_wg_ms": round(ms_topk, 4), "topk_pack_ms": round(ms_old, 4),
             "topk_pack_frac_hbm": round(gbs(ms_old) / PEAK_HBM_GBS, 4),
             "select_multi_wg_ms": round(ms_sel, 4), "select_pack_ms": round(ms_new, 4),
-            "select_pack_gbs": round(gbs(ms_new), 1), "select_pack_frac_hbm": round(gbs(ms_new) / PEAK_HBM_GBS, 4)}
+            "select_pack_gbs": round(gbs(ms_new), 1), "select_pack_frac_hbm": round(gbs(ms_new) / PEAK_HBM_GBS, 4),
+            "score_select_pack_ms": round(ms_chain, 4),
+            "score_select_pack_frac_hbm": round((byts + score_bytes) / (ms_chain * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
 
 def bench_ttft(dev, reps=5):
