@@ -445,6 +445,7 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
     float bk = 0.f;
     if constexpr (HAS_BIAS)
       if (kvalid) bk = a.bias[(int64_t)b * a.bias_bs + (int64_t)hh * a.bias_hs + key];
+    const f32x4 bk4 = {bk, bk, bk, bk};   // the S accumulators' start: the key's bias costs no VALU per tile
     float dbacc = 0.f;
 
     auto issue_tile = [&](int m0, auto buf_c) {
@@ -466,6 +467,13 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       constexpr int BUF = decltype(buf_c)::value;
       const int m00 = m_start + t * kQSlot;
       wait_vm<0>();
+      // the slot's LSE rows (DMA'd by wave 0, now complete) to log2 units, once for every wave;
+      // the barrier below orders this write before the other waves' reads
+      static_assert(kQSub * kQT == 64, "wave 0 DMAs every LSE row of a slot");
+      if (wave == 0) {
+        float *lw = lslot(buf_c) + lane;
+        *lw = *lw * kLog2e;
+      }
       ring_barrier();
       if (t + 1 < n_qt) issue_tile(m00 + kQSlot, std::integral_constant<int, 1 - BUF>());
 #pragma unroll
@@ -478,11 +486,11 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       const float *const dsl = dslot(buf_c) + sub * kQT;
 
       // S = Q K^T and dP = dO V^T for queries m0 + pi_rb(row), this lane's key
-      f32x4 sacc[2], pacc[2];
+      f32x4 sacc[2] = {bk4, bk4}, pacc[2];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) { sacc[rb][v] = 0.f; pacc[rb][v] = 0.f; }
+        for (int v = 0; v < 4; ++v) pacc[rb][v] = 0.f;
 #pragma unroll
       for (int k2 = 0; k2 < 4; k2 += 2) {
         bf16x8 qa[2][2], da[2][2];
@@ -511,11 +519,7 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       for (int rb = 0; rb < 2; ++rb) {
         const f32x4 l4 = *reinterpret_cast<const f32x4 *>(lsl + 8 * g + 4 * rb);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float z = sacc[rb][i];
-          if constexpr (HAS_BIAS) z += bk;
-          p[rb][i] = fast_exp2(fmaf(z, a.scale_log2, -l4[i] * kLog2e));
-        }
+        for (int i = 0; i < 4; ++i) p[rb][i] = fast_exp2(fmaf(sacc[rb][i], a.scale_log2, -l4[i]));
       }
       // one uniform branch for the whole tile, and no per-element branches inside it: P -> +0 where
       // the query is past the sequence, the key past the keys, or (causal) the key after the query,
