@@ -416,6 +416,35 @@ def test_select_pack_workspace_reuse_across_batch_sizes(cuda):
         _check_select_pack(scores, seqs, ref, p, cuda)
 
 
+@pytest.mark.parametrize("over", [-1, 0, 1, 97])
+def test_select_pack_one_and_three_launch_forms(cuda, over):
+    """tg_gate_select_pack runs the selection in one launch when its chunk workgroups (4096 keys
+    each here) all fit the chip at once (at most one per CU) and in three launches above that:
+    batches of CU count - 1, CU count, CU count + 1 and CU count + 97 chunks, sequences of 1-8
+    chunks (ragged lengths inside the last chunk, a few empty spans), bf16-valued scores (ties at
+    every threshold), K from 1 to beyond the span; keep lists, positions, rows bit-exact, bias
+    against the oracle's float32 chain, the error word clear."""
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    target = cus + over
+    rng = np.random.default_rng(40 + over)
+    seqs, r0, n_chunks = [], 0, 0
+    while n_chunks < target:
+        g = int(min(rng.integers(1, 9), target - n_chunks))
+        n_art = int(rng.integers((g - 1) * 4096 + 1, g * 4096 + 1))
+        pre, suf = int(rng.integers(0, 70)), int(rng.integers(0, 300))
+        L = pre + n_art + suf
+        seqs.append((r0, L, pre, pre + n_art, int(rng.choice([1, 100, 500, 2000, n_art, n_art + 5]))))
+        r0 += L
+        n_chunks += g
+        if rng.random() < 0.1:                       # an empty span: no chunk, prefix and suffix kept
+            seqs.append((r0, 40, 20, 20, 100))
+            r0 += 40
+    print(f"[launch forms] cus={cus} chunks={n_chunks} seqs={len(seqs)} rows={r0}", flush=True)
+    scores = og.bf16(rng.standard_normal(r0).astype(np.float32))
+    keep, p = _check_select(scores, seqs, cuda)
+    assert p.sel_kpt == 8 and p.sel_starts[-1] == target
+
+
 def test_pack_skips_positions_outside_their_sequence(cuda):
     """A kept position outside [0, seq_len) of its sequence (what an unwritten keep entry holds)
     gathers nothing: that destination row and its position / bias entries keep their contents, the

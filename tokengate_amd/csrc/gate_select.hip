@@ -51,14 +51,18 @@ constexpr int kQBins2 = 2048;          // bits 19..9
 constexpr int kQBins3 = 512;           // bits 8..0
 constexpr int kQMaxChunks = 64;        // chunks per sequence
 constexpr int kQCap = 16384;           // candidate buffer per sequence (key, position)
+constexpr int kQLdsCand = 4096;        // digit-B1 keys the one-launch form resolves in LDS
+constexpr int kQFusedMaxChunks = 512;  // chunk workgroups of the one-launch form (at most one per CU)
+constexpr int kQMaxChunkKeys = 32 * kQThreads;
 constexpr int kQMaxStreams = 16;
 constexpr int kQSeqWords = 16;         // per-sequence record
 constexpr int kQChunkWords = 8;        // per-chunk record
 
 // per-sequence record words
-enum { SQ_CNT1 = 0, SQ_CNT2, SQ_CAND, SQ_B1, SQ_R1, SQ_T, SQ_RNORM };
+enum { SQ_CNT1 = 0, SQ_CNT2, SQ_CAND, SQ_B1, SQ_R1, SQ_T, SQ_RNORM, SQ_FLAG };   // SQ_FLAG: one-launch phase
 // per-chunk record words
-enum { CK_SUMSQ = 0, CK_QUOTA, CK_AGG };   // CK_AGG: zero, or kept count | 1 << 31 once published
+enum { CK_SUMSQ = 0, CK_QUOTA, CK_AGG, CK_OFF };   // CK_AGG: zero, or kept count | 1 << 31 once published;
+                                                 // CK_OFF: output offset (one-launch form, resolved in LDS)
 // global words
 enum { GL_TICKET = 0, GL_EXIT, GL_ERROR };
 
@@ -90,6 +94,7 @@ struct SelArgs {
   uint32_t *hist1;           // (n_sel, kQBins1)
   uint32_t *hist2;           // (n_sel, kQBins2)
   uint32_t *cand;            // (nseq, kQCap, 2)
+  uint32_t *sorted;          // one-launch form: (n_sel, 512 * KPT) each chunk's keys by top digit, descending
   int spin_limit;
 };
 
@@ -136,15 +141,23 @@ __device__ __forceinline__ void load_keys(const float *art, int n, int t0, uint3
   }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave on the DPP network: shifts by 1, 2, 4, 8 inside
+// each row of 16 lanes (lanes without a source add 0), then the last lane of row 0 broadcast into
+// row 1 and that of row 2 into row 3, then lane 31 into rows 2 and 3.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);    // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);    // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);    // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);    // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31 into rows 2, 3
+  return v;
+}
+
 // Block-wide exclusive prefix sum of one int per thread (thread order), and the total.
 __device__ __forceinline__ int q_scan(int v, int *s_w, int &total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int incl = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(incl, o);
-    if (lane >= o) incl += y;
-  }
+  const int incl = wave_incl_scan(v);
   __syncthreads();
   if (lane == 63) s_w[w] = incl;
   __syncthreads();
@@ -159,11 +172,7 @@ __device__ __forceinline__ int q_scan(int v, int *s_w, int &total) {
   return before + incl - v;
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
+__device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 
 // Every wave's global stores have completed (reached L2) before the workgroup barrier, so that
 // the one agent-scope release issued after it (which writes L2 back for the other XCDs) covers
@@ -215,53 +224,80 @@ __device__ __forceinline__ void find_digit(const uint32_t (&tv)[PER], int bin0, 
 }
 
 // ---------------------------------------------------------------------------------------------
+// The selection's phases, composed into three launches (select1, select2, compact) or one
+// (gate_select_fused_kernel).  Per chunk workgroup: its sequence, geometry and keys.
 template <int KPT>
-__global__ __launch_bounds__(kQThreads) void gate_select1_kernel(SelArgs a) {
-  constexpr int CHUNK = KPT * kQThreads;
-  constexpr int PER = kQBins1 / kQThreads;   // 8 bins per thread
-  __shared__ uint32_t s_hist[kQBins1];
-  __shared__ int s_w[kQWaves], s_flag, s_d, s_cnt, s_above_d;
-  __shared__ float s_r2[kQWaves], s_r2c[kQMaxChunks];
-  const int tid = threadIdx.x, gc = blockIdx.x;
-  int g0, G;
-  const int b = seq_of_chunk(a, gc, g0, G);
-  const int *gm = a.geom + 6 * b;
-  const int s = gm[2], e = gm[3], kc = gm[4];
-  const int n = e - s;
-  const int t0 = (gc - g0) * CHUNK + tid * KPT;
-  const float *art = a.scores + (int64_t)gm[0] + s;
+struct Chunk {
+  static constexpr int CHUNK = KPT * kQThreads;
+  int gc, b, g0, G, s, e, n, kc, kstart, t0;
+  const int *gm;
+  const float *art;
+  uint32_t *sq_rec;
   uint32_t key[KPT], valid;
   float ssq;
-  load_keys<KPT>(art, n, t0, key, valid, ssq);
-  for (int i = tid; i < kQBins1; i += kQThreads) s_hist[i] = 0u;
+  __device__ __forceinline__ void init(const SelArgs &a, int gc_) {
+    gc = gc_;
+    b = seq_of_chunk(a, gc, g0, G);
+    gm = a.geom + 6 * b;
+    s = gm[2];
+    e = gm[3];
+    kc = gm[4];
+    kstart = gm[5];
+    n = e - s;
+    t0 = (gc - g0) * CHUNK + (int)threadIdx.x * KPT;
+    art = a.scores + (int64_t)gm[0] + s;
+    sq_rec = a.seq + (int64_t)b * kQSeqWords;
+    load_keys<KPT>(art, n, t0, key, valid, ssq);
+  }
+};
+
+struct SelShared {
+  uint32_t hist[kQBins1];
+  int w[kQWaves], flag, d, cnt, above, base;
+  float r2[kQWaves], r2c[kQMaxChunks];
+  int tie[kQMaxChunks];
+  int coff[kQMaxChunks], clo[kQMaxChunks], ctot;   // one-launch form: digit-B1 key ranges per chunk
+  int gt[kQMaxChunks];                             // ... and their keys above T
+};
+
+// Pass 1, every chunk: the histogram of the keys' top 12 bits and the chunk's sum of squares,
+// published for the sequence's last arrival.
+template <int KPT>
+__device__ __forceinline__ void pass1_chunk(const SelArgs &a, Chunk<KPT> &c, SelShared &sh) {
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kQBins1; i += kQThreads) sh.hist[i] = 0u;
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < KPT; ++i)
-    if (valid >> i & 1u) atomicAdd(&s_hist[key[i] >> 20], 1u);
+    if (c.valid >> i & 1u) atomicAdd(&sh.hist[c.key[i] >> 20], 1u);
+  float ssq = c.ssq;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) ssq += __shfl_xor(ssq, o);
-  if ((tid & 63) == 0) s_r2[tid >> 6] = ssq;
+  if ((tid & 63) == 0) sh.r2[tid >> 6] = ssq;
   __syncthreads();
-  u32x4 *gh = reinterpret_cast<u32x4 *>(a.hist1 + (int64_t)gc * kQBins1);
-  gh[tid] = reinterpret_cast<const u32x4 *>(s_hist)[tid];
-  gh[tid + kQThreads] = reinterpret_cast<const u32x4 *>(s_hist)[tid + kQThreads];
+  u32x4 *gh = reinterpret_cast<u32x4 *>(a.hist1 + (int64_t)c.gc * kQBins1);
+  gh[tid] = reinterpret_cast<const u32x4 *>(sh.hist)[tid];
+  gh[tid + kQThreads] = reinterpret_cast<const u32x4 *>(sh.hist)[tid + kQThreads];
   if (tid == 0) {
     float sq = 0.f;
-    for (int i = 0; i < kQWaves; ++i) sq += s_r2[i];
-    a.chunk[(int64_t)gc * kQChunkWords + CK_SUMSQ] = __builtin_bit_cast(uint32_t, sq);
+    for (int i = 0; i < kQWaves; ++i) sq += sh.r2[i];
+    a.chunk[(int64_t)c.gc * kQChunkWords + CK_SUMSQ] = __builtin_bit_cast(uint32_t, sq);
   }
-  uint32_t *sq_rec = a.seq + (int64_t)b * kQSeqWords;
-  if (!arrive_last(sq_rec + SQ_CNT1, G, &s_flag)) return;
+}
 
-  // ---- the sequence's last chunk: digit B1, the rank still needed inside it, the normaliser ----
+// Pass 1, the sequence's last arrival: digit B1, the rank still needed inside it, the normaliser.
+template <int KPT>
+__device__ __forceinline__ void pass1_last(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
+  constexpr int PER = kQBins1 / kQThreads;   // 8 bins per thread
+  const int tid = threadIdx.x;
   const int bin0 = kQBins1 - PER * (tid + 1);     // this thread's bins bin0 .. bin0+PER-1 (descending threads)
   uint32_t tv[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) tv[j] = 0u;
   {
-    const uint32_t *hb = a.hist1 + (int64_t)g0 * kQBins1 + bin0;
+    const uint32_t *hb = a.hist1 + (int64_t)c.g0 * kQBins1 + bin0;
     int w = 0;
-    for (; w + 4 <= G; w += 4) {      // four chunks' loads in flight at once
+    for (; w + 4 <= c.G; w += 4) {      // four chunks' loads in flight at once
       u32x4 x[8];
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -276,7 +312,7 @@ __global__ __launch_bounds__(kQThreads) void gate_select1_kernel(SelArgs a) {
           tv[4 + j] += x[2 * q + 1][j];
         }
     }
-    for (; w < G; ++w) {
+    for (; w < c.G; ++w) {
       const u32x4 x0 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[0];
       const u32x4 x1 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[1];
 #pragma unroll
@@ -287,81 +323,71 @@ __global__ __launch_bounds__(kQThreads) void gate_select1_kernel(SelArgs a) {
     }
   }
   // the chunks' sums of squares, one per lane, added in chunk order
-  if (tid < G) s_r2c[tid] = __builtin_bit_cast(float, a.chunk[(int64_t)(g0 + tid) * kQChunkWords + CK_SUMSQ]);
-  find_digit<PER>(tv, bin0, kc, s_w, &s_d, &s_cnt, &s_above_d);
+  if (tid < c.G) sh.r2c[tid] = __builtin_bit_cast(float, a.chunk[(int64_t)(c.g0 + tid) * kQChunkWords + CK_SUMSQ]);
+  find_digit<PER>(tv, bin0, c.kc, sh.w, &sh.d, &sh.cnt, &sh.above);
   if (tid == 0) {
     float sq = 0.f;
-    for (int w = 0; w < G; ++w) sq += s_r2c[w];
-    sq_rec[SQ_B1] = (uint32_t)s_d;
-    sq_rec[SQ_R1] = (uint32_t)(kc - s_above_d);
-    sq_rec[SQ_RNORM] = __builtin_bit_cast(uint32_t, rsqrtf(sq / (float)n + a.eps));
-    sq_rec[SQ_CNT1] = 0u;           // every chunk has arrived: reset for the next call
+    for (int w = 0; w < c.G; ++w) sq += sh.r2c[w];
+    c.sq_rec[SQ_B1] = (uint32_t)sh.d;
+    c.sq_rec[SQ_R1] = (uint32_t)(c.kc - sh.above);
+    c.sq_rec[SQ_RNORM] = __builtin_bit_cast(uint32_t, rsqrtf(sq / (float)c.n + a.eps));
+    c.sq_rec[SQ_CNT1] = 0u;           // every chunk has arrived: reset for the next call
   }
 }
 
-// ---------------------------------------------------------------------------------------------
+// Pass 2, every chunk: the histogram of bits 19..9 of the keys of digit B1, and those keys (with
+// positions) appended to the sequence's candidate buffer.
 template <int KPT>
-__global__ __launch_bounds__(kQThreads) void gate_select2_kernel(SelArgs a) {
-  constexpr int CHUNK = KPT * kQThreads;
-  constexpr int PER = kQBins2 / kQThreads;   // 4 bins per thread
-  __shared__ uint32_t s_hist[kQBins2];
-  __shared__ int s_w[kQWaves], s_flag, s_d, s_cnt, s_above_d, s_base;
-  __shared__ int s_tie[kQMaxChunks];
-  const int tid = threadIdx.x, gc = blockIdx.x;
-  int g0, G;
-  const int b = seq_of_chunk(a, gc, g0, G);
-  const int *gm = a.geom + 6 * b;
-  const int s = gm[2], e = gm[3];
-  const int n = e - s;
-  const int t0 = (gc - g0) * CHUNK + tid * KPT;
-  const float *art = a.scores + (int64_t)gm[0] + s;
-  uint32_t *sq_rec = a.seq + (int64_t)b * kQSeqWords;
-  const uint32_t B1 = sq_rec[SQ_B1];
-  const int r1 = (int)sq_rec[SQ_R1];
-  uint32_t key[KPT], valid;
-  float ssq;
-  load_keys<KPT>(art, n, t0, key, valid, ssq);
-  for (int i = tid; i < kQBins2; i += kQThreads) s_hist[i] = 0u;
+__device__ __forceinline__ void pass2_chunk(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
+  const int tid = threadIdx.x;
+  const uint32_t B1 = c.sq_rec[SQ_B1];
+  for (int i = tid; i < kQBins2; i += kQThreads) sh.hist[i] = 0u;
   __syncthreads();
   uint32_t inplay = 0u;
 #pragma unroll
   for (int i = 0; i < KPT; ++i)
-    if ((valid >> i & 1u) && (key[i] >> 20) == B1) {
+    if ((c.valid >> i & 1u) && (c.key[i] >> 20) == B1) {
       inplay |= 1u << i;
-      atomicAdd(&s_hist[(key[i] >> 9) & (kQBins2 - 1)], 1u);
+      atomicAdd(&sh.hist[(c.key[i] >> 9) & (kQBins2 - 1)], 1u);
     }
-  // candidates: this chunk's keys of digit B1, appended to the sequence's buffer
   int nin_tot;
-  const int in_off = q_scan(__builtin_popcount(inplay), s_w, nin_tot);
+  const int in_off = q_scan(__builtin_popcount(inplay), sh.w, nin_tot);
   if (tid == 0)
-    s_base = nin_tot ? (int)__hip_atomic_fetch_add(sq_rec + SQ_CAND, (uint32_t)nin_tot, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)
-                     : 0;
+    sh.base = nin_tot ? (int)__hip_atomic_fetch_add(c.sq_rec + SQ_CAND, (uint32_t)nin_tot, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                      : 0;
   __syncthreads();
   {
-    uint32_t *cb = a.cand + (int64_t)b * kQCap * 2;
-    int o = s_base + in_off;
+    uint32_t *cb = a.cand + (int64_t)c.b * kQCap * 2;
+    int o = sh.base + in_off;
 #pragma unroll
     for (int i = 0; i < KPT; ++i)
       if (inplay >> i & 1u) {
         if (o < kQCap) {
-          cb[2 * o] = key[i];
-          cb[2 * o + 1] = (uint32_t)(t0 + i);
+          cb[2 * o] = c.key[i];
+          cb[2 * o + 1] = (uint32_t)(c.t0 + i);
         }
         ++o;
       }
   }
-  reinterpret_cast<u32x4 *>(a.hist2 + (int64_t)gc * kQBins2)[tid] = reinterpret_cast<const u32x4 *>(s_hist)[tid];
-  if (!arrive_last(sq_rec + SQ_CNT2, G, &s_flag)) return;
+  reinterpret_cast<u32x4 *>(a.hist2 + (int64_t)c.gc * kQBins2)[tid] = reinterpret_cast<const u32x4 *>(sh.hist)[tid];
+}
 
-  // ---- the sequence's last chunk: digit B2, then T and the ties still needed from the candidates,
-  // then each chunk's quota of ties (lowest positions first) ----
+// Pass 2, the sequence's last arrival: digit B2, then T and the ties still needed from the
+// candidates, then each chunk's quota of ties (lowest positions first).
+template <int KPT>
+__device__ __forceinline__ void pass2_last(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
+  constexpr int PER = kQBins2 / kQThreads;   // 4 bins per thread
+  constexpr int CHUNK = Chunk<KPT>::CHUNK;
+  const int tid = threadIdx.x;
+  const uint32_t B1 = c.sq_rec[SQ_B1];
+  const int r1 = (int)c.sq_rec[SQ_R1];
   const int bin0 = kQBins2 - PER * (tid + 1);
   uint32_t tv[PER] = {0u, 0u, 0u, 0u};
   {
-    const uint32_t *hb = a.hist2 + (int64_t)g0 * kQBins2 + bin0;
+    const uint32_t *hb = a.hist2 + (int64_t)c.g0 * kQBins2 + bin0;
     int w = 0;
-    for (; w + 8 <= G; w += 8) {      // eight chunks' loads in flight at once
+    for (; w + 8 <= c.G; w += 8) {      // eight chunks' loads in flight at once
       u32x4 x[8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const u32x4 *>(hb + (int64_t)(w + q) * kQBins2);
@@ -370,100 +396,86 @@ __global__ __launch_bounds__(kQThreads) void gate_select2_kernel(SelArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) tv[j] += x[q][j];
     }
-    for (; w < G; ++w) {
+    for (; w < c.G; ++w) {
       const u32x4 x = *reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins2);
 #pragma unroll
       for (int j = 0; j < 4; ++j) tv[j] += x[j];
     }
   }
-  find_digit<PER>(tv, bin0, r1, s_w, &s_d, &s_cnt, &s_above_d);
-  const uint32_t B2 = (uint32_t)s_d;
-  const int r2 = r1 - s_above_d;
-  if (tid < G) s_tie[tid] = 0;
+  find_digit<PER>(tv, bin0, r1, sh.w, &sh.d, &sh.cnt, &sh.above);
+  const uint32_t B2 = (uint32_t)sh.d;
+  const int r2 = r1 - sh.above;
+  if (tid < c.G) sh.tie[tid] = 0;
   // keys of prefix B1.B2 (23 bits): from the candidate buffer, or the whole span if it overflowed
   const uint32_t pre = (B1 << 11) | B2;
-  const int ncand = (int)sq_rec[SQ_CAND];
+  const int ncand = (int)c.sq_rec[SQ_CAND];
   const bool from_buf = ncand <= kQCap;
-  const uint32_t *cb = a.cand + (int64_t)b * kQCap * 2;
-  const int nscan = from_buf ? ncand : n;
-  for (int i = tid; i < kQBins3; i += kQThreads) s_hist[i] = 0u;
+  const uint32_t *cb = a.cand + (int64_t)c.b * kQCap * 2;
+  const int nscan = from_buf ? ncand : c.n;
+  for (int i = tid; i < kQBins3; i += kQThreads) sh.hist[i] = 0u;
   __syncthreads();
   for (int i = tid; i < nscan; i += kQThreads) {
-    const uint32_t k = from_buf ? cb[2 * i] : qkey(art[i]);
-    if ((k >> 9) == pre) atomicAdd(&s_hist[k & (kQBins3 - 1)], 1u);
+    const uint32_t k = from_buf ? cb[2 * i] : qkey(c.art[i]);
+    if ((k >> 9) == pre) atomicAdd(&sh.hist[k & (kQBins3 - 1)], 1u);
   }
   __syncthreads();
-  const uint32_t t3 = s_hist[kQBins3 - 1 - tid];        // thread t owns bin 511 - t
+  const uint32_t t3 = sh.hist[kQBins3 - 1 - tid];        // thread t owns bin 511 - t
   uint32_t tv3[1] = {t3};
-  find_digit<1>(tv3, kQBins3 - 1 - tid, r2, s_w, &s_d, &s_cnt, &s_above_d);
-  const uint32_t T = (pre << 9) | (uint32_t)s_d;
-  const int rT = r2 - s_above_d;                       // ties of T still needed
+  find_digit<1>(tv3, kQBins3 - 1 - tid, r2, sh.w, &sh.d, &sh.cnt, &sh.above);
+  const uint32_t T = (pre << 9) | (uint32_t)sh.d;
+  const int rT = r2 - sh.above;                       // ties of T still needed
   for (int i = tid; i < nscan; i += kQThreads) {
-    const uint32_t k = from_buf ? cb[2 * i] : qkey(art[i]);
-    if (k == T) atomicAdd(&s_tie[(from_buf ? (int)cb[2 * i + 1] : i) / CHUNK], 1);
+    const uint32_t k = from_buf ? cb[2 * i] : qkey(c.art[i]);
+    if (k == T) atomicAdd(&sh.tie[(from_buf ? (int)cb[2 * i + 1] : i) / CHUNK], 1);
   }
   __syncthreads();
   if (tid == 0) {
     int tb = 0;
-    for (int w = 0; w < G; ++w) {       // chunks in position order
-      const int q = max(0, min(s_tie[w], rT - tb));
-      tb += s_tie[w];
-      a.chunk[(int64_t)(g0 + w) * kQChunkWords + CK_QUOTA] = (uint32_t)q;
+    for (int w = 0; w < c.G; ++w) {       // chunks in position order
+      const int q = max(0, min(sh.tie[w], rT - tb));
+      tb += sh.tie[w];
+      a.chunk[(int64_t)(c.g0 + w) * kQChunkWords + CK_QUOTA] = (uint32_t)q;
     }
-    sq_rec[SQ_T] = T;
-    sq_rec[SQ_CNT2] = 0u;
-    sq_rec[SQ_CAND] = 0u;
+    c.sq_rec[SQ_T] = T;
+    c.sq_rec[SQ_CNT2] = 0u;
+    c.sq_rec[SQ_CAND] = 0u;
   }
 }
 
-// ---------------------------------------------------------------------------------------------
+// Compaction of one chunk: its keys above T plus its quota of ties, published at once; its output
+// offset is the sum of the sequence's earlier chunks' counts (a look-back over chunks that publish
+// without waiting); then kept positions ascending, int64 positions and gate bias.
 template <int KPT>
-__global__ __launch_bounds__(kQThreads) void gate_compact_kernel(SelArgs a) {
-  constexpr int CHUNK = KPT * kQThreads;
-  __shared__ int s_w[kQWaves], s_flag;
+__device__ __forceinline__ void compact_chunk(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh, bool known_off) {
   const int tid = threadIdx.x;
-  if (tid == 0)
-    s_flag = (int)__hip_atomic_fetch_add(a.glob + GL_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  const int ticket = s_flag;
-
-  if (ticket < a.n_sel) {
-    // ---- compaction of chunk `ticket` ----
-    const int gc = ticket;
-    int g0, G;
-    const int b = seq_of_chunk(a, gc, g0, G);
-    const int *gm = a.geom + 6 * b;
-    const int s = gm[2], e = gm[3], kstart = gm[5];
-    const int n = e - s;
-    const int t0 = (gc - g0) * CHUNK + tid * KPT;
-    const float *art = a.scores + (int64_t)gm[0] + s;
-    const uint32_t *sq_rec = a.seq + (int64_t)b * kQSeqWords;
-    const uint32_t T = sq_rec[SQ_T];
-    const float rn = __builtin_bit_cast(float, sq_rec[SQ_RNORM]);
-    const int quota = (int)a.chunk[(int64_t)gc * kQChunkWords + CK_QUOTA];
-    uint32_t key[KPT], valid;
-    float ssq;
-    load_keys<KPT>(art, n, t0, key, valid, ssq);
-    uint32_t gtm = 0u, tiem = 0u;
+  const uint32_t T = c.sq_rec[SQ_T];
+  const float rn = __builtin_bit_cast(float, c.sq_rec[SQ_RNORM]);
+  const int quota = (int)a.chunk[(int64_t)c.gc * kQChunkWords + CK_QUOTA];
+  uint32_t gtm = 0u, tiem = 0u;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const bool v = valid >> i & 1u;
-      gtm |= (v && key[i] > T) ? 1u << i : 0u;
-      tiem |= (v && key[i] == T) ? 1u << i : 0u;
-    }
-    int ntie, ngt;
-    int tr = q_scan(__builtin_popcount(tiem), s_w, ntie);   // ties of T before this thread's
-    q_scan(__builtin_popcount(gtm), s_w, ngt);
-    // publish this chunk's kept count, then add those of the sequence's earlier chunks (their
-    // workgroups hold lower tickets: they started first and publish without waiting)
+  for (int i = 0; i < KPT; ++i) {
+    const bool v = c.valid >> i & 1u;
+    gtm |= (v && c.key[i] > T) ? 1u << i : 0u;
+    tiem |= (v && c.key[i] == T) ? 1u << i : 0u;
+  }
+  // one scan of both counts (keys above T in the high half, ties in the low; a chunk holds at most
+  // 16384 keys, so the low half never carries)
+  int both;
+  const int before = q_scan((__builtin_popcount(gtm) << 16) | __builtin_popcount(tiem), sh.w, both);
+  const int tie_before = before & 0xffff, gt_before = before >> 16;
+  int off;
+  if (known_off) {
+    off = (int)a.chunk[(int64_t)c.gc * kQChunkWords + CK_OFF];
+  } else {
     if (tid == 0)
-      __hip_atomic_store(a.chunk + (int64_t)gc * kQChunkWords + CK_AGG,
-                         0x80000000u | (uint32_t)(ngt + min(quota, ntie)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.chunk + (int64_t)c.gc * kQChunkWords + CK_AGG,
+                         0x80000000u | (uint32_t)((both >> 16) + min(quota, both & 0xffff)), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     if (tid < 64) {
-      const int wl = gc - g0;
+      const int wl = c.gc - c.g0;
       int add = 0;
       if (tid < wl) {
-        const uint32_t *ag = a.chunk + (int64_t)(g0 + tid) * kQChunkWords + CK_AGG;
+        const uint32_t *ag = a.chunk + (int64_t)(c.g0 + tid) * kQChunkWords + CK_AGG;
         uint32_t v = 0u;
         int it = 0;
         while (!((v = __hip_atomic_load(ag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) & 0x80000000u)) {
@@ -476,77 +488,419 @@ __global__ __launch_bounds__(kQThreads) void gate_compact_kernel(SelArgs a) {
         add = (int)(v & 0x7fffffffu);
       }
       add = wave_sum_i(add);
-      if (tid == 0) s_flag = add;
+      if (tid == 0) sh.flag = add;
     }
     __syncthreads();
-    const int off = s_flag;
-    uint32_t keepm = gtm;
+    off = sh.flag;
+  }
+  // the quota's ties are the chunk's first ones in position order
+  uint32_t keepm = gtm;
+  int tr = tie_before;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (tiem >> i & 1u) {
-        if (tr < quota) keepm |= 1u << i;
-        ++tr;
-      }
-    int nk;
-    const int koff = q_scan(__builtin_popcount(keepm), s_w, nk);
-    int64_t j = (int64_t)kstart + s + off + koff;
-    const int64_t j_end = (int64_t)kstart + s + gm[4];      // this sequence's state rows end here
+  for (int i = 0; i < KPT; ++i)
+    if (tiem >> i & 1u) {
+      if (tr < quota) keepm |= 1u << i;
+      ++tr;
+    }
+  const int koff = gt_before + min(tie_before, quota);
+  int64_t j = (int64_t)c.kstart + c.s + off + koff;
+  const int64_t j_end = (int64_t)c.kstart + c.s + c.kc;      // this sequence's state rows end here
 #pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (keepm >> i & 1u) {
-        const int64_t pos = s + t0 + i;
-        if (j < j_end) {
-          a.keep[j] = pos;
-          if (a.pos_out) a.pos_out[j] = pos;
-          if (a.bias_out) a.bias_out[j] = qval(key[i]) * rn;
-        } else {
-          __hip_atomic_store(a.glob + GL_ERROR, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        ++j;
+  for (int i = 0; i < KPT; ++i)
+    if (keepm >> i & 1u) {
+      const int64_t pos = c.s + c.t0 + i;
+      if (j < j_end) {
+        a.keep[j] = pos;
+        if (a.pos_out) a.pos_out[j] = pos;
+        if (a.bias_out) a.bias_out[j] = qval(c.key[i]) * rn;
+      } else {
+        __hip_atomic_store(a.glob + GL_ERROR, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-  } else {
-    // ---- prefix / suffix rows of 512 packed rows: positions need no selection ----
-    const int64_t jr = (int64_t)(ticket - a.n_sel) * kQThreads + tid;
-    if (jr < a.total_kept) {
-      int lo = 0, hi = a.nseq - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if ((int64_t)a.geom[6 * mid + 5] <= jr) lo = mid; else hi = mid - 1;
-      }
-      const int *gm = a.geom + 6 * lo;
-      const int64_t t = jr - gm[5];
-      const int s = gm[2], e = gm[3], kc = gm[4];
-      const int64_t pos = t < s ? t : (t >= (int64_t)s + kc ? e + (t - s - kc) : -1);
-      if (pos >= 0) {
-        a.keep[jr] = pos;
-        if (a.pos_out) a.pos_out[jr] = pos;
-        if (a.bias_out) a.bias_out[jr] = 0.f;
-      }
+      ++j;
+    }
+}
+
+// Prefix / suffix rows of 512 packed rows (workgroup `mw` of them): positions need no selection.
+__device__ __forceinline__ void write_meta_rows(const SelArgs &a, int64_t mw) {
+  const int64_t jr = mw * kQThreads + threadIdx.x;
+  if (jr < a.total_kept) {
+    int lo = 0, hi = a.nseq - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)a.geom[6 * mid + 5] <= jr) lo = mid; else hi = mid - 1;
+    }
+    const int *gm = a.geom + 6 * lo;
+    const int64_t t = jr - gm[5];
+    const int s = gm[2], e = gm[3], kc = gm[4];
+    const int64_t pos = t < s ? t : (t >= (int64_t)s + kc ? e + (t - s - kc) : -1);
+    if (pos >= 0) {
+      a.keep[jr] = pos;
+      if (a.pos_out) a.pos_out[jr] = pos;
+      if (a.bias_out) a.bias_out[jr] = 0.f;
     }
   }
+}
 
-  // ---- exit: the last workgroup resets the counters ----
+// The workgroup that finishes last zeroes the compaction counters (and, in the one-launch form,
+// the sequences' phase flags): a zeroed workspace stays zeroed.
+__device__ __forceinline__ void exit_reset(const SelArgs &a, SelShared &sh, bool flags) {
   __syncthreads();
-  if (tid == 0) {
+  if (threadIdx.x == 0) {
     const uint32_t prev =
         __hip_atomic_fetch_add(a.glob + GL_EXIT, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_flag = prev == gridDim.x - 1 ? 1 : 0;
+    sh.flag = prev == gridDim.x - 1 ? 1 : 0;
   }
   __syncthreads();
-  if (s_flag) {
-    for (int i = tid; i < a.n_sel; i += kQThreads) a.chunk[(int64_t)i * kQChunkWords + CK_AGG] = 0u;
-    if (tid == 0) {
+  if (sh.flag) {
+    for (int i = threadIdx.x; i < a.n_sel; i += kQThreads) a.chunk[(int64_t)i * kQChunkWords + CK_AGG] = 0u;
+    if (flags)
+      for (int i = threadIdx.x; i < a.nseq; i += kQThreads) a.seq[(int64_t)i * kQSeqWords + SQ_FLAG] = 0u;
+    if (threadIdx.x == 0) {
       a.glob[GL_TICKET] = 0u;
       a.glob[GL_EXIT] = 0u;
     }
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+template <int KPT>
+__global__ __launch_bounds__(kQThreads) void gate_select1_kernel(SelArgs a) {
+  __shared__ SelShared sh;
+  Chunk<KPT> c;
+  c.init(a, blockIdx.x);
+  pass1_chunk<KPT>(a, c, sh);
+  if (arrive_last(c.sq_rec + SQ_CNT1, c.G, &sh.flag)) pass1_last<KPT>(a, c, sh);
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kQThreads) void gate_select2_kernel(SelArgs a) {
+  __shared__ SelShared sh;
+  Chunk<KPT> c;
+  c.init(a, blockIdx.x);
+  pass2_chunk<KPT>(a, c, sh);
+  if (arrive_last(c.sq_rec + SQ_CNT2, c.G, &sh.flag)) pass2_last<KPT>(a, c, sh);
+}
+
+// Workgroups take tickets in start order: the first n_sel tickets compact one chunk each (their
+// look-back only waits for lower tickets, which started first and publish without waiting), the
+// rest write the prefix / suffix rows.
+template <int KPT>
+__global__ __launch_bounds__(kQThreads) void gate_compact_kernel(SelArgs a) {
+  __shared__ SelShared sh;
+  if (threadIdx.x == 0)
+    sh.flag = (int)__hip_atomic_fetch_add(a.glob + GL_TICKET, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const int ticket = sh.flag;
+  if (ticket < a.n_sel) {
+    Chunk<KPT> c;
+    c.init(a, ticket);
+    compact_chunk<KPT>(a, c, sh, false);
+  } else {
+    write_meta_rows(a, ticket - a.n_sel);
+  }
+  exit_reset(a, sh, false);
+}
+
+// One launch for batches whose chunk workgroups all fit the chip at once (n_sel at most the CU
+// count; the host checks): workgroups 0 .. n_sel-1 are the chunks, in sequence order, the rest
+// write the prefix / suffix rows and wait for nothing.  A chunk keeps its keys in registers
+// through the phases; between phases the chunks of a sequence wait for the phase flag that the
+// sequence's last arrival raises after writing its results (a bounded spin: on expiry the error
+// word is set and the chunk goes on, so every workgroup finishes whatever happens).  The pass-1
+// last arrival resolves T, the quotas and every chunk's output offset itself when digit B1 holds
+// at most kQLdsCand keys and raises the flag straight to 3: the chunks then skip pass 2 and compact
+// without the look-back.
+__device__ __forceinline__ uint32_t wait_flag(const SelArgs &a, const uint32_t *flag, uint32_t want, int *s_val) {
+  if (threadIdx.x == 0) {
+    int it = 0;
+    uint32_t v;
+    while ((v = __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < want) {
+      if (++it > a.spin_limit) {
+        __hip_atomic_store(a.glob + GL_ERROR, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v = want;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    *s_val = (int)v;
+  }
+  __syncthreads();
+  return (uint32_t)*s_val;
+}
+
+// Publish the last arrival's results (stores of this workgroup, complete before the barrier) and
+// raise the sequence's phase flag.
+__device__ __forceinline__ void raise_flag(uint32_t *flag, uint32_t value) {
+  stores_done_barrier();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Pass 1 of the one-launch form, every chunk: the histogram of its keys' top 12 bits published as
+// descending cumulative counts (cex[b]: keys of the chunk in bins above b), and its keys ordered by
+// that digit, descending (bin b's keys at cex[b] .. cex[b-1] - 1), for the sequence's last arrival.
+template <int KPT>
+__device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh,
+                                                   uint32_t *stage) {
+  constexpr int PER = kQBins1 / kQThreads;   // 8 bins per thread
+  constexpr int CHUNK = Chunk<KPT>::CHUNK;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kQBins1; i += kQThreads) sh.hist[i] = 0u;
+  __syncthreads();
+  uint32_t rank[KPT];                        // each key's place among the chunk's keys of its bin
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) rank[i] = (c.valid >> i & 1u) ? atomicAdd(&sh.hist[c.key[i] >> 20], 1u) : 0u;
+  float ssq = c.ssq;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) ssq += __shfl_xor(ssq, o);
+  if ((tid & 63) == 0) sh.r2[tid >> 6] = ssq;
+  __syncthreads();
+  const int bin0 = kQBins1 - PER * (tid + 1);     // this thread's bins bin0 .. bin0+PER-1 (descending threads)
+  uint32_t h[PER];
+  int mine = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    h[j] = sh.hist[bin0 + j];
+    mine += (int)h[j];
+  }
+  int nvalid;
+  uint32_t run = (uint32_t)q_scan(mine, sh.w, nvalid);   // keys in the bins of lower threads (higher bins)
+  uint32_t cx[PER];
+#pragma unroll
+  for (int j = PER - 1; j >= 0; --j) {
+    cx[j] = run;
+    run += h[j];
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sh.hist[bin0 + j] = cx[j];
+  u32x4 *gh = reinterpret_cast<u32x4 *>(a.hist1 + (int64_t)c.gc * kQBins1 + bin0);
+  gh[0] = u32x4{cx[0], cx[1], cx[2], cx[3]};
+  gh[1] = u32x4{cx[4], cx[5], cx[6], cx[7]};
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < KPT; ++i)
+    if (c.valid >> i & 1u) stage[sh.hist[c.key[i] >> 20] + rank[i]] = c.key[i];
+  __syncthreads();
+  uint32_t *dst = a.sorted + (int64_t)c.gc * CHUNK;
+  for (int i = 4 * tid; i < nvalid; i += 4 * kQThreads)
+    *reinterpret_cast<u32x4 *>(dst + i) = *reinterpret_cast<const u32x4 *>(stage + i);
+  if (tid == 0) {
+    float sq = 0.f;
+    for (int i = 0; i < kQWaves; ++i) sq += sh.r2[i];
+    a.chunk[(int64_t)c.gc * kQChunkWords + CK_SUMSQ] = __builtin_bit_cast(uint32_t, sq);
+  }
+}
+
+// Pass 1 of the one-launch form, the sequence's last arrival: the chunks' cumulative counts summed
+// (CEX[b]: the sequence's keys above bin b), digit B1 = the bin with CEX[B1] < K_c <= CEX[B1 - 1],
+// the keys of B1 (sh.cnt) and above it (sh.above), the normaliser.
+template <int KPT>
+__device__ __forceinline__ void pass1_last_sorted(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
+  constexpr int PER = kQBins1 / kQThreads;
+  const int tid = threadIdx.x;
+  const int bin0 = kQBins1 - PER * (tid + 1);
+  uint32_t tv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) tv[j] = 0u;
+  {
+    const uint32_t *hb = a.hist1 + (int64_t)c.g0 * kQBins1 + bin0;
+    int w = 0;
+    for (; w + 4 <= c.G; w += 4) {      // four chunks' loads in flight at once
+      u32x4 x[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        x[2 * q] = reinterpret_cast<const u32x4 *>(hb + (int64_t)(w + q) * kQBins1)[0];
+        x[2 * q + 1] = reinterpret_cast<const u32x4 *>(hb + (int64_t)(w + q) * kQBins1)[1];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          tv[j] += x[2 * q][j];
+          tv[4 + j] += x[2 * q + 1][j];
+        }
+    }
+    for (; w < c.G; ++w) {
+      const u32x4 x0 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[0];
+      const u32x4 x1 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tv[j] += x0[j];
+        tv[4 + j] += x1[j];
+      }
+    }
+  }
+  if (tid < c.G) sh.r2c[tid] = __builtin_bit_cast(float, a.chunk[(int64_t)(c.g0 + tid) * kQChunkWords + CK_SUMSQ]);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sh.hist[bin0 + j] = tv[j];
+  __syncthreads();
+  const uint32_t kc = (uint32_t)c.kc;
+  const uint32_t ge0 = bin0 > 0 ? sh.hist[bin0 - 1] : (uint32_t)c.n;     // keys at or above bin bin0
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t ge = j > 0 ? tv[j - 1] : ge0;                           // keys at or above bin bin0 + j
+    if (tv[j] < kc && kc <= ge) {
+      sh.d = bin0 + j;
+      sh.cnt = (int)(ge - tv[j]);
+      sh.above = (int)tv[j];
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float sq = 0.f;
+    for (int w = 0; w < c.G; ++w) sq += sh.r2c[w];
+    c.sq_rec[SQ_B1] = (uint32_t)sh.d;
+    c.sq_rec[SQ_R1] = (uint32_t)(c.kc - sh.above);
+    c.sq_rec[SQ_RNORM] = __builtin_bit_cast(uint32_t, rsqrtf(sq / (float)c.n + a.eps));
+    c.sq_rec[SQ_CNT1] = 0u;           // every chunk has arrived: reset for the next call
+  }
+}
+
+// Pass-1 last arrival of the one-launch form, when digit B1 holds at most kQLdsCand keys: those
+// keys, read from the chunks' ordered lists, resolve T, the ties still needed and each chunk's quota
+// in LDS -- what pass2_last writes, without a second pass over the chunks.
+template <int KPT>
+__device__ void resolve_in_lds(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh, uint32_t *ckey,
+                               uint32_t *cchunk) {
+  constexpr int CHUNK = Chunk<KPT>::CHUNK;
+  constexpr int UNROLL = kQLdsCand / kQThreads;
+  const int tid = threadIdx.x;
+  const uint32_t B1 = (uint32_t)sh.d;
+  const int r1 = c.kc - sh.above;
+  // each chunk's range of digit-B1 keys in its ordered list, and where it goes in LDS
+  if (tid < 64) {
+    int lo = 0, len = 0;
+    if (tid < c.G) {
+      const uint32_t *cw = a.hist1 + (int64_t)(c.g0 + tid) * kQBins1;
+      lo = (int)cw[B1];
+      len = (B1 > 0 ? (int)cw[B1 - 1] : min(CHUNK, c.n - tid * CHUNK)) - lo;
+    }
+    const int incl = wave_incl_scan(len);
+    if (tid < c.G) {
+      sh.coff[tid] = incl - len;
+      sh.clo[tid] = lo;
+      sh.tie[tid] = 0;
+      sh.gt[tid] = 0;
+    }
+    if (tid == 63) sh.ctot = incl;
+  }
+  for (int i = tid; i < kQBins2; i += kQThreads) sh.hist[i] = 0u;
+  __syncthreads();
+  const int nc = min(sh.ctot, kQLdsCand);
+  if (nc > 0) {
+    const int rounds = (nc + kQThreads - 1) / kQThreads;
+    uint32_t kk[UNROLL];
+    int wk[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {   // every load in flight at once (indices past nc repeat the last)
+      if (u >= rounds) break;
+      const int i = min(tid + u * kQThreads, nc - 1);
+      int lo = 0, hi = c.G - 1;          // the last chunk whose range starts at or before i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (sh.coff[mid] <= i) lo = mid; else hi = mid - 1;
+      }
+      wk[u] = lo;
+      kk[u] = a.sorted[(int64_t)(c.g0 + lo) * CHUNK + sh.clo[lo] + (i - sh.coff[lo])];
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (u >= rounds) break;
+      const int i = tid + u * kQThreads;
+      if (i < nc) {
+        ckey[i] = kk[u];
+        cchunk[i] = (uint32_t)wk[u];
+      }
+    }
+  }
+  __syncthreads();
+  // digit B2 (bits 19..9) among them
+  for (int i = tid; i < nc; i += kQThreads) atomicAdd(&sh.hist[(ckey[i] >> 9) & (kQBins2 - 1)], 1u);
+  __syncthreads();
+  constexpr int PER = kQBins2 / kQThreads;
+  const int bin0 = kQBins2 - PER * (tid + 1);
+  uint32_t tv[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) tv[j] = sh.hist[bin0 + j];
+  find_digit<PER>(tv, bin0, r1, sh.w, &sh.d, &sh.cnt, &sh.above);
+  const uint32_t pre = (B1 << 11) | (uint32_t)sh.d;
+  const int r2 = r1 - sh.above;
+  for (int i = tid; i < kQBins3; i += kQThreads) sh.hist[i] = 0u;
+  __syncthreads();
+  // the last digit (bits 8..0) among the keys of prefix B1.B2
+  for (int i = tid; i < nc; i += kQThreads) {
+    const uint32_t k = ckey[i];
+    if ((k >> 9) == pre) atomicAdd(&sh.hist[k & (kQBins3 - 1)], 1u);
+  }
+  __syncthreads();
+  uint32_t tv3[1] = {sh.hist[kQBins3 - 1 - tid]};
+  find_digit<1>(tv3, kQBins3 - 1 - tid, r2, sh.w, &sh.d, &sh.cnt, &sh.above);
+  const uint32_t T = (pre << 9) | (uint32_t)sh.d;
+  const int rT = r2 - sh.above;                       // ties of T still needed
+  for (int i = tid; i < nc; i += kQThreads) {
+    const uint32_t k = ckey[i];
+    if (k >= T) atomicAdd(k == T ? &sh.tie[cchunk[i]] : &sh.gt[cchunk[i]], 1);
+  }
+  __syncthreads();
+  // each chunk's quota of ties (lowest positions first) and output offset: its keys above digit B1,
+  // its digit-B1 keys above T and its quota, summed over the chunks before it
+  if (tid == 0) {
+    int tb = 0, off = 0;
+    for (int w = 0; w < c.G; ++w) {       // chunks in position order
+      const int q = max(0, min(sh.tie[w], rT - tb));
+      tb += sh.tie[w];
+      uint32_t *ck = a.chunk + (int64_t)(c.g0 + w) * kQChunkWords;
+      ck[CK_QUOTA] = (uint32_t)q;
+      ck[CK_OFF] = (uint32_t)off;
+      off += sh.clo[w] + sh.gt[w] + q;
+    }
+    c.sq_rec[SQ_T] = T;
+  }
+}
+
+template <int KPT>
+__global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a) {
+  constexpr int POOL = KPT * kQThreads > 2 * kQLdsCand ? KPT * kQThreads : 2 * kQLdsCand;
+  __shared__ SelShared sh;
+  __shared__ __align__(16) uint32_t pool[POOL];     // pass 1: the ordered keys; then the digit-B1 keys
+  if ((int)blockIdx.x >= a.n_sel) {
+    write_meta_rows(a, (int64_t)blockIdx.x - a.n_sel);
+    exit_reset(a, sh, true);
+    return;
+  }
+  Chunk<KPT> c;
+  c.init(a, blockIdx.x);
+  uint32_t *flag = c.sq_rec + SQ_FLAG;
+  pass1_chunk_sorted<KPT>(a, c, sh, pool);
+  if (arrive_last(c.sq_rec + SQ_CNT1, c.G, &sh.flag)) {
+    pass1_last_sorted<KPT>(a, c, sh);
+    // phase 3 when T and the offsets are resolved here (digit B1 small enough for LDS), else
+    // phase 1: pass 2 runs, then phase 2 and the compaction's look-back
+    const bool in_lds = sh.cnt <= kQLdsCand;
+    if (in_lds) resolve_in_lds<KPT>(a, c, sh, pool, pool + kQLdsCand);
+    raise_flag(flag, in_lds ? 3u : 1u);
+  }
+  const bool resolved = wait_flag(a, flag, 1u, &sh.flag) == 3u;
+  if (!resolved) {
+    pass2_chunk<KPT>(a, c, sh);
+    if (arrive_last(c.sq_rec + SQ_CNT2, c.G, &sh.flag)) {
+      pass2_last<KPT>(a, c, sh);
+      raise_flag(flag, 2u);
+    }
+    wait_flag(a, flag, 2u, &sh.flag);
+  }
+  compact_chunk<KPT>(a, c, sh, resolved);
+  exit_reset(a, sh, true);
+}
+
 // Workspace layout for up to seq_cap sequences and chunk_cap chunks.  The counters that must be
 // zero when a call starts (global words, per-sequence records) come first at offsets that depend
 // only on the capacities, so calls of any size within them find the counters the previous call
 // left zeroed.
-int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[6]) {
+int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[7]) {
   int64_t o = 0;
   auto take = [&](int64_t bytes) { const int64_t r = o; o += (bytes + 255) / 256 * 256; return r; };
   off[0] = take(64 * 4);                                       // global words
@@ -555,11 +909,16 @@ int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[6]) {
   off[3] = take((int64_t)chunk_cap * kQBins1 * 4);             // hist1
   off[4] = take((int64_t)chunk_cap * kQBins2 * 4);             // hist2
   off[5] = take((int64_t)seq_cap * kQCap * 8);                 // candidates
+  off[6] = take((int64_t)std::min(chunk_cap, kQFusedMaxChunks) * kQMaxChunkKeys * 4);   // ordered keys
   return o;
 }
 
 template <int KPT>
-void launch_select(const SelArgs &a, int grid, hipStream_t stream) {
+void launch_select(const SelArgs &a, int grid, bool fused, hipStream_t stream) {
+  if (fused) {
+    hipLaunchKernelGGL(gate_select_fused_kernel<KPT>, dim3(grid), dim3(kQThreads), 0, stream, a);
+    return;
+  }
   hipLaunchKernelGGL(gate_select1_kernel<KPT>, dim3(a.n_sel), dim3(kQThreads), 0, stream, a);
   hipLaunchKernelGGL(gate_select2_kernel<KPT>, dim3(a.n_sel), dim3(kQThreads), 0, stream, a);
   hipLaunchKernelGGL(gate_compact_kernel<KPT>, dim3(grid), dim3(kQThreads), 0, stream, a);
@@ -572,7 +931,7 @@ using namespace tg;
 
 extern "C" int64_t tg_gate_select_pack_workspace_size(int32_t seq_capacity, int32_t chunk_capacity) {
   if (seq_capacity <= 0 || chunk_capacity < 0) return 0;
-  int64_t off[6];
+  int64_t off[7];
   return ws_layout(seq_capacity, chunk_capacity, off);
 }
 
@@ -596,7 +955,7 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   TG_CHECK((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
   const int64_t meta_wgs = (total_kept + kQThreads - 1) / kQThreads;   // prefix / suffix rows, 512 per workgroup
   TG_CHECK((int64_t)n_select_wgs + meta_wgs < (1ll << 31), "grid too large");
-  int64_t off[6];
+  int64_t off[7];
   ws_layout(seq_capacity, chunk_capacity, off);
   SelArgs a{};
   a.scores = scores;
@@ -616,15 +975,19 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   a.hist1 = reinterpret_cast<uint32_t *>(w + off[3]);
   a.hist2 = reinterpret_cast<uint32_t *>(w + off[4]);
   a.cand = reinterpret_cast<uint32_t *>(w + off[5]);
+  a.sorted = reinterpret_cast<uint32_t *>(w + off[6]);
   a.spin_limit = 1 << 22;
   const int grid = (int)(n_select_wgs + meta_wgs);
+  // one launch when every chunk workgroup fits the chip at once (its waits are for chunks of the
+  // same sequence, which must be resident); three otherwise
+  const bool fused = n_select_wgs <= std::min(device_cus(), std::min(chunk_capacity, kQFusedMaxChunks));
   if (n_select_wgs == 0) {
     hipLaunchKernelGGL(gate_compact_kernel<8>, dim3(grid), dim3(kQThreads), 0, stream, a);
   } else {
     switch (keys_per_thread) {
-      case 8: launch_select<8>(a, grid, stream); break;
-      case 16: launch_select<16>(a, grid, stream); break;
-      default: launch_select<32>(a, grid, stream); break;
+      case 8: launch_select<8>(a, grid, fused, stream); break;
+      case 16: launch_select<16>(a, grid, fused, stream); break;
+      default: launch_select<32>(a, grid, fused, stream); break;
     }
   }
   TG_HIP_CHECK(hipPeekAtLastError());
