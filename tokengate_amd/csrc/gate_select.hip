@@ -59,7 +59,7 @@ constexpr int kQSeqWords = 16;         // per-sequence record
 constexpr int kQChunkWords = 8;        // per-chunk record
 
 // per-sequence record words
-enum { SQ_CNT1 = 0, SQ_CNT2, SQ_CAND, SQ_B1, SQ_R1, SQ_T, SQ_RNORM, SQ_FLAG };   // SQ_FLAG: one-launch phase
+enum { SQ_CNT1 = 0, SQ_CNT2, SQ_CAND, SQ_B1, SQ_R1, SQ_T, SQ_RNORM, SQ_FLAG, SQ_DONE };   // SQ_FLAG, SQ_DONE: one-launch form
 // per-chunk record words
 enum { CK_SUMSQ = 0, CK_QUOTA, CK_AGG, CK_OFF };   // CK_AGG: zero, or kept count | 1 << 31 once published;
                                                  // CK_OFF: output offset (one-launch form, resolved in LDS)
@@ -173,6 +173,17 @@ __device__ __forceinline__ int q_scan(int v, int *s_w, int &total) {
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
+
+// Maximum over the 64 lanes of a wave of non-negative ints (the same DPP network as wave_incl_scan).
+__device__ __forceinline__ int wave_max_nonneg(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false));
+  return __builtin_amdgcn_readlane(v, 63);
+}
 
 // Every wave's global stores have completed (reached L2) before the workgroup barrier, so that
 // the one agent-scope release issued after it (which writes L2 back for the other XCDs) covers
@@ -541,9 +552,9 @@ __device__ __forceinline__ void write_meta_rows(const SelArgs &a, int64_t mw) {
   }
 }
 
-// The workgroup that finishes last zeroes the compaction counters (and, in the one-launch form,
-// the sequences' phase flags): a zeroed workspace stays zeroed.
-__device__ __forceinline__ void exit_reset(const SelArgs &a, SelShared &sh, bool flags) {
+// Compaction launch: the workgroup that finishes last zeroes the tickets and the look-back words,
+// so that a zeroed workspace stays zeroed.
+__device__ __forceinline__ void exit_reset(const SelArgs &a, SelShared &sh) {
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t prev =
@@ -553,11 +564,28 @@ __device__ __forceinline__ void exit_reset(const SelArgs &a, SelShared &sh, bool
   __syncthreads();
   if (sh.flag) {
     for (int i = threadIdx.x; i < a.n_sel; i += kQThreads) a.chunk[(int64_t)i * kQChunkWords + CK_AGG] = 0u;
-    if (flags)
-      for (int i = threadIdx.x; i < a.nseq; i += kQThreads) a.seq[(int64_t)i * kQSeqWords + SQ_FLAG] = 0u;
     if (threadIdx.x == 0) {
       a.glob[GL_TICKET] = 0u;
       a.glob[GL_EXIT] = 0u;
+    }
+  }
+}
+
+// One-launch form: the chunk of a sequence that finishes last (its own counter) zeroes the
+// sequence's phase flag and its chunks' look-back words, so that a zeroed workspace stays zeroed.
+// Every chunk's reads of those words are complete here (their values were used), and the last
+// arrival of each pass finishes after raising the flag.
+__device__ __forceinline__ void seq_done(const SelArgs &a, uint32_t *sq_rec, int g0, int G, SelShared &sh) {
+  __syncthreads();
+  if (threadIdx.x == 0)
+    sh.flag = __hip_atomic_fetch_add(sq_rec + SQ_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (uint32_t)(G - 1);
+  __syncthreads();
+  if (sh.flag) {
+    for (int i = threadIdx.x; i < G; i += kQThreads) a.chunk[(int64_t)(g0 + i) * kQChunkWords + CK_AGG] = 0u;
+    if (threadIdx.x == 0) {
+      sq_rec[SQ_FLAG] = 0u;
+      sq_rec[SQ_DONE] = 0u;
     }
   }
 }
@@ -598,7 +626,7 @@ __global__ __launch_bounds__(kQThreads) void gate_compact_kernel(SelArgs a) {
   } else {
     write_meta_rows(a, ticket - a.n_sel);
   }
-  exit_reset(a, sh, false);
+  exit_reset(a, sh);
 }
 
 // One launch for batches whose chunk workgroups all fit the chip at once (n_sel at most the CU
@@ -642,6 +670,9 @@ __device__ __forceinline__ void raise_flag(uint32_t *flag, uint32_t value) {
 // Pass 1 of the one-launch form, every chunk: the histogram of its keys' top 12 bits published as
 // descending cumulative counts (cex[b]: keys of the chunk in bins above b), and its keys ordered by
 // that digit, descending (bin b's keys at cex[b] .. cex[b-1] - 1), for the sequence's last arrival.
+// Only the bins with cex[b] < K_c are written: T is at least the chunk's own K_c-th largest key
+// (the chunk alone holds K_c keys at or above it), so digit B1 is at least that key's bin, the
+// lowest such bin.
 template <int KPT>
 __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh,
                                                    uint32_t *stage) {
@@ -649,6 +680,7 @@ __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk
   constexpr int CHUNK = Chunk<KPT>::CHUNK;
   const int tid = threadIdx.x;
   for (int i = tid; i < kQBins1; i += kQThreads) sh.hist[i] = 0u;
+  if (tid == 0) sh.base = 0;
   __syncthreads();
   uint32_t rank[KPT];                        // each key's place among the chunk's keys of its bin
 #pragma unroll
@@ -680,12 +712,21 @@ __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk
   gh[0] = u32x4{cx[0], cx[1], cx[2], cx[3]};
   gh[1] = u32x4{cx[4], cx[5], cx[6], cx[7]};
   __syncthreads();
+  int nwrite = 0;                            // the written prefix: keys of the bins with cex < K_c
 #pragma unroll
-  for (int i = 0; i < KPT; ++i)
-    if (c.valid >> i & 1u) stage[sh.hist[c.key[i] >> 20] + rank[i]] = c.key[i];
+  for (int i = 0; i < KPT; ++i) {
+    const uint32_t first = sh.hist[c.key[i] >> 20];
+    if ((c.valid >> i & 1u) && first < (uint32_t)c.kc) {
+      stage[first + rank[i]] = c.key[i];
+      nwrite = max(nwrite, (int)(first + rank[i]) + 1);
+    }
+  }
+  nwrite = wave_max_nonneg(nwrite);
+  if ((tid & 63) == 0 && nwrite) atomicMax(&sh.base, nwrite);
   __syncthreads();
+  nwrite = sh.base;
   uint32_t *dst = a.sorted + (int64_t)c.gc * CHUNK;
-  for (int i = 4 * tid; i < nvalid; i += 4 * kQThreads)
+  for (int i = 4 * tid; i < nwrite; i += 4 * kQThreads)
     *reinterpret_cast<u32x4 *>(dst + i) = *reinterpret_cast<const u32x4 *>(stage + i);
   if (tid == 0) {
     float sq = 0.f;
@@ -846,18 +887,20 @@ __device__ void resolve_in_lds(const SelArgs &a, const Chunk<KPT> &c, SelShared 
   }
   __syncthreads();
   // each chunk's quota of ties (lowest positions first) and output offset: its keys above digit B1,
-  // its digit-B1 keys above T and its quota, summed over the chunks before it
-  if (tid == 0) {
-    int tb = 0, off = 0;
-    for (int w = 0; w < c.G; ++w) {       // chunks in position order
-      const int q = max(0, min(sh.tie[w], rT - tb));
-      tb += sh.tie[w];
-      uint32_t *ck = a.chunk + (int64_t)(c.g0 + w) * kQChunkWords;
+  // its digit-B1 keys above T and its quota, summed over the chunks before it (wave 0, a lane per
+  // chunk in position order)
+  if (tid < 64) {
+    const bool in = tid < c.G;
+    const int tie = in ? sh.tie[tid] : 0;
+    const int q = in ? max(0, min(tie, rT - (wave_incl_scan(tie) - tie))) : 0;
+    const int kept = in ? sh.clo[tid] + sh.gt[tid] + q : 0;
+    const int off = wave_incl_scan(kept) - kept;
+    if (in) {
+      uint32_t *ck = a.chunk + (int64_t)(c.g0 + tid) * kQChunkWords;
       ck[CK_QUOTA] = (uint32_t)q;
       ck[CK_OFF] = (uint32_t)off;
-      off += sh.clo[w] + sh.gt[w] + q;
     }
-    c.sq_rec[SQ_T] = T;
+    if (tid == 0) c.sq_rec[SQ_T] = T;
   }
 }
 
@@ -866,9 +909,8 @@ __global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a)
   constexpr int POOL = KPT * kQThreads > 2 * kQLdsCand ? KPT * kQThreads : 2 * kQLdsCand;
   __shared__ SelShared sh;
   __shared__ __align__(16) uint32_t pool[POOL];     // pass 1: the ordered keys; then the digit-B1 keys
-  if ((int)blockIdx.x >= a.n_sel) {
+  if ((int)blockIdx.x >= a.n_sel) {      // prefix / suffix rows: no counters, no waits
     write_meta_rows(a, (int64_t)blockIdx.x - a.n_sel);
-    exit_reset(a, sh, true);
     return;
   }
   Chunk<KPT> c;
@@ -893,7 +935,7 @@ __global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a)
     wait_flag(a, flag, 2u, &sh.flag);
   }
   compact_chunk<KPT>(a, c, sh, resolved);
-  exit_reset(a, sh, true);
+  seq_done(a, c.sq_rec, c.g0, c.G, sh);
 }
 
 // Workspace layout for up to seq_cap sequences and chunk_cap chunks.  The counters that must be
