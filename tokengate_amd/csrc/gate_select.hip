@@ -54,6 +54,7 @@ constexpr int kQCap = 16384;           // candidate buffer per sequence (key, po
 constexpr int kQLdsCand = 4096;        // digit-B1 keys the one-launch form resolves in LDS
 constexpr int kQFusedMaxChunks = 512;  // chunk workgroups of the one-launch form (at most one per CU)
 constexpr int kQMaxChunkKeys = 32 * kQThreads;
+constexpr int kQGroups = kQBins1 / 16;   // one-launch form: coarse groups of 16 top-digit bins
 constexpr int kQMaxStreams = 16;
 constexpr int kQSeqWords = 16;         // per-sequence record
 constexpr int kQChunkWords = 8;        // per-chunk record
@@ -95,6 +96,7 @@ struct SelArgs {
   uint32_t *hist2;           // (n_sel, kQBins2)
   uint32_t *cand;            // (nseq, kQCap, 2)
   uint32_t *sorted;          // one-launch form: (n_sel, 512 * KPT) each chunk's keys by top digit, descending
+  uint32_t *coarse;          // one-launch form: (n_sel, kQGroups) each chunk's keys above each group of 16 bins
   int spin_limit;
 };
 
@@ -711,6 +713,8 @@ __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk
   u32x4 *gh = reinterpret_cast<u32x4 *>(a.hist1 + (int64_t)c.gc * kQBins1 + bin0);
   gh[0] = u32x4{cx[0], cx[1], cx[2], cx[3]};
   gh[1] = u32x4{cx[4], cx[5], cx[6], cx[7]};
+  // the even threads own the top bin of a group of 16: keys above that group
+  if ((tid & 1) == 0) a.coarse[(int64_t)c.gc * kQGroups + (kQGroups - 1 - (tid >> 1))] = cx[PER - 1];
   __syncthreads();
   int nwrite = 0;                            // the written prefix: keys of the bins with cex < K_c
 #pragma unroll
@@ -735,58 +739,68 @@ __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk
   }
 }
 
-// Pass 1 of the one-launch form, the sequence's last arrival: the chunks' cumulative counts summed
-// (CEX[b]: the sequence's keys above bin b), digit B1 = the bin with CEX[B1] < K_c <= CEX[B1 - 1],
-// the keys of B1 (sh.cnt) and above it (sh.above), the normaliser.
+// Pass 1 of the one-launch form, the sequence's last arrival: digit B1 = the bin with
+// CEX[B1] < K_c <= CEX[B1 - 1], CEX[b] being the sequence's keys above bin b (the chunks' cumulative
+// counts summed), found in two steps -- the group of 16 bins from the chunks' coarse counts, then
+// the bin from that group's 16 counts of each chunk -- with the keys of B1 (sh.cnt) and above it
+// (sh.above), and the normaliser.
 template <int KPT>
 __device__ __forceinline__ void pass1_last_sorted(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
-  constexpr int PER = kQBins1 / kQThreads;
+  constexpr int UNROLL = 8;
   const int tid = threadIdx.x;
-  const int bin0 = kQBins1 - PER * (tid + 1);
-  uint32_t tv[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) tv[j] = 0u;
+  const uint32_t kc = (uint32_t)c.kc;
+  if (tid < c.G) sh.r2c[tid] = __builtin_bit_cast(float, a.chunk[(int64_t)(c.g0 + tid) * kQChunkWords + CK_SUMSQ]);
+  if (tid == 0) {                 // exactly one group and one bin qualify; these only keep indexes in range
+    sh.d = 0;
+    sh.above = 0;
+    sh.cnt = c.n;
+  }
+  // coarse: thread t sums group 255 - (t % 256) over the even (t < 256) or odd chunks
   {
-    const uint32_t *hb = a.hist1 + (int64_t)c.g0 * kQBins1 + bin0;
-    int w = 0;
-    for (; w + 4 <= c.G; w += 4) {      // four chunks' loads in flight at once
-      u32x4 x[8];
+    const int g = kQGroups - 1 - (tid & (kQGroups - 1)), half = tid >> 8;
+    const uint32_t *cb = a.coarse + (int64_t)c.g0 * kQGroups + g;
+    uint32_t acc = 0u;
+    for (int w0 = half; w0 < c.G; w0 += 2 * UNROLL) {
+      uint32_t x[UNROLL];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        x[2 * q] = reinterpret_cast<const u32x4 *>(hb + (int64_t)(w + q) * kQBins1)[0];
-        x[2 * q + 1] = reinterpret_cast<const u32x4 *>(hb + (int64_t)(w + q) * kQBins1)[1];
-      }
+      for (int u = 0; u < UNROLL; ++u) x[u] = cb[(int64_t)min(w0 + 2 * u, c.G - 1) * kQGroups];   // all in flight
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          tv[j] += x[2 * q][j];
-          tv[4 + j] += x[2 * q + 1][j];
-        }
+      for (int u = 0; u < UNROLL; ++u) acc += w0 + 2 * u < c.G ? x[u] : 0u;
     }
-    for (; w < c.G; ++w) {
-      const u32x4 x0 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[0];
-      const u32x4 x1 = reinterpret_cast<const u32x4 *>(hb + (int64_t)w * kQBins1)[1];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        tv[j] += x0[j];
-        tv[4 + j] += x1[j];
-      }
+    sh.hist[half * kQGroups + g] = acc;
+  }
+  __syncthreads();
+  if (tid < kQGroups) {
+    const int g = kQGroups - 1 - tid;
+    const uint32_t above = sh.hist[g] + sh.hist[kQGroups + g];                              // keys above group g
+    const uint32_t ge = g > 0 ? sh.hist[g - 1] + sh.hist[kQGroups + g - 1] : (uint32_t)c.n;  // keys at or above it
+    if (above < kc && kc <= ge) {
+      sh.d = g;
+      sh.above = (int)above;
+      sh.cnt = (int)ge;
     }
   }
-  if (tid < c.G) sh.r2c[tid] = __builtin_bit_cast(float, a.chunk[(int64_t)(c.g0 + tid) * kQChunkWords + CK_SUMSQ]);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) sh.hist[bin0 + j] = tv[j];
+  for (int i = tid; i < 16; i += kQThreads) sh.hist[2 * kQGroups + i] = 0u;
   __syncthreads();
-  const uint32_t kc = (uint32_t)c.kc;
-  const uint32_t ge0 = bin0 > 0 ? sh.hist[bin0 - 1] : (uint32_t)c.n;     // keys at or above bin bin0
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const uint32_t ge = j > 0 ? tv[j - 1] : ge0;                           // keys at or above bin bin0 + j
-    if (tv[j] < kc && kc <= ge) {
-      sh.d = bin0 + j;
-      sh.cnt = (int)(ge - tv[j]);
-      sh.above = (int)tv[j];
+  // fine: the 16 bins of group C, chunk t / 16 (and t / 16 + 32), bin t % 16
+  const int C = min(max(sh.d, 0), kQGroups - 1);
+  const uint32_t ge_group = (uint32_t)sh.cnt;
+  {
+    const int j = tid & 15;
+    uint32_t v = 0u;
+    for (int w = tid >> 4; w < c.G; w += kQThreads / 16) v += a.hist1[(int64_t)(c.g0 + w) * kQBins1 + 16 * C + j];
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    if ((tid & 63) < 16) atomicAdd(&sh.hist[2 * kQGroups + j], v);
+  }
+  __syncthreads();
+  if (tid < 16) {
+    const uint32_t above = sh.hist[2 * kQGroups + tid];
+    const uint32_t ge = tid > 0 ? sh.hist[2 * kQGroups + tid - 1] : ge_group;
+    if (above < kc && kc <= ge) {
+      sh.d = 16 * C + tid;
+      sh.cnt = (int)(ge - above);
+      sh.above = (int)above;
     }
   }
   __syncthreads();
@@ -816,8 +830,8 @@ __device__ void resolve_in_lds(const SelArgs &a, const Chunk<KPT> &c, SelShared 
     int lo = 0, len = 0;
     if (tid < c.G) {
       const uint32_t *cw = a.hist1 + (int64_t)(c.g0 + tid) * kQBins1;
-      lo = (int)cw[B1];
-      len = (B1 > 0 ? (int)cw[B1 - 1] : min(CHUNK, c.n - tid * CHUNK)) - lo;
+      lo = min((int)cw[B1], CHUNK);   // (the bounds hold by construction; they keep every read in range)
+      len = min(max((B1 > 0 ? (int)cw[B1 - 1] : min(CHUNK, c.n - tid * CHUNK)) - lo, 0), CHUNK - lo);
     }
     const int incl = wave_incl_scan(len);
     if (tid < c.G) {
@@ -942,7 +956,7 @@ __global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a)
 // zero when a call starts (global words, per-sequence records) come first at offsets that depend
 // only on the capacities, so calls of any size within them find the counters the previous call
 // left zeroed.
-int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[7]) {
+int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[8]) {
   int64_t o = 0;
   auto take = [&](int64_t bytes) { const int64_t r = o; o += (bytes + 255) / 256 * 256; return r; };
   off[0] = take(64 * 4);                                       // global words
@@ -952,6 +966,7 @@ int64_t ws_layout(int32_t seq_cap, int32_t chunk_cap, int64_t off[7]) {
   off[4] = take((int64_t)chunk_cap * kQBins2 * 4);             // hist2
   off[5] = take((int64_t)seq_cap * kQCap * 8);                 // candidates
   off[6] = take((int64_t)std::min(chunk_cap, kQFusedMaxChunks) * kQMaxChunkKeys * 4);   // ordered keys
+  off[7] = take((int64_t)std::min(chunk_cap, kQFusedMaxChunks) * kQGroups * 4);         // coarse counts
   return o;
 }
 
@@ -973,7 +988,7 @@ using namespace tg;
 
 extern "C" int64_t tg_gate_select_pack_workspace_size(int32_t seq_capacity, int32_t chunk_capacity) {
   if (seq_capacity <= 0 || chunk_capacity < 0) return 0;
-  int64_t off[7];
+  int64_t off[8];
   return ws_layout(seq_capacity, chunk_capacity, off);
 }
 
@@ -997,7 +1012,7 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   TG_CHECK((reinterpret_cast<uintptr_t>(workspace) & 255) == 0, "workspace must be 256-byte aligned");
   const int64_t meta_wgs = (total_kept + kQThreads - 1) / kQThreads;   // prefix / suffix rows, 512 per workgroup
   TG_CHECK((int64_t)n_select_wgs + meta_wgs < (1ll << 31), "grid too large");
-  int64_t off[7];
+  int64_t off[8];
   ws_layout(seq_capacity, chunk_capacity, off);
   SelArgs a{};
   a.scores = scores;
@@ -1018,6 +1033,7 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   a.hist2 = reinterpret_cast<uint32_t *>(w + off[4]);
   a.cand = reinterpret_cast<uint32_t *>(w + off[5]);
   a.sorted = reinterpret_cast<uint32_t *>(w + off[6]);
+  a.coarse = reinterpret_cast<uint32_t *>(w + off[7]);
   a.spin_limit = 1 << 22;
   const int grid = (int)(n_select_wgs + meta_wgs);
   // one launch when every chunk workgroup fits the chip at once (its waits are for chunks of the
