@@ -176,6 +176,21 @@ __device__ __forceinline__ int q_scan(int v, int *s_w, int &total) {
 
 __device__ __forceinline__ int wave_sum_i(int v) { return __builtin_amdgcn_readlane(wave_incl_scan(v), 63); }
 
+// Sum over the 64 lanes of a wave (the same DPP network as wave_incl_scan; lane 63 ends with it).
+template <int CTRL, int ROWS, bool BOUND>
+__device__ __forceinline__ float dpp_add_f(float x) {
+  return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROWS, 0xf, BOUND));
+}
+__device__ __forceinline__ float wave_sum_f(float v) {
+  v = dpp_add_f<0x111, 0xf, true>(v);    // row_shr:1
+  v = dpp_add_f<0x112, 0xf, true>(v);    // row_shr:2
+  v = dpp_add_f<0x114, 0xf, true>(v);    // row_shr:4
+  v = dpp_add_f<0x118, 0xf, true>(v);    // row_shr:8
+  v = dpp_add_f<0x142, 0xa, false>(v);   // row_bcast:15 into rows 1, 3
+  v = dpp_add_f<0x143, 0xc, false>(v);   // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // Maximum over the 64 lanes of a wave of non-negative ints (the same DPP network as wave_incl_scan).
 __device__ __forceinline__ int wave_max_nonneg(int v) {
   v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true));
@@ -681,16 +696,12 @@ __device__ __forceinline__ void pass1_chunk_sorted(const SelArgs &a, const Chunk
   constexpr int PER = kQBins1 / kQThreads;   // 8 bins per thread
   constexpr int CHUNK = Chunk<KPT>::CHUNK;
   const int tid = threadIdx.x;
-  for (int i = tid; i < kQBins1; i += kQThreads) sh.hist[i] = 0u;
-  if (tid == 0) sh.base = 0;
-  __syncthreads();
+  // (sh.hist and sh.base were zeroed, and the workgroup synchronised, before the keys were loaded)
   uint32_t rank[KPT];                        // each key's place among the chunk's keys of its bin
 #pragma unroll
   for (int i = 0; i < KPT; ++i) rank[i] = (c.valid >> i & 1u) ? atomicAdd(&sh.hist[c.key[i] >> 20], 1u) : 0u;
-  float ssq = c.ssq;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) ssq += __shfl_xor(ssq, o);
-  if ((tid & 63) == 0) sh.r2[tid >> 6] = ssq;
+  const float wsq = wave_sum_f(c.ssq);       // read by thread 0 after the barriers below
+  if ((tid & 63) == 0) sh.r2[tid >> 6] = wsq;
   __syncthreads();
   const int bin0 = kQBins1 - PER * (tid + 1);     // this thread's bins bin0 .. bin0+PER-1 (descending threads)
   uint32_t h[PER];
@@ -927,6 +938,9 @@ __global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a)
     write_meta_rows(a, (int64_t)blockIdx.x - a.n_sel);
     return;
   }
+  for (int i = threadIdx.x; i < kQBins1; i += kQThreads) sh.hist[i] = 0u;   // pass 1's histogram, while
+  if (threadIdx.x == 0) sh.base = 0;                                         // the keys load
+  __syncthreads();
   Chunk<KPT> c;
   c.init(a, blockIdx.x);
   uint32_t *flag = c.sq_rec + SQ_FLAG;
@@ -939,16 +953,26 @@ __global__ __launch_bounds__(kQThreads) void gate_select_fused_kernel(SelArgs a)
     if (in_lds) resolve_in_lds<KPT>(a, c, sh, pool, pool + kQLdsCand);
     raise_flag(flag, in_lds ? 3u : 1u);
   }
-  const bool resolved = wait_flag(a, flag, 1u, &sh.flag) == 3u;
-  if (!resolved) {
-    pass2_chunk<KPT>(a, c, sh);
-    if (arrive_last(c.sq_rec + SQ_CNT2, c.G, &sh.flag)) {
-      pass2_last<KPT>(a, c, sh);
-      raise_flag(flag, 2u);
+  if (wait_flag(a, flag, 1u, &sh.flag) == 3u) {
+    // resolved: the flag is not read again and the look-back words not at all, so the chunk counts
+    // itself done now (the count's latency hides behind the compaction); the last one resets
+    uint32_t prev = 0u;
+    if (threadIdx.x == 0)
+      prev = __hip_atomic_fetch_add(c.sq_rec + SQ_DONE, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    compact_chunk<KPT>(a, c, sh, true);
+    if (threadIdx.x == 0 && prev == (uint32_t)(c.G - 1)) {
+      c.sq_rec[SQ_FLAG] = 0u;
+      c.sq_rec[SQ_DONE] = 0u;
     }
-    wait_flag(a, flag, 2u, &sh.flag);
+    return;
   }
-  compact_chunk<KPT>(a, c, sh, resolved);
+  pass2_chunk<KPT>(a, c, sh);
+  if (arrive_last(c.sq_rec + SQ_CNT2, c.G, &sh.flag)) {
+    pass2_last<KPT>(a, c, sh);
+    raise_flag(flag, 2u);
+  }
+  wait_flag(a, flag, 2u, &sh.flag);
+  compact_chunk<KPT>(a, c, sh, false);
   seq_done(a, c.sq_rec, c.g0, c.G, sh);
 }
 
