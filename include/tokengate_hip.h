@@ -225,7 +225,9 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
 
 /* tg_gate_topk_keep then tg_gate_pack, with the keep lists selected by many workgroups per
  * sequence (the reference's per-sample score -> topk -> sort -> cat -> index_select loop,
- * gate_forward.py:1396-1522, for a whole ragged batch); four stream-ordered launches.  Sequence
+ * gate_forward.py:1396-1522, for a whole ragged batch); two stream-ordered launches (the
+ * selection, then the gather) when n_select_wgs is at most the device's CU count, 512 and
+ * chunk_capacity, four above (three selection launches).  Sequence
  * b's state span is cut into chunks of 512 * keys_per_thread scores (keys_per_thread 8, 16 or 32)
  * selected by one workgroup each: wg_start (num_seqs + 1, int32, device) lists them, sequence b
  * owning chunks [wg_start[b], wg_start[b + 1]) (none when its span is empty, at most 64),
@@ -233,17 +235,21 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
  * tg_gate_topk_keep), positions_out = keep (optional), bias_out (optional) = the kept state rows'
  * scores times rsqrt(mean of the span's squared scores + rms_eps), 0 on prefix / suffix rows, and
  * every stream's rows gathered as tg_gate_pack does.  workspace:
- * tg_gate_select_pack_workspace_size(seq_capacity, chunk_capacity) bytes, 256-byte aligned,
+ * tg_gate_select_pack_workspace_size(seq_capacity, chunk_capacity) bytes (about 90 KB per
+ * chunk of capacity up to 512 and 25 KB per chunk beyond, plus 128 KB per sequence: 55 MB for
+ * 64 sequences and 512 chunks), 256-byte aligned,
  * zero-filled before its first use, for calls of at most seq_capacity sequences and
  * chunk_capacity chunks (every call on one workspace passes the same capacities: its layout
  * depends on them alone).  Every call leaves its counters zeroed again, so stream-ordered calls
  * reuse it without clearing; calls that overlap on one workspace race.  The 32-bit word at byte
  * offset 8 of the workspace is an error word that stays set until the caller clears it: 1 = a
- * look-back wait timed out, 2 = a chunk's count overran its sequence, 3 = the gather met a kept
- * position outside its sequence (a keep entry left unwritten) and skipped that row.  Nonzero means
- * the keep lists and gathered rows of the calls since it was last cleared are not to be used; no
- * row outside a sequence is ever read or written.  No workgroup waits for one that may not have
- * started: every call completes whatever the scheduling. */
+ * wait timed out, 2 = a chunk's count overran its sequence, 3 = the gather met a kept position
+ * outside its sequence (a keep entry left unwritten) and skipped that row.  Nonzero means the keep
+ * lists and gathered rows of the calls since it was last cleared are not to be used; no row outside
+ * a sequence is ever read or written.  Every wait is bounded (seconds), so every call completes.
+ * In the one-launch form the chunk workgroups of a sequence wait for one another: at most one per
+ * CU, they are resident together unless other work holds the CUs for longer than the bound (then
+ * error 1); in the three-launch form no workgroup waits for one that may not have started. */
 int tg_gate_select_pack(const float *scores, const int32_t *geom, const int32_t *wg_start, int32_t num_seqs,
                         int32_t n_select_wgs, int32_t keys_per_thread, const tg_pack_stream *streams,
                         int32_t n_streams, int64_t total_kept, int64_t *keep, int64_t *positions_out,
