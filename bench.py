@@ -172,12 +172,15 @@ def bench_gate(dev, iters=50):
     kv = [torch.randn(S, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
     scores = torch.empty(S, dtype=torch.float32, device=dev)
     n_art = e - s
-    ms_score = time_graph(lambda: gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e]))
+    w1k = gate.ktile_w1(w1)   # the head's k-step-major W1 (gate.ScoringHead streams this copy)
+    ms_score = time_graph(lambda: gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e], w1_ktiled=w1k))
+    ms_score_rm = time_graph(lambda: gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e]))
     score_bytes = n_art * d * 2 + w1.numel() * 2 + n_art * 4
     score_flop = 2.0 * n_art * d * 256
     res = {"score": {"ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
                      "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1), "rows": n_art}}
+                     "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1), "rows": n_art,
+                     "ms_w1_row_major": round(ms_score_rm, 4)}}
     for K in (100, 500, 2000):
         p = gate.plan([0], [S], [s], [e], [K], dev)
         T = p.total_kept
@@ -204,7 +207,7 @@ def bench_gate(dev, iters=50):
         ms_sp = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
         sp = (pack_bytes + topk_bytes) / (ms_sp * 1e-3) / 1e9
         # the whole chain from the hidden states: scoring head, selection, pack (one graph)
-        ms_chain = time_graph(lambda: (gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e]),
+        ms_chain = time_graph(lambda: (gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e], w1_ktiled=w1k),
                                        gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias,
                                                         keep_out=keep)))
         chain = (score_bytes + pack_bytes + topk_bytes) / (ms_chain * 1e-3) / 1e9
@@ -246,7 +249,9 @@ def bench_gate_ragged8(dev):
     w2 = (torch.rand(256, generator=g, device=dev) * 2 - 1) * math.sqrt(6.0 / 257)
     b1 = torch.zeros(256, device=dev)
     sc_out = torch.empty(R, dtype=torch.float32, device=dev)
-    ms_score = time_graph(lambda: gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out))
+    w1k = gate.ktile_w1(w1)
+    ms_score = time_graph(lambda: gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out, w1_ktiled=w1k))
+    ms_score_rm = time_graph(lambda: gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out))
     score_bytes = R * 2048 * 2 + w1.numel() * 2 + R * 4
     p = gate.plan(row0, lens, starts, ends, Ks, dev)
     T = p.total_kept
@@ -263,13 +268,14 @@ def bench_gate_ragged8(dev):
     ms_sel = time_graph(lambda: gate.select_pack(scores, p, [], positions=pos, bias_out=bias, keep_out=keep))
     ms_new = time_graph(lambda: gate.select_pack(scores, p, pairs, positions=pos, bias_out=bias, keep_out=keep))
     # the whole chain from the hidden states: scoring head over every row, selection, pack (one graph)
-    ms_chain = time_graph(lambda: (gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out),
+    ms_chain = time_graph(lambda: (gate.score_mlp(x, w1, b1, w2, 0.0, out=sc_out, w1_ktiled=w1k),
                                    gate.select_pack(sc_out, p, pairs, positions=pos, bias_out=bias, keep_out=keep)))
     n_art = sum(e - s for s, e in zip(starts, ends))
     byts = 2 * T * (2048 * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4) + n_art * 4
     gbs = lambda ms: byts / (ms * 1e-3) / 1e9
     return {"score": {"rows": R, "ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
-                      "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+                      "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                      "ms_w1_row_major": round(ms_score_rm, 4)},
             "kept": T, "lens": lens, "K": Ks, "bytes": byts,
             "topk_single_wg_ms": round(ms_topk, 4), "topk_pack_ms": round(ms_old, 4),
             "topk_pack_frac_hbm": round(gbs(ms_old) / PEAK_HBM_GBS, 4),
@@ -459,8 +465,9 @@ def gate_counter_run(dev, reps=5):
     w2 = (torch.rand(256, generator=g, device=dev) * 2 - 1) * math.sqrt(6.0 / 257)
     b1 = torch.zeros(256, device=dev)
     scores = torch.zeros(S, dtype=torch.float32, device=dev)
+    w1k = gate.ktile_w1(w1)
     for _ in range(reps):
-        gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e])
+        gate.score_mlp(x[s:e], w1, b1, w2, 0.0, out=scores[s:e], w1_ktiled=w1k)
     torch.cuda.synchronize()
     print("gate counters: scoring done", flush=True)
     kv = [torch.randn(S, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
@@ -490,7 +497,7 @@ def gate_counter_run(dev, reps=5):
     kv8 = [torch.randn(R, 8, 128, generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
     sc8_head = torch.empty(R, dtype=torch.float32, device=dev)
     for _ in range(reps):
-        gate.score_mlp(x8, w1, b1, w2, 0.0, out=sc8_head)
+        gate.score_mlp(x8, w1, b1, w2, 0.0, out=sc8_head, w1_ktiled=w1k)
     torch.cuda.synchronize()
     print("gate counters: ragged8 scoring done", flush=True)
     p8 = gate.plan([sum(lens[:b]) for b in range(8)], lens, [64] * 8, [L - 256 for L in lens], Ks, dev)

@@ -176,6 +176,16 @@ int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_stride, int32
                       int32_t d_hidden, const void *w1, const float *b1, const float *w2, float b2,
                       float *scores, hipStream_t stream);
 
+/* tg_gate_score_mlp with W1 stored k-step major: w1_ktiled (d_in / 32, d_hidden, 32) bf16,
+ * element (s, u, j) = W1[u, 32 s + j] (torch: w1.view(256, 64, 32).transpose(0, 1).contiguous()),
+ * so that each 32-input step of the weight stream is 16 KiB contiguous instead of 256 rows of
+ * 64 bytes 4 KiB apart.  The same results bit for bit; the scoring head's own (synthetic) weight
+ * layout, kept by gate.ScoringHead next to the row-major W1.  Stands in for the same gate-layer
+ * scoring (gate_forward.py:491-524, e2e_gate_module.py:348-385). */
+int tg_gate_score_mlp_ktiled(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in,
+                             int32_t d_hidden, const void *w1_ktiled, const float *b1, const float *w2,
+                             float b2, float *scores, hipStream_t stream);
+
 /* Order-preserving top-K keep lists, one per sequence (gate_forward.py:1396-1421, _keep_indices
  * :77-81, torch.topk via _select_topk_or_random :84-99).
  * geom: device int32 (num_seqs, 6) rows [row_start, seq_len, art_start, art_end, k_clamped,

@@ -358,6 +358,31 @@ def test_scoring_wide_workgroups(cuda):
     assert_close("wide scores", to_np(scores.index_select(0, idx)), ref, max_abs=2e-3, rel_l2=1e-4)
 
 
+@pytest.mark.parametrize("n", [32448, 256 * 2 * 304 + 77, 1000, 129])
+def test_scoring_ktiled_w1_bit_identical(cuda, n):
+    """The k-step-major W1 (gate.ktile_w1, tg_gate_score_mlp_ktiled) changes only where the
+    kernel's weight stream reads from: scores bit-identical to the row-major W1 in both workgroup
+    forms (32k and 256 x 2 x 304 + 77 rows take the 128- and 256-row forms), ragged tails included,
+    and ScoringHead.scores (which streams the tiled copy) equal to both."""
+    from tokengate_amd import gate
+    g = torch.Generator(device=cuda).manual_seed(17)
+    x = torch.randn(n, 2048, generator=g, device=cuda).to(torch.bfloat16)
+    w1 = _xavier((256, 2048), g, cuda).to(torch.bfloat16)
+    w2 = _xavier((1, 256), g, cuda)[0].contiguous()
+    b1 = torch.randn(256, generator=g, device=cuda) * 0.1
+    w1k = gate.ktile_w1(w1)
+    assert torch.equal(w1k[5, 17], w1[17, 160:192])
+    rm = gate.score_mlp(x, w1, b1, w2, 0.25)
+    kt = gate.score_mlp(x, w1, b1, w2, 0.25, w1_ktiled=w1k)
+    head = gate.ScoringHead(w1, b1, w2, 0.25, torch.zeros(1, 16, device=cuda))
+    hd = head.scores(x)
+    torch.cuda.synchronize()
+    assert torch.equal(rm, kt) and torch.equal(rm, hd)
+    rows = torch.arange(0, n, 101, device=cuda)
+    ref = og.score_mlp(to_np(x.index_select(0, rows)), to_np(w1), to_np(b1), to_np(w2), 0.25)
+    assert_close("ktiled scores", to_np(kt.index_select(0, rows)), ref, max_abs=2e-3, rel_l2=1e-4)
+
+
 def test_ragged8_select_pack(cuda):
     """The ragged pruned-prefill batch at full size: 8 prompts of 16k-128k tokens (prefix 64,
     suffix 256), K from {100, 500, 2000, 4000}, bf16-valued scores (ties at every threshold), the

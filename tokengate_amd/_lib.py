@@ -41,6 +41,7 @@ SIGNATURES = {
     "tg_keybias_bwd": [vp] * 12 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_keybias_varlen_bwd": [vp] * 13 + [i32] * 6 + [vp, f32, i32, vp],
     "tg_gate_score_mlp": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
+    "tg_gate_score_mlp_ktiled": [vp, i64, i64, i32, i32, vp, vp, vp, f32, vp, vp],
     "tg_gate_topk_keep": [vp, vp, i32, i32, vp, vp, vp],
     "tg_gate_pack": [vp, i32, vp, vp, i32, i64, vp, vp, vp, f32, vp, vp],
     "tg_gate_select_pack": [vp, vp, vp, i32, i32, i32, vp, i32, i64, vp, vp, vp, f32, vp, i32, i32, vp],

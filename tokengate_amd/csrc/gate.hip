@@ -69,7 +69,9 @@ struct ScoreArgs {
   const bf16_t *x;
   int64_t x_rs;        // row stride (elements)
   int64_t n_rows;
-  const bf16_t *w1;    // (256, 2048) row-major
+  const bf16_t *w1;    // element (u, k) at w1[u * w_rs + (k / 32) * w_ss / 2 + k % 32]:
+  int64_t w_rs;        //   row-major (256, 2048): w_rs = 2048, w_ss = 64 bytes;
+  int64_t w_ss;        //   k-step major (64, 256, 32): w_rs = 32, w_ss = 16384 bytes (a step's 16 KiB contiguous)
   const float *b1, *w2;
   float b2;
   float *out;
@@ -126,15 +128,15 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
   for (int it = 0; it < 2; ++it) {
     const int slot = (wave * 2 + it) * 64 + lane;        // 0..1023
     const int r = slot >> 2, p = slot & 3;
-    woff[it] = (uint32_t)((r * kDin + 8 * (p ^ ((r >> 2) & 3))) * 2);
+    woff[it] = (uint32_t)((r * a.w_rs + 8 * (p ^ ((r >> 2) & 3))) * 2);
   }
   auto issue = [&](int kstep, auto buf_c) {
-    const uint32_t k0b = (uint32_t)(kstep * kSK * 2);
+    const uint32_t k0b = (uint32_t)(kstep * kSK * 2), k0w = (uint32_t)(kstep * a.w_ss);
     char *xd = xsl(buf_c), *wd = wsl(buf_c);
 #pragma unroll
     for (int it = 0; it < XI; ++it) dma16(xrs, xd + (wave * XI + it) * 1024, xoff[it] + k0b);
 #pragma unroll
-    for (int it = 0; it < 2; ++it) dma16(wrs, wd + (wave * 2 + it) * 1024, woff[it] + k0b);
+    for (int it = 0; it < 2; ++it) dma16(wrs, wd + (wave * 2 + it) * 1024, woff[it] + k0w);
   };
 
   // fragments of one k step: [substep s][block]: X^T columns (B operand, token (ROWS/2)rg + 32t +
@@ -974,10 +976,11 @@ __global__ __launch_bounds__(kThThreads) void gate_threshold_kernel(ThArgs a) {
 
 using namespace tg;
 
-extern "C" int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in,
-                                 int32_t d_hidden, const void *w1, const float *b1, const float *w2, float b2,
-                                 float *scores, hipStream_t stream) {
-  clear_error();
+namespace tg {
+namespace {
+int score_launch(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in, int32_t d_hidden, const void *w1,
+                 int64_t w_rs, int64_t w_ss, const float *b1, const float *w2, float b2, float *scores,
+                 hipStream_t stream) {
   TG_CHECK(d_in == kDin && d_hidden == kDh, "the scoring head is Linear(2048->256) -> SiLU -> Linear(256->1) "
                                             "(got %d -> %d)", d_in, d_hidden);
   TG_CHECK(x && w1 && b1 && w2 && scores, "null pointer");
@@ -988,8 +991,8 @@ extern "C" int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_st
   if (n_rows == 0) return 0;
   TG_CHECK((int64_t)(kSRowsMax + 1) * x_row_stride * 2 < (1ll << 32) - 1024,
            "a 256-row block of x must span less than 4 GiB");
-  ScoreArgs a{static_cast<const bf16_t *>(x), x_row_stride, n_rows, static_cast<const bf16_t *>(w1), b1, w2, b2,
-              scores};
+  ScoreArgs a{static_cast<const bf16_t *>(x), x_row_stride, n_rows, static_cast<const bf16_t *>(w1), w_rs, w_ss,
+              b1, w2, b2, scores};
   // 256-row workgroups (each W1 byte streamed through LDS serves twice the rows) once they still
   // give every CU two of them; 128-row ones below that, where a grid of the larger ones would
   // leave CUs idle
@@ -1003,6 +1006,23 @@ extern "C" int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_st
     hipLaunchKernelGGL((gate_score_kernel<128, 6>), dim3((unsigned)nb), dim3(kSThreads), 0, stream, a);
   TG_HIP_CHECK(hipPeekAtLastError());
   return 0;
+}
+}  // namespace
+}  // namespace tg
+
+extern "C" int tg_gate_score_mlp(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in,
+                                 int32_t d_hidden, const void *w1, const float *b1, const float *w2, float b2,
+                                 float *scores, hipStream_t stream) {
+  clear_error();
+  return score_launch(x, n_rows, x_row_stride, d_in, d_hidden, w1, kDin, kSK * 2, b1, w2, b2, scores, stream);
+}
+
+extern "C" int tg_gate_score_mlp_ktiled(const void *x, int64_t n_rows, int64_t x_row_stride, int32_t d_in,
+                                        int32_t d_hidden, const void *w1_ktiled, const float *b1, const float *w2,
+                                        float b2, float *scores, hipStream_t stream) {
+  clear_error();
+  return score_launch(x, n_rows, x_row_stride, d_in, d_hidden, w1_ktiled, kSK, (int64_t)kDh * kSK * 2, b1, w2, b2,
+                      scores, stream);
 }
 
 extern "C" int tg_gate_topk_keep(const float *scores, const int32_t *geom, int32_t num_seqs,

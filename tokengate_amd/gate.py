@@ -14,7 +14,7 @@ one launch per step for the whole batch.  The threshold selection mode (_select_
 then the same top-K selection over a derived score (threshold_plan).
 """
 import ctypes
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import ClassVar, List, Optional, Sequence, Tuple
 
 import numpy as np
@@ -352,18 +352,30 @@ def pack(keep: torch.Tensor, p: KeepPlan, pairs: Sequence[tuple],
               bias_out.data_ptr() if bias_out is not None else None, _stream(keep))
 
 
+def ktile_w1(w1: torch.Tensor) -> torch.Tensor:
+    """W1 (256, 2048) stored k-step major, (64, 256, 32): each 32-input step of the scoring kernel's
+    weight stream is then 16 KiB contiguous (tg_gate_score_mlp_ktiled)."""
+    d_h, d_in = w1.shape
+    return w1.reshape(d_h, d_in // 32, 32).transpose(0, 1).contiguous()
+
+
 def score_mlp(x: torch.Tensor, w1: torch.Tensor, b1: torch.Tensor, w2: torch.Tensor, b2: float,
-              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+              out: Optional[torch.Tensor] = None, w1_ktiled: Optional[torch.Tensor] = None) -> torch.Tensor:
     """scores[r] = w2 . silu(W1 x_r + b1) + b2 for every row of x (rows, 2048) bf16;
-    W1 (256, 2048) bf16; b1, w2 (256,) float32."""
+    W1 (256, 2048) bf16; b1, w2 (256,) float32.  With w1_ktiled = ktile_w1(W1) the kernel streams
+    that copy instead (the same results, bit for bit)."""
     if x.dtype != torch.bfloat16 or w1.dtype != torch.bfloat16 or x.dim() != 2 or x.stride(1) != 1:
         raise RuntimeError("score_mlp: x (rows, 2048) and W1 (256, 2048) must be bf16 with contiguous rows")
     if not w1.is_contiguous() or b1.dtype != torch.float32 or w2.dtype != torch.float32:
         raise RuntimeError("score_mlp: W1 contiguous bf16, b1 / w2 float32")
+    if w1_ktiled is not None and (w1_ktiled.dtype != torch.bfloat16 or not w1_ktiled.is_contiguous() or
+                                  w1_ktiled.shape != (w1.shape[1] // 32, w1.shape[0], 32)):
+        raise RuntimeError("score_mlp: w1_ktiled must be ktile_w1(W1)")
     n = x.shape[0]
     out = out if out is not None else torch.empty(n, dtype=torch.float32, device=x.device)
     if n:
-        _lib.call("tg_gate_score_mlp", x.data_ptr(), n, x.stride(0), x.shape[1], w1.shape[0], w1.data_ptr(),
+        fn, w = ("tg_gate_score_mlp", w1) if w1_ktiled is None else ("tg_gate_score_mlp_ktiled", w1_ktiled)
+        _lib.call(fn, x.data_ptr(), n, x.stride(0), x.shape[1], w1.shape[0], w.data_ptr(),
                   b1.contiguous().data_ptr(), w2.contiguous().data_ptr(), float(b2), out.data_ptr(), _stream(x))
     return out
 
@@ -491,9 +503,13 @@ class ScoringHead(_BiasScales):
     # _phase2_q_bias, qwen3_flex_attention.py:433-473).  Needs attn_scale.
     scaled_softmax: bool = False
     split_gate_layer: ClassVar[bool] = False      # scores the gate layer's full output
+    _w1k: Optional[tuple] = field(default=None, init=False, repr=False, compare=False)
 
     def scores(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        return score_mlp(x, self.w1, self.b1, self.w2, self.b2, out=out)
+        # the k-step-major copy of W1 the kernel streams, made once (and again if w1 is replaced)
+        if self._w1k is None or self._w1k[0] is not self.w1:
+            self._w1k = (self.w1, ktile_w1(self.w1))
+        return score_mlp(x, self.w1, self.b1, self.w2, self.b2, out=out, w1_ktiled=self._w1k[1])
 
 
 @dataclass
