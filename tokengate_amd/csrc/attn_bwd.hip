@@ -128,6 +128,34 @@ __device__ __forceinline__ uint32_t dq_kswz(int row) {
   return (uint32_t)(((row >> 2) & 1) | ((row & 3) << 1) | ((((row >> 2) ^ (row >> 3)) & 1) << 3));
 }
 
+// LDS DMA issued from inline assembly.  The compiler keeps a wave's LDS reads behind its own
+// in-flight LDS DMA whenever it cannot tell the two apart, and with a ring slot chosen at run time
+// (ks[buf]) it cannot: every read of tile t would wait for the DMA of tile t+1.  Issued this way
+// the DMA is invisible to that bookkeeping; completion is waited for explicitly (wait_all_mem at
+// the top of the next tile), and the reads of a tile never touch the slot being filled.
+struct RawRsrc {
+  uint32_t w[4];
+};
+__device__ __forceinline__ RawRsrc raw_rsrc(const void *base, uint32_t num_bytes) {
+  const uint64_t addr = reinterpret_cast<uint64_t>(base);
+  return RawRsrc{{(uint32_t)addr, (uint32_t)(addr >> 32), num_bytes, 0x00020000u}};
+}
+__device__ __forceinline__ uint32_t lds_addr32(const void *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p;
+}
+template <int BYTES>
+__device__ __forceinline__ void dma_asm(const RawRsrc &rs, const void *lds_wave_base, uint32_t voff) {
+  const u32x4 r = {(uint32_t)__builtin_amdgcn_readfirstlane(rs.w[0]), (uint32_t)__builtin_amdgcn_readfirstlane(rs.w[1]),
+                   (uint32_t)__builtin_amdgcn_readfirstlane(rs.w[2]), (uint32_t)__builtin_amdgcn_readfirstlane(rs.w[3])};
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr32(lds_wave_base));
+  if constexpr (BYTES == 16)
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(r) : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(r) : "memory", "m0");
+}
+
 template <int HP, bool CAUSAL, bool HAS_BIAS, bool VARLEN>
 __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   constexpr int QW = 32;   // query positions per wave (all of one head)
@@ -159,11 +187,11 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
   const int64_t dob = VARLEN ? row0 * a.do_rs : (int64_t)b * a.do_bs;
   const bf16_t *kbase = a.k + (VARLEN ? row0 * a.k_rs : (int64_t)b * a.k_bs) + (int64_t)kh * a.k_hs;
   const bf16_t *vbase = a.v + (VARLEN ? row0 * a.v_rs : (int64_t)b * a.v_bs) + (int64_t)kh * a.v_hs;
-  const brsrc_t krs = make_rsrc(kbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.k_rs + kD) * 2) : 0u);
-  const brsrc_t vrs = make_rsrc(vbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.v_rs + kD) * 2) : 0u);
+  const RawRsrc krs = raw_rsrc(kbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.k_rs + kD) * 2) : 0u);
+  const RawRsrc vrs = raw_rsrc(vbase, sk > 0 ? (uint32_t)(((int64_t)(sk - 1) * a.v_rs + kD) * 2) : 0u);
   const float *bbase = HAS_BIAS ? a.bias + (int64_t)b * a.bias_bs + (int64_t)h0 * a.bias_hs : nullptr;
-  const brsrc_t brs =
-      make_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
+  const RawRsrc brs =
+      raw_rsrc(bbase, (HAS_BIAS && sk > 0) ? (uint32_t)(((int64_t)(HP - 1) * a.bias_hs + sk) * 4) : 0u);
 
   // this wave's 32 columns: 32 query positions of one head (HP = 2: waves 0-3 the first head of the
   // pair, 4-7 the second), block cb (0, 1) = positions 16 cb .. 16 cb + 15, lane l holding column
@@ -219,11 +247,12 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     const uint32_t vb0 = (uint32_t)((int64_t)tile * kBN * a.v_rs * 2);
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-      dma16(krs, ks[buf] + (wave * 2 + it) * 1024, kb0 + koff[it]);
-      dma16(vrs, vs[buf] + (wave * 2 + it) * 1024, vb0 + voff[it]);
+      dma_asm<16>(krs, ks[buf] + (wave * 2 + it) * 1024, kb0 + koff[it]);
+      dma_asm<16>(vrs, vs[buf] + (wave * 2 + it) * 1024, vb0 + voff[it]);
     }
     if constexpr (HAS_BIAS) {
-      if (wave < HP) dma4(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
+      if (wave < HP)
+        dma_asm<4>(brs, &bs[buf][wave][0], (uint32_t)(((int64_t)wave * a.bias_hs + tile * kBN + lane) * 4));
     }
   };
 

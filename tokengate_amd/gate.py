@@ -208,14 +208,17 @@ def _error_word(ws: torch.Tensor) -> torch.Tensor:
 
 
 def raise_select_error(code: int, device, stream: int) -> None:
-    """If `code` (the error word select_pack reported) is nonzero, clear the word in the workspace of
-    (device, stream), so that the next call starts clean, and raise RuntimeError: the keep lists and
-    packed rows of the calls since it was last cleared are not valid."""
+    """If `code` (the error word select_pack reported) is nonzero, zero the workspace of (device,
+    stream) -- the word, and any counter a failed wait left mid-count -- so that the next call starts
+    clean, and raise RuntimeError: the keep lists and packed rows of the calls since it was last
+    cleared are not valid."""
     if not code:
         return
     ent = _SEL_WS.get((torch.device(device).index, stream))
-    if ent is not None:
-        _error_word(ent[0]).zero_()
+    if ent is not None:   # (an error path: the device is drained around the clear)
+        torch.cuda.synchronize(device)
+        ent[0].zero_()
+        torch.cuda.synchronize(device)
     raise RuntimeError(f"tg_gate_select_pack: error word {code} "
                        f"({_SELECT_ERRORS.get(code, 'unknown')}); the keep lists are not valid")
 
