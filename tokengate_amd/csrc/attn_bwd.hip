@@ -321,6 +321,22 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
       sacc[1][kb] = sacc[0][kb];
       pacc[0][kb] = pacc[1][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    // keys past the end or in the causal future start from -inf (one uniform branch, before the
+    // MFMAs), so that P = exp2(-inf) = +0 below needs no per-element test
+    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
+    if (need_mask) {
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        int lim = sk - 1;
+        if constexpr (CAUSAL) lim = min(lim, qrow[cb] + off);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          const int rel = lim - (n0 + 32 * (kb >> 1) + 8 * G + 4 * (kb & 1));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sacc[cb][kb][i] = rel - i < 0 ? -__builtin_inff() : sacc[cb][kb][i];
+        }
+      }
+    }
 #pragma unroll
     for (int ks4 = 0; ks4 < 4; ++ks4) {
       bf16x8 kf[4], vf[4];
@@ -344,33 +360,26 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
         }
       }
     }
-    // dS = P (dP - D), P = exp2(S scale log2e - lse log2e); keys past the end or in the causal
-    // future get P = 0 (a sign mask from lim - key, no per-element compare results in SGPRs)
-    const bool need_mask = (n0 + kBN > sk) || (CAUSAL && n0 + kBN - 1 > qw0 + off);
+    // dS = P (dP - D), P = exp2(S scale log2e - lse log2e) (+0 for the masked keys); the
+    // scheduling fences keep the three phases apart (hoisting across them raises the register
+    // pressure past the file)
+    __builtin_amdgcn_sched_barrier(0);
     uint32_t dsk[2][4][2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-      int lim = sk - 1;
-      if constexpr (CAUSAL) lim = min(lim, qrow[cb] + off);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const int rel = lim - (n0 + 32 * (kb >> 1) + 8 * G + 4 * (kb & 1));
         float ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float p = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, -lse2[cb]));
-          if (need_mask) {
-            int sgn;
-            asm("v_ashrrev_i32 %0, 31, %1" : "=v"(sgn) : "v"(rel - i));   // -1 where key > lim
-            const uint32_t pbits = __builtin_bit_cast(uint32_t, p) & ~(uint32_t)sgn;
-            p = __builtin_bit_cast(float, pbits);
-          }
+          const float p = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, -lse2[cb]));
           ds[i] = p * (pacc[cb][kb][i] - dsum[cb]);
         }
         dsk[cb][kb][0] = pack_bf16x2(ds[0], ds[1]);
         dsk[cb][kb][1] = pack_bf16x2(ds[2], ds[3]);
       }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // dQ^T += K^T dS^T: 2 key steps x 8 d-blocks x 2 column blocks
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
