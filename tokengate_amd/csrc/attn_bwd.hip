@@ -232,6 +232,7 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
     }
   }
 
+  const f32x4 nd4[2] = {f32x4{-dsum[0], -dsum[0], -dsum[0], -dsum[0]}, f32x4{-dsum[1], -dsum[1], -dsum[1], -dsum[1]}};
   int kv_end = sk;
   if constexpr (CAUSAL) kv_end = min(sk, q0 + BM + off);
   const int n_tiles = kv_end > 0 ? (kv_end + kBN - 1) / kBN : 0;
@@ -319,7 +320,8 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
       else
         sacc[0][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
       sacc[1][kb] = sacc[0][kb];
-      pacc[0][kb] = pacc[1][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      pacc[0][kb] = nd4[0];   // dP^T - D accumulated from -D (D is per column)
+      pacc[1][kb] = nd4[1];
     }
     // keys past the end or in the causal future start from -inf (one uniform branch, before the
     // MFMAs), so that P = exp2(-inf) = +0 below needs no per-element test
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(kQThreads, 1) void bwd_dq_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float p = fast_exp2(fmaf(sacc[cb][kb][i], a.scale_log2, -lse2[cb]));
-          ds[i] = p * (pacc[cb][kb][i] - dsum[cb]);
+          ds[i] = p * pacc[cb][kb][i];
         }
         dsk[cb][kb][0] = pack_bf16x2(ds[0], ds[1]);
         dsk[cb][kb][1] = pack_bf16x2(ds[2], ds[3]);
