@@ -538,12 +538,16 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       constexpr int BUF = decltype(buf_c)::value;
       const int m00 = m_start + t * kQSlot;
       wait_vm<0>();
-      // the slot's LSE rows (DMA'd by wave 0, now complete) to log2 units, once for every wave;
-      // the barrier below orders this write before the other waves' reads
-      static_assert(kQSub * kQT == 64, "wave 0 DMAs every LSE row of a slot");
+      // the slot's LSE rows (DMA'd by wave 0, now complete) to log2 units and its D rows (wave 1)
+      // negated, once for every wave; the barrier below orders these writes before the other
+      // waves' reads
+      static_assert(kQSub * kQT == 64, "waves 0 and 1 DMA every LSE / D row of a slot");
       if (wave == 0) {
         float *lw = lslot(buf_c) + lane;
         *lw = *lw * kLog2e;
+      } else if (wave == 1) {
+        float *dw = dslot(buf_c) + lane;
+        *dw = -*dw;
       }
       ring_barrier();
       if (t + 1 < n_qt) issue_tile(m00 + kQSlot, std::integral_constant<int, 1 - BUF>());
@@ -557,11 +561,10 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       const float *const dsl = dslot(buf_c) + sub * kQT;
 
       // S = Q K^T and dP = dO V^T for queries m0 + pi_rb(row), this lane's key
-      f32x4 sacc[2] = {bk4, bk4}, pacc[2];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) pacc[rb][v] = 0.f;
+      // dP accumulates from -D (the slot's D rows are stored negated), so dS = P * dP needs no
+      // subtraction
+      f32x4 sacc[2] = {bk4, bk4};
+      f32x4 pacc[2] = {*reinterpret_cast<const f32x4 *>(dsl + 8 * g), *reinterpret_cast<const f32x4 *>(dsl + 8 * g + 4)};
 #pragma unroll
       for (int k2 = 0; k2 < 4; k2 += 2) {
         bf16x8 qa[2][2], da[2][2];
@@ -611,11 +614,10 @@ __global__ __launch_bounds__(kK16Threads, 1) void bwd_dkdv16_kernel(BwdArgs a) {
       }
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        const f32x4 d4 = *reinterpret_cast<const f32x4 *>(dsl + 8 * g + 4 * rb);
         float ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          ds[i] = p[rb][i] * (pacc[rb][i] - d4[i]);
+          ds[i] = p[rb][i] * pacc[rb][i];
           dbacc += ds[i];
         }
         pk[2 * rb] = pack_bf16x2(p[rb][0], p[rb][1]);
