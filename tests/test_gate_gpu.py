@@ -470,6 +470,42 @@ def test_select_pack_one_and_three_launch_forms(cuda, over):
     assert p.sel_kpt == 8 and p.sel_starts[-1] == target
 
 
+def test_one_launch_selection_many_geometries(cuda):
+    """60 random batches through the one-launch selection (chunk counts up to the CU count,
+    sequences of 1-16 chunks, K from 0 to beyond the span including span - 1 and the span itself,
+    normal, bf16-valued and few-valued scores): every keep list bit-exact through select_keep and
+    select_pack, positions and gathered rows, the error word clear.  A chunk that saw its sequence's
+    phase flag before the data the flag publishes had reached memory (a release whose L2
+    write-back was not waited for) compacted at a stale offset about once in a hundred such batches,
+    silently."""
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    for case in range(60):
+        rng = np.random.default_rng(7000 + case)
+        target = int(rng.choice([8, 40, cus // 2, cus - 1, cus]))
+        seqs, r0, n_chunks = [], 0, 0
+        while n_chunks < target:
+            g = int(min(rng.integers(1, 17), target - n_chunks))
+            n_art = int(rng.integers((g - 1) * 4096 + 1, g * 4096 + 1))
+            pre, suf = int(rng.integers(0, 70)), int(rng.integers(0, 300))
+            L = pre + n_art + suf
+            K = int(rng.choice([0, 1, 7, 100, 500, 2000, n_art - 1, n_art, n_art + 5, int(rng.integers(1, n_art + 1))]))
+            seqs.append((r0, L, pre, pre + n_art, K))
+            r0 += L
+            n_chunks += g
+            if rng.random() < 0.1:
+                seqs.append((r0, 40, 20, 20, 100))
+                r0 += 40
+        kind = int(rng.integers(3))
+        scores = rng.standard_normal(r0).astype(np.float32)
+        if kind == 1:
+            scores = og.bf16(scores)
+        elif kind == 2:
+            scores = np.round(scores * 3).astype(np.float32)
+        print(f"[one-launch geometries] case {case}: chunks={n_chunks} seqs={len(seqs)} rows={r0} kind={kind}",
+              flush=True)
+        _check_select(scores, seqs, cuda)
+
+
 def test_pack_skips_positions_outside_their_sequence(cuda):
     """A kept position outside [0, seq_len) of its sequence (what an unwritten keep entry holds)
     gathers nothing: that destination row and its position / bias entries keep their contents, the

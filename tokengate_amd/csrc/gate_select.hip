@@ -210,15 +210,37 @@ __device__ __forceinline__ void stores_done_barrier() {
   __syncthreads();
 }
 
+// Agent-scope release and acquire whose cache operations have completed when they return.  The
+// release writes this XCD's L2 back (buffer_wbl2) and the acquire invalidates it (buffer_inv);
+// both are vector-memory operations, but the compiler does not count them as outstanding, so
+// after an earlier s_waitcnt it emits no wait for them: a flag or counter stored right after the
+// write-back could reach the other XCDs ahead of the data it publishes, and the workgroup's other
+// waves, released by the barrier after the invalidate, could read lines it had not yet dropped.
+// The explicit waits (inline assembly, which the compiler's wait insertion leaves in place) close
+// both windows.  The chunks waiting on a sequence's phase flag take no acquire at all: the few
+// words the flag publishes to them are read with agent-coherent loads (ld_agent), which read
+// through this XCD's L2, so no invalidate (whose completion takes microseconds) is needed there.
+__device__ __forceinline__ void release_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ void acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+__device__ __forceinline__ uint32_t ld_agent(const uint32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Publish this workgroup's global writes and count its arrival; true in every thread of the
 // workgroup that arrived last (which then sees every other arrival's writes).
 __device__ bool arrive_last(uint32_t *ctr, int G, int *s_flag) {
   stores_done_barrier();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    release_agent();
     const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = old == (uint32_t)(G - 1);
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (last) acquire_agent();
     *s_flag = last ? 1 : 0;
   }
   __syncthreads();
@@ -368,7 +390,7 @@ __device__ __forceinline__ void pass1_last(const SelArgs &a, const Chunk<KPT> &c
 template <int KPT>
 __device__ __forceinline__ void pass2_chunk(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh) {
   const int tid = threadIdx.x;
-  const uint32_t B1 = c.sq_rec[SQ_B1];
+  const uint32_t B1 = ld_agent(c.sq_rec + SQ_B1);   // published with the phase flag
   for (int i = tid; i < kQBins2; i += kQThreads) sh.hist[i] = 0u;
   __syncthreads();
   uint32_t inplay = 0u;
@@ -476,9 +498,10 @@ __device__ __forceinline__ void pass2_last(const SelArgs &a, const Chunk<KPT> &c
 template <int KPT>
 __device__ __forceinline__ void compact_chunk(const SelArgs &a, const Chunk<KPT> &c, SelShared &sh, bool known_off) {
   const int tid = threadIdx.x;
-  const uint32_t T = c.sq_rec[SQ_T];
-  const float rn = __builtin_bit_cast(float, c.sq_rec[SQ_RNORM]);
-  const int quota = (int)a.chunk[(int64_t)c.gc * kQChunkWords + CK_QUOTA];
+  // published with the phase flag (or by the previous launch)
+  const uint32_t T = ld_agent(c.sq_rec + SQ_T);
+  const float rn = __builtin_bit_cast(float, ld_agent(c.sq_rec + SQ_RNORM));
+  const int quota = (int)ld_agent(a.chunk + (int64_t)c.gc * kQChunkWords + CK_QUOTA);
   uint32_t gtm = 0u, tiem = 0u;
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
@@ -493,7 +516,7 @@ __device__ __forceinline__ void compact_chunk(const SelArgs &a, const Chunk<KPT>
   const int tie_before = before & 0xffff, gt_before = before >> 16;
   int off;
   if (known_off) {
-    off = (int)a.chunk[(int64_t)c.gc * kQChunkWords + CK_OFF];
+    off = (int)ld_agent(a.chunk + (int64_t)c.gc * kQChunkWords + CK_OFF);
   } else {
     if (tid == 0)
       __hip_atomic_store(a.chunk + (int64_t)c.gc * kQChunkWords + CK_AGG,
@@ -574,8 +597,9 @@ __device__ __forceinline__ void write_meta_rows(const SelArgs &a, int64_t mw) {
 __device__ __forceinline__ void exit_reset(const SelArgs &a, SelShared &sh) {
   __syncthreads();
   if (threadIdx.x == 0) {
-    const uint32_t prev =
-        __hip_atomic_fetch_add(a.glob + GL_EXIT, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    release_agent();
+    const uint32_t prev = __hip_atomic_fetch_add(a.glob + GL_EXIT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev == gridDim.x - 1) acquire_agent();
     sh.flag = prev == gridDim.x - 1 ? 1 : 0;
   }
   __syncthreads();
@@ -667,7 +691,8 @@ __device__ __forceinline__ uint32_t wait_flag(const SelArgs &a, const uint32_t *
       }
       __builtin_amdgcn_s_sleep(1);
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // no acquire: what the flag publishes is read with ld_agent
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     *s_val = (int)v;
   }
   __syncthreads();
@@ -679,7 +704,7 @@ __device__ __forceinline__ uint32_t wait_flag(const SelArgs &a, const uint32_t *
 __device__ __forceinline__ void raise_flag(uint32_t *flag, uint32_t value) {
   stores_done_barrier();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    release_agent();
     __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
