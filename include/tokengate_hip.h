@@ -238,7 +238,7 @@ int tg_gate_pack(const tg_pack_stream *streams, int32_t n_streams, const int64_t
  * gate_forward.py:1396-1522, for a whole ragged batch); two stream-ordered launches (the
  * selection, then the gather) when n_select_wgs is at most the device's CU count, 512 and
  * chunk_capacity, four above (three selection launches).  Sequence
- * b's state span is cut into chunks of 512 * keys_per_thread scores (keys_per_thread 8, 16 or 32)
+ * b's state span is cut into chunks of 512 * keys_per_thread scores (keys_per_thread 4, 8, 16 or 32)
  * selected by one workgroup each: wg_start (num_seqs + 1, int32, device) lists them, sequence b
  * owning chunks [wg_start[b], wg_start[b + 1]) (none when its span is empty, at most 64),
  * n_select_wgs = wg_start[num_seqs].  Outputs: keep (total_kept, int64, the same lists as

@@ -117,6 +117,28 @@ def test_argmax_rows_rejects_bad_arguments_without_touching_the_gpu():
         assert rc != 0 and msg in lib.tg_last_error(), (args, lib.tg_last_error())
 
 
+def test_select_pack_layout_and_keys_per_thread():
+    """gate.plan's chunking for tg_gate_select_pack: 4 keys per thread (chunks of 2048 scores) for
+    small batches (every span at most 32768 scores, at most 64 chunks in all), else the smallest of
+    8 / 16 / 32 that keeps every span within 64 chunks; the C ABI rejects other values before any
+    launch."""
+    from tokengate_amd import _lib, gate
+    lay = gate._select_layout
+    assert lay([32448]) == (4, [0, 16])
+    assert lay([32768] * 4) == (4, [0, 16, 32, 48, 64])
+    assert lay([0, 100, 0]) == (4, [0, 0, 1, 1])
+    assert lay([32769]) == (8, [0, 9])
+    assert lay([32768] * 5) == (8, [0, 8, 16, 24, 32, 40])
+    assert lay([64 * 4096]) == (8, [0, 64])
+    assert lay([64 * 4096 + 1]) == (16, [0, 33])
+    assert lay([64 * 16384, 5]) == (32, [0, 64, 65])
+    assert lay([64 * 16384 + 1]) == (0, None)
+    lib = _lib.load()
+    for kpt in (2, 6, 64):
+        rc = lib.tg_gate_select_pack(16, 16, 16, 1, 1, kpt, None, 0, 1, 16, None, None, 1e-6, 256, 1, 1, None)
+        assert rc != 0 and b"keys_per_thread" in lib.tg_last_error()
+
+
 def test_fwd_workspace_size_queries():
     """The split workspace is planned only for grids that leave the chip idle, and never for
     invalid sizes; the size queries make no GPU call."""

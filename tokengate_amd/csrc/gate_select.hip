@@ -1052,8 +1052,8 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
   TG_CHECK(num_seqs >= 0 && n_select_wgs >= 0 && total_kept >= 0, "negative size");
   TG_CHECK(n_streams >= 0 && n_streams <= kQMaxStreams, "at most %d streams", kQMaxStreams);
   TG_CHECK(n_streams == 0 || streams != nullptr, "null streams");
-  TG_CHECK(keys_per_thread == 8 || keys_per_thread == 16 || keys_per_thread == 32,
-           "keys_per_thread must be 8, 16 or 32");
+  TG_CHECK(keys_per_thread == 4 || keys_per_thread == 8 || keys_per_thread == 16 || keys_per_thread == 32,
+           "keys_per_thread must be 4, 8, 16 or 32");
   if (num_seqs == 0 || total_kept == 0) return 0;
   TG_CHECK(num_seqs <= seq_capacity && n_select_wgs <= chunk_capacity,
            "workspace capacity (%d sequences, %d chunks) below this call's (%d, %d)", seq_capacity, chunk_capacity,
@@ -1092,6 +1092,7 @@ extern "C" int tg_gate_select_pack(const float *scores, const int32_t *geom, con
     hipLaunchKernelGGL(gate_compact_kernel<8>, dim3(grid), dim3(kQThreads), 0, stream, a);
   } else {
     switch (keys_per_thread) {
+      case 4: launch_select<4>(a, grid, fused, stream); break;
       case 8: launch_select<8>(a, grid, fused, stream); break;
       case 16: launch_select<16>(a, grid, fused, stream); break;
       default: launch_select<32>(a, grid, fused, stream); break;
