@@ -513,7 +513,7 @@ def gate_counter_run(dev, reps=5):
 
 def cpu_threads() -> int:
     """Host threads for the CPU legs: the job's CPU share (OMP_NUM_THREADS when the environment
-    sets it, as on a GPU box shared by several jobs), else every core this process may run on
+    sets it, as on a machine shared by several jobs), else every core this process may run on
     (len(os.sched_getaffinity(0))); the report gives both counts."""
     env = os.environ.get("OMP_NUM_THREADS", "")
     n = len(os.sched_getaffinity(0))

@@ -1,5 +1,5 @@
 """Oracle: the reference's own CPU execution of the hot path's two stages, restated in torch on the
-host (TEST INFRASTRUCTURE ONLY: the checker in tests/ and bench.py's timed CPU baseline).
+host (TEST INFRASTRUCTURE ONLY: the parity tests in tests/ and bench.py's timed CPU baseline).
 
   sdpa_chunked — the reference's SDPA compatibility prefill, sdpa_causal
                  (tokengate/e2e_gate/attn/sdpa_compat.py:6-37): K / V heads repeated to the query

@@ -1,6 +1,6 @@
 """Writes gate_chain.npz: input/output vectors of the reference's gate-bias and Phase-2 transform
 chain, produced by the reference's own functions (run in the build container only, where the
-reference checkout exists; the GPU box and the tests read only the .npz).
+reference checkout exists; GPU runs and the tests read only the .npz).
 
 Functions exercised (reference paths relative to its checkout):
   * E2EGate.forward / aggregate            tokengate/e2e_gate/gate_module/e2e_gate_module.py:348-399
