@@ -506,6 +506,33 @@ def test_one_launch_selection_many_geometries(cuda):
         _check_select(scores, seqs, cuda)
 
 
+def test_four_keys_per_thread_both_launch_forms(cuda, monkeypatch):
+    """4 keys per thread (chunks of 2048 scores) through both selection forms.  gate.plan gives 4 keys
+    per thread only to batches of at most 64 chunks, so that limit is lifted here.  Batches of CU
+    count - 1 chunks (one launch) and CU count + 40 chunks (three launches) are run, with spans of up
+    to 16 chunks.  Every keep list must be bit-exact against the oracle, with positions, gathered
+    rows and gate bias checked as well."""
+    from tokengate_amd import gate
+    monkeypatch.setattr(gate, "_SEL_SMALL_CHUNKS", 1 << 20)
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    for case, target in enumerate([cus - 1, cus + 40]):
+        rng = np.random.default_rng(7500 + case)
+        seqs, r0, n_chunks = [], 0, 0
+        while n_chunks < target:
+            g = int(min(rng.integers(1, 17), target - n_chunks))
+            n_art = int(rng.integers((g - 1) * 2048 + 1, g * 2048 + 1))
+            pre, suf = int(rng.integers(0, 70)), int(rng.integers(0, 300))
+            L = pre + n_art + suf
+            K = int(rng.choice([1, 100, 500, 2000, n_art - 1, n_art, int(rng.integers(1, n_art + 1))]))
+            seqs.append((r0, L, pre, pre + n_art, K))
+            r0 += L
+            n_chunks += g
+        scores = og.bf16(rng.standard_normal(r0).astype(np.float32))
+        print(f"[4 keys per thread] case {case}: chunks={n_chunks} cus={cus} seqs={len(seqs)} rows={r0}", flush=True)
+        keep, p = _check_select(scores, seqs, cuda)
+        assert p.sel_kpt == 4 and p.sel_starts[-1] == target
+
+
 def test_pack_skips_positions_outside_their_sequence(cuda):
     """A kept position outside [0, seq_len) of its sequence (what an unwritten keep entry holds)
     gathers nothing: that destination row and its position / bias entries keep their contents, the
