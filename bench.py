@@ -179,7 +179,8 @@ def bench_gate(dev, iters=50):
     score_flop = 2.0 * n_art * d * 256
     res = {"score": {"ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
                      "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
-                     "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1), "rows": n_art,
+                     "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1),
+                     "frac_mfma": round(score_flop / (ms_score * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4), "rows": n_art,
                      "ms_w1_row_major": round(ms_score_rm, 4)}}
     for K in (100, 500, 2000):
         p = gate.plan([0], [S], [s], [e], [K], dev)
@@ -273,8 +274,11 @@ def bench_gate_ragged8(dev):
     n_art = sum(e - s for s, e in zip(starts, ends))
     byts = 2 * T * (2048 * 2 + 4 * 8 * 128 * 2) + T * (8 + 8 + 4 + 4) + n_art * 4
     gbs = lambda ms: byts / (ms * 1e-3) / 1e9
+    score_flop = 2.0 * R * 2048 * 256
     return {"score": {"rows": R, "ms": round(ms_score, 4), "gbs": round(score_bytes / (ms_score * 1e-3) / 1e9, 1),
                       "frac_hbm": round(score_bytes / (ms_score * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                      "tflops": round(score_flop / (ms_score * 1e-3) / 1e12, 1),
+                      "frac_mfma": round(score_flop / (ms_score * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
                       "ms_w1_row_major": round(ms_score_rm, 4)},
             "kept": T, "lens": lens, "K": Ks, "bytes": byts,
             "topk_single_wg_ms": round(ms_topk, 4), "topk_pack_ms": round(ms_old, 4),
