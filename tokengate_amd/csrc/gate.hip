@@ -231,7 +231,7 @@ __global__ __launch_bounds__(kSThreads, 1) void gate_score_kernel(ScoreArgs a) {
       for (int v = 0; v < 16; ++v) {
         const int u = 64 * hq + 32 * j + 8 * (v >> 2) + 4 * g + (v & 3);
         const float h = acc[j][t][v] + a.b1[u];
-        const float sl = h / (1.f + __expf(-h));
+        const float sl = h * __builtin_amdgcn_rcpf(1.f + __expf(-h));   // SiLU, reciprocal to 1 ulp
         part = fmaf(sl, a.w2[u], part);
       }
     const float tot = pair_sum(part);
