@@ -49,9 +49,13 @@ namespace {
 // C^T blocks (hidden unit = MFMA row, token = column): each lane ends with one token's hidden
 // units of each block, the SiLU . w2 reduction is in-lane plus one cross-half exchange, and the four
 // hidden quarters of a row are added through LDS in a fixed order.
-// With 128-row workgroups the W1 stream through the LDS DMA path (about 11-12 TB/s over the whole
-// chip) bounded the kernel: with the matrix work alone a launch took 0.33x, with X alone 0.49x,
-// with W1 alone 0.54x of the full kernel's time at 710k rows.
+// At 256 FLOP per byte of X the head sits at the ridge of the MFMA and HBM roofs.  Probes at 710k
+// rows with 128-row workgroups, each with one piece compiled out, took 0.33x of the full time with
+// only the matrix work, 0.49x with X alone and 0.54x with W1 alone.  A form that loaded W1 from
+// L2 straight into registers, leaving only X in the LDS ring, was slower at every size.  The limit
+// is therefore the per-step chain (barrier, DMA wait, fragment reads), with MFMA busy about half the
+// SIMD cycles.  The SiLU takes the hardware reciprocal: the IEEE division it replaced cost about
+// one VALU instruction per MFMA in the epilogue, which both waves of a SIMD run at the same time.
 // ---------------------------------------------------------------------------------------------
 // f(integral_constant<int, J>) for J = 0, 1, ... in order
 template <typename F, int... J>
