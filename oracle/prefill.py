@@ -116,16 +116,26 @@ def layer(W: Weights, i: int, x: torch.Tensor, pos: torch.Tensor, bias_logit: Op
     return mlp_half(W, i, x), k, v
 
 
-def phase2_tables(head, scores_art: np.ndarray, keep: np.ndarray, art_start: int, art_end: int):
+def phase2_tables(head, scores_art: np.ndarray, keep: np.ndarray, art_start: int, art_end: int,
+                  ratio=None):
     """The reference's Phase-2 constants of one sample (oracle.gate's bf16 chain): per Phase-2
     layer j, the key bias bias'[j] (H, n_kept) in logit units and the query multiplier
-    s[j] (H, n_kept), both bf16 values as float32 tensors; s is None without a temperature."""
+    s[j] (H, n_kept), both bf16 values as float32 tensors; s is None without a temperature.
+
+    ratio: the kept rows' scaled-softmax ratio r as fp32 values, or None for the closed form
+    (ssmax_ratio, float64) rounded to fp32.  The reference evaluates r with fp32 logs on its own
+    device (_ssmax_ratio, gate_forward.py:573-584), so where r lies within an fp32 unit or two of
+    a bf16 rounding point its bf16 value depends on that device's logf.  A parity test therefore
+    checks a pipeline's r against the closed form to fp32 accuracy and passes it here."""
     gs = head.gate_scale.float().cpu().numpy()
     b = og.gate_bias_layers(scores_art, gs, gain=float(getattr(head, "bias_gain", 1.0)))
     gb = og.kept_bias_layers(b, keep, art_start, art_end)                   # (n, L2, H)
     temp = og.softplus32(head.attn_scale.float().cpu().numpy()) if head.attn_scale is not None else None
     ssmax = bool(getattr(head, "scaled_softmax", False)) and temp is not None
-    r = og.ssmax_ratio(keep).astype(np.float32) if ssmax else None
+    if ssmax:
+        r = (og.ssmax_ratio(keep) if ratio is None else np.asarray(ratio, dtype=np.float64)).astype(np.float32)
+    else:
+        r = None
     biases, scales = [], []
     for j in range(gb.shape[1]):
         tj = temp[j] if temp is not None else None

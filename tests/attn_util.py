@@ -114,3 +114,18 @@ def qkv(B, Sq, Sk, H, Hkv, gen, device, scale=1.0, D=128):
     k = (torch.randn(B, Sk, Hkv, D, generator=gen, device=device) * scale).to(torch.bfloat16)
     v = (torch.randn(B, Sk, Hkv, D, generator=gen, device=device) * scale).to(torch.bfloat16)
     return q, k, v
+
+
+def checked_ratio(ratio, keep, rtol=5e-7):
+    """A pipeline's scaled-softmax ratio of one sequence's kept rows (fp32, None without one),
+    checked against the float64 closed form r = min(1, ln max(m, 2) / ln max(p + 1, 2)) to a few
+    fp32 units, and returned as numpy for the oracle's bf16 chain (oracle.prefill.phase2_tables),
+    whose rounding of r to bf16 must follow the pipeline's own fp32 value."""
+    if ratio is None:
+        return None
+    from oracle import gate as og
+    got = ratio.float().cpu().numpy().astype(np.float64)
+    want = og.ssmax_ratio(np.asarray(keep))
+    np.testing.assert_allclose(got, want, rtol=rtol, atol=0)
+    return got.astype(np.float32)
+

@@ -22,7 +22,7 @@ import torch
 
 from oracle import gate as og
 from oracle import prefill as op
-from tests.attn_util import assert_close_grad, to_np
+from tests.attn_util import assert_close_grad, checked_ratio, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +94,10 @@ def test_ragged8_28_layers(cuda):
 
     ins2 = list(cap["phase2"]) + [cap["h2"]]
     tables = [op.phase2_tables(head, scores[cu1[b] + starts[b]:cu1[b] + ends[b]].astype(np.float32), keeps[b],
-                               starts[b], ends[b]) for b in range(len(LENS))]
+                               starts[b], ends[b],
+                               ratio=checked_ratio(r.kept_ratio[cu2[b]:cu2[b + 1]] if r.kept_ratio is not None
+                                                   else None, keeps[b]))
+              for b in range(len(LENS))]
     for i in (2, shape.n_layers - 1):
         j = i - 2
         for b in range(len(LENS)):

@@ -25,7 +25,7 @@ import torch
 
 from oracle import gate as og
 from oracle import prefill as op
-from tests.attn_util import assert_close_grad, to_np
+from tests.attn_util import assert_close_grad, checked_ratio, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -108,7 +108,8 @@ def _check_phase2_and_e2e(r, W, head, shape, ids, lens, starts, ends, Ks, keeps,
     tables = []
     for b in range(len(lens)):
         sc = scores[cu1[b] + starts[b]:cu1[b] + ends[b]]
-        tables.append(op.phase2_tables(head, sc.astype(np.float32), keeps[b], starts[b], ends[b]))
+        rb = checked_ratio(r.kept_ratio[cu2[b]:cu2[b + 1]] if r.kept_ratio is not None else None, keeps[b])
+        tables.append(op.phase2_tables(head, sc.astype(np.float32), keeps[b], starts[b], ends[b], ratio=rb))
     # the Phase-2 constants against the oracle's restatement of the reference's bf16 chain: equal
     # up to the last fp32 bit of the normalisation (the product's sum of squares runs in another
     # order), which can move a bf16 rounding by one unit on rare entries

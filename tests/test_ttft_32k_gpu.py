@@ -22,7 +22,7 @@ import torch
 
 from oracle import gate as og
 from oracle import prefill as op
-from tests.attn_util import assert_close_grad, to_np
+from tests.attn_util import assert_close_grad, checked_ratio, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -83,7 +83,8 @@ def test_ttft_32k_k2000_28_layers(cuda):
         del ref
 
     ins2 = list(cap["phase2"]) + [cap["h2"]]
-    bias_tab, s_tab = op.phase2_tables(head, sc.astype(np.float32), want, START, END)[:2]
+    bias_tab, s_tab = op.phase2_tables(head, sc.astype(np.float32), want, START, END,
+                                       ratio=checked_ratio(r.kept_ratio, want))[:2]
     pos2 = torch.as_tensor(want, device=cuda)[None]
     for i in (2, shape.n_layers - 1):
         j = i - 2
