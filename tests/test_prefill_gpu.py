@@ -48,6 +48,9 @@ def _setup(cuda, seed=0, ssmax=False):
 CASES = {
     "ragged3": ([700, 1290, 333], [16, 64, 0], [600, 1100, 333], [100, 500, 4000]),
     "one": ([517], [64], [417], [1]),
+    # with the branch head, kept row 1070 of sequence 1 (position 1321) has a scaled-softmax ratio
+    # ln 1071 / ln 1322 two fp32 units past a bf16 rounding point
+    "ratio_edge": ([1085, 1489, 55], [57, 59, 7], [1020, 1341, 22], [973, 1025, 25]),
 }
 
 
@@ -156,7 +159,7 @@ def _check_phase2_and_e2e(r, W, head, shape, ids, lens, starts, ends, Ks, keeps,
         assert d <= 2e-2 and dl <= 2e-2
 
 
-@pytest.mark.parametrize("case", ["ragged3", "one"])
+@pytest.mark.parametrize("case", ["ragged3", "one", "ratio_edge"])
 def test_prefill_branch_head_split_matches_oracle(cuda, case):
     """The finalized gate (MLP scoring branch, scaled softmax) with the split gate layer: Phase 1
     ends at the gate layer's attention boundary, the branch scores it, the gate layer's MLP runs
