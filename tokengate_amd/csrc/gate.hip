@@ -837,8 +837,11 @@ __global__ __launch_bounds__(kPThreads) void gate_pack_kernel(PackArgs a) {
   __syncthreads();
   // every 16-byte unit of every stream of the workgroup's rows, flattened; each thread issues the
   // loads of up to kPBatch units before their stores, so that a row's streams are in flight
-  // together instead of one stream's latency after another
-  constexpr int kPBatch = 8;
+  // together instead of one stream's latency after another.  Six per thread measured best: a
+  // hidden row and two layers' K/V (768 units) make 4-row workgroups two full rounds of 1536 (with
+  // 8, a full round and a half-empty one) and keep fewer registers live (ragged8 select + pack 105
+  // -> 101 us, 32k K=2000 24.9 -> 24.5 us; 3, 4 and 12 measured slower)
+  constexpr int kPBatch = 6;
   const int U = upre[a.n_streams];
   const int total = U * kPRows;
   for (int w0 = tid; w0 < total; w0 += kPBatch * kPThreads) {
