@@ -373,3 +373,34 @@ def test_phase2_graph_replay_matches_oracle(cuda):
             assert dl <= 2e-2
         _ = torch.randn(1000, 1000, device=cuda) @ torch.randn(1000, 1000, device=cuda)   # eager work between replays
         torch.cuda.synchronize()
+
+
+def _random_geometry(seed):
+    """A seeded random batch: 1-4 prompts of 1-1500 tokens (some of 1-40), prefix up to 100, a state
+    span that is empty one time in ten, K from 0 to beyond the span; scaled softmax one time in three."""
+    rng = np.random.default_rng(seed)
+    lens, starts, ends, Ks = [], [], [], []
+    for _ in range(int(rng.integers(1, 5))):
+        L = int(rng.integers(1, 1500)) if rng.random() < 0.85 else int(rng.integers(1, 40))
+        s = int(rng.integers(0, min(L, 100) + 1))
+        e = int(rng.integers(s, L + 1)) if rng.random() < 0.9 else s
+        na = e - s
+        K = int(rng.choice([0, 1, 5, 100, max(na, 1), na + 10, int(rng.integers(0, na + 2))]))
+        lens.append(L); starts.append(s); ends.append(e); Ks.append(K)
+    return (lens, starts, ends, Ks), bool(rng.random() < 0.3)
+
+
+@pytest.mark.parametrize("seed", [500, 504, 512, 515, 523, 2001, 2017, 2038])
+def test_prefill_random_geometries(cuda, seed):
+    """Seeded random batches through the whole gated prefill, checked as test_prefill_matches_oracle
+    checks its fixed cases (keep lists, packed rows, gate bias, Phase-2 tables, every layer
+    teacher-forced, logits, end to end).  The seeds include empty state spans, one-token prompts,
+    K = 0 and K beyond the span, and scaled softmax."""
+    geo, ssmax = _random_geometry(seed)
+    print(f"[random prefill] seed {seed}: lens={geo[0]} starts={geo[1]} ends={geo[2]} K={geo[3]} ssmax={ssmax}",
+          flush=True)
+    CASES[f"random{seed}"] = geo
+    try:
+        test_prefill_matches_oracle(cuda, f"random{seed}", ssmax)
+    finally:
+        del CASES[f"random{seed}"]
