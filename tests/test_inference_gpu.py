@@ -80,6 +80,51 @@ def test_decode_matches_oracle(cuda, prune_below_gate, ssmax, branch, headroom, 
     assert (st._graph is not None) == graph
 
 
+@pytest.mark.parametrize("seed", [100, 110, 113, 124, 129])
+def test_decode_random_geometries(cuda, seed):
+    """Seeded random batches (1-4 prompts of up to 900 tokens, state spans down to one token, K
+    from 1 to beyond the span, 1-5 greedy steps) over random combinations of prune-below-gate,
+    scaled softmax, the finalized gate, in-place headroom and graph replay, against the oracle's
+    teacher-forced decode as in test_decode_matches_oracle."""
+    from tokengate_amd import inference as I
+    from tokengate_amd.decode import DecodeState
+    torch.set_num_threads(min(16, torch.get_num_threads()))
+    rng = np.random.default_rng(seed)
+    lens, spans, Ks = [], [], []
+    for _ in range(int(rng.integers(1, 5))):
+        L = int(rng.integers(2, 900))
+        s = int(rng.integers(0, min(L, 60) + 1))
+        e = int(rng.integers(s, L + 1))
+        lens.append(L); spans.append((s, e))
+        Ks.append(int(rng.choice([1, 16, 64, 300, 5000, int(rng.integers(1, L + 1))])))
+    pbg, ssmax, branch, headroom, graph = (bool(rng.random() < p) for p in (0.5, 0.4, 0.3, 0.7, 0.4))
+    steps = int(rng.integers(1, 6))
+    print(f"[random decode] seed {seed}: lens={lens} spans={spans} K={Ks} prune_below_gate={pbg} ssmax={ssmax} "
+          f"branch={branch} headroom={headroom} graph={graph} steps={steps}", flush=True)
+    m = _model(cuda, ssmax=ssmax, branch=branch)
+    split = [I.split_state_span(p) for p in _prompts(lens, spans, 5 + seed)]
+    pf = m.prefill(split, Ks, prune_below_gate=pbg, decode_headroom=steps + 1 if headroom else 0)
+    st = DecodeState(m.weights, m.gate, m.gate_layer, pf, steps + 1, pbg, graph=graph)
+    assert st.in_place == headroom
+    cur = pf.first_tokens
+    toks, logits = [cur], []
+    for _ in range(steps):
+        cur = st.step(cur)
+        toks.append(cur)
+        logits.append(st.last_logits.float().cpu())
+    torch.cuda.synchronize()
+    W = op.Weights(m.weights)
+    kp = pf.kept_positions.cpu().numpy()
+    for b, (clean, s, e) in enumerate(split):
+        keep = kp[pf.cu_kept[b]:pf.cu_kept[b + 1]]
+        gen = [int(t[b]) for t in toks[:steps]]
+        ref = op.decode_logits(W, m.gate, clean, s, e, m.gate_layer, keep, gen, pbg)
+        for i in range(steps):
+            ma, rl = assert_close_grad(f"seq {b} step {i}", to_np(logits[i][b]), to_np(ref[1 + i]), rel_l2=2e-2)
+            print(f"[random decode] seq {b} step {i}: logits max-abs/max(1,|ref|) {ma:.2e} rel-L2 {rl:.2e}", flush=True)
+            assert int(toks[i + 1][b]) == int(logits[i][b].argmax())
+
+
 def test_decode_fused_projections_match_unfused(cuda):
     """The decode step with each RMSNorm folded into the projection after it, the SwiGLU product
     into the down projection and the final norm into the LM head (one launch each) gives the same
